@@ -1,0 +1,274 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X W8A8 SmoothQuant path (one GPU).
+
+Headline (BASELINE.json metric "int8 TOPS (%MFMA peak) fused SQ+GEMM; SmoothQuant
+GB/s (%HBM peak)", config 3): one step = SmoothQuant of the fp16 activations
+followed by the int8 GEMM with fused per-token x per-channel dequant, for the
+four Llama-3-8B projections at M=8192 tokens:
+    qkv (K=4096, N=6144), o_proj (4096, 4096), gate_up (4096, 28672), down (14336, 4096)
+value = total GEMM ops (2*M*N*K summed) / step time, in TOPS; inputs are
+resident in HBM before timing starts.
+
+Also reported: config 1 (standalone quantizer, X fp16 [2048, 4096]) in GB/s
+with buffer sets rotated over >512 MB so the 256 MB MALL cannot serve repeats,
+and config 2 (W8A8 GEMM 4096^3 + dequant) in TOPS.  Per-kernel durations come
+from HIP events recorded on the stream the kernels run on.
+
+    python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--m 8192] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_INT8_OPS = 5.0e15   # MI355X dense int8 MFMA, ops/s
+PEAK_HBM_BPS = 8.0e12    # MI355X HBM3E, bytes/s
+
+LLAMA3_8B = [("qkv", 4096, 6144), ("o_proj", 4096, 4096), ("gate_up", 4096, 28672),
+             ("down", 14336, 4096)]
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def make_projection(torch, gen, dev, m, k, n):
+    x = torch.randn((m, k), generator=gen, device=dev, dtype=torch.float32)
+    ncols = max(1, round(0.005 * k))
+    cols = torch.randperm(k, generator=gen, device=dev)[:ncols]
+    x[:, cols] *= 20.0
+    x = x.to(torch.float16)
+    s = torch.rand(k, generator=gen, device=dev) * 1.5 + 0.5
+    w = torch.randint(-127, 128, (n, k), generator=gen, device=dev, dtype=torch.int8)
+    sb = torch.rand(n, generator=gen, device=dev) * 9e-3 + 1e-3
+    q = torch.empty((m, k), dtype=torch.int8, device=dev)
+    r = torch.empty(m, dtype=torch.float32, device=dev)
+    c = torch.empty((m, n), dtype=torch.float16, device=dev)
+    return dict(x=x, s=s, w=w, sb=sb, q=q, r=r, c=c, m=m, k=k, n=n)
+
+
+def cpu_baseline(projs, rows: int):
+    """Reference CPU path on a row sample of every projection: oracle SmoothQuant
+    (port of rocwmma_smoothquant.cpp:74-121) + the reference's gemm_cpu_h
+    (common.hpp:299-345, compiled from source into oracle/_ref) + dequant."""
+    import numpy as np
+
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib as O
+
+    use_ref = O.ref() is not None
+    ops = 0.0
+    t0 = time.perf_counter()
+    for p in projs:
+        x = p["x"][:rows].cpu().numpy()
+        s = p["s"].cpu().numpy()
+        w = p["w"].cpu().numpy()
+        sb = p["sb"].cpu().numpy()
+        t_start = time.perf_counter()
+        q, r = O.smoothquant(x, s)
+        acc = O.ref_gemm_cpu_i8(q, w) if use_ref else O.gemm_i32(q, w)
+        O.dequant_f16(acc, r, sb)
+        ops += 2.0 * rows * p["n"] * p["k"]
+        log(f"cpu baseline {p['k']}x{p['n']} rows={rows}: {time.perf_counter() - t_start:.2f}s")
+    dt = time.perf_counter() - t0
+    threads = int(O.oracle().w8a8o_num_threads())
+    return {
+        "value": ops / dt / 1e12,
+        "unit": "TOPS",
+        "cores": threads,
+        "kind": "reference" if use_ref else "port",
+        "sample": (f"{rows} of 8192 rows of each Llama-3-8B projection (qkv, o_proj, gate_up, "
+                   f"down): SmoothQuant (oracle port) + gemm_cpu_h "
+                   f"({'reference common.hpp' if use_ref else 'oracle port'}) + dequant; "
+                   f"{ops / 1e9:.1f} GOP in {dt:.1f} s"),
+    }
+
+
+def bench_quantizer(torch, w8a8, dev, gen, iters=40):
+    """Config 1: X fp16 [2048, 4096]; 24 rotating buffer sets (~600 MB)."""
+    m, n = 2048, 4096
+    sets = []
+    for _ in range(24):
+        x = torch.randn((m, n), generator=gen, device=dev).to(torch.float16)
+        s = torch.rand(n, generator=gen, device=dev) * 1.5 + 0.5
+        sets.append((x, s, torch.empty((m, n), dtype=torch.int8, device=dev),
+                     torch.empty(m, dtype=torch.float32, device=dev)))
+    for i in range(8):
+        x, s, q, r = sets[i % len(sets)]
+        w8a8.smoothquant(x, s, out=q, row_scale=r)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(iters)]
+    for i in range(iters):
+        x, s, q, r = sets[i % len(sets)]
+        evs[i][0].record()
+        w8a8.smoothquant(x, s, out=q, row_scale=r)
+        evs[i][1].record()
+    torch.cuda.synchronize()
+    us = sum(a.elapsed_time(b) for a, b in evs) / iters * 1e3
+    nbytes = 2 * m * n + 4 * n + m * n + 4 * m  # rocwmma_smoothquant.cpp:157-158
+    gbps = nbytes / (us * 1e-6) / 1e9
+    return {"workload": "cfg1 X fp16 [2048,4096] -> int8, 24 rotating buffer sets",
+            "us_per_launch": us, "bytes_per_launch": nbytes, "GBps": gbps,
+            "frac_hbm": gbps * 1e9 / PEAK_HBM_BPS}
+
+
+def bench_gemm_4096(torch, w8a8, dev, gen, iters=20):
+    m = n = k = 4096
+    a = torch.randint(-127, 128, (m, k), generator=gen, device=dev, dtype=torch.int8)
+    b = torch.randint(-127, 128, (n, k), generator=gen, device=dev, dtype=torch.int8)
+    sa = torch.rand(m, generator=gen, device=dev) * 9e-3 + 1e-3
+    sb = torch.rand(n, generator=gen, device=dev) * 9e-3 + 1e-3
+    c = torch.empty((m, n), dtype=torch.float16, device=dev)
+    for _ in range(3):
+        w8a8.gemm(a, b, sa, sb, out=c)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        w8a8.gemm(a, b, sa, sb, out=c)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / iters * 1e3
+    tops = 2.0 * m * n * k / (us * 1e-6) / 1e12
+    return {"workload": "cfg2 4096^3 int8 GEMM + fp16 dequant", "us_per_launch": us,
+            "TOPS": tops, "frac_mfma": tops * 1e12 / PEAK_INT8_OPS}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--m", type=int, default=8192, help="tokens per projection")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=32)
+    ap.add_argument("--no-extras", action="store_true", help="skip cfg1/cfg2 side measurements")
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the W8A8 path is a "
+                          "single-GPU kernel path (run with --gpus 1)", "n_gpus": args.gpus}))
+        return 2
+
+    import torch
+
+    import optimized_rocwmma_samples_amd as w8a8
+
+    w8a8.library()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x5EED0003)
+
+    log(f"{w8a8.version()} on {torch.cuda.get_device_name(dev)}")
+    projs = [make_projection(torch, gen, dev, args.m, k, n) for (_, k, n) in LLAMA3_8B]
+    total_ops = sum(2.0 * p["m"] * p["n"] * p["k"] for p in projs)
+
+    def step(events=None):
+        for i, p in enumerate(projs):
+            if events is not None:
+                events[i][0].record()
+            w8a8.smoothquant(p["x"], p["s"], out=p["q"], row_scale=p["r"])
+            if events is not None:
+                events[i][1].record()
+            w8a8.gemm(p["q"], p["w"], p["r"], p["sb"], out=p["c"])
+            if events is not None:
+                events[i][2].record()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log("warmup done")
+
+    # timed region: exactly `steps` steps, synchronized on both sides
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    for _ in range(args.steps):
+        step()
+    t1.record()
+    torch.cuda.synchronize()
+    ms_per_step = t0.elapsed_time(t1) / args.steps
+    value = total_ops / (ms_per_step * 1e-3) / 1e12
+    log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step, {value:.1f} TOPS")
+
+    # per-kernel durations (separate pass with an event around every launch)
+    ev = [[[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in projs]
+          for _ in range(args.steps)]
+    for s in range(args.steps):
+        step(ev[s])
+    torch.cuda.synchronize()
+    q_ms = [0.0] * len(projs)
+    g_ms = [0.0] * len(projs)
+    for s in range(args.steps):
+        for i in range(len(projs)):
+            q_ms[i] += ev[s][i][0].elapsed_time(ev[s][i][1]) / args.steps
+            g_ms[i] += ev[s][i][1].elapsed_time(ev[s][i][2]) / args.steps
+    gemm_ops = [2.0 * p["m"] * p["n"] * p["k"] for p in projs]
+    gemm_avg_us = sum(g_ms) / len(g_ms) * 1e3
+    gemm_tops = sum(gemm_ops) / (sum(g_ms) * 1e-3) / 1e12
+    per_proj = []
+    for (name, k, n), p, qm, gm, ops in zip(LLAMA3_8B, projs, q_ms, g_ms, gemm_ops):
+        qbytes = 3 * p["m"] * k + 4 * k + 4 * p["m"]
+        per_proj.append({"proj": name, "K": k, "N": n, "quant_us": qm * 1e3,
+                         "quant_GBps": qbytes / (qm * 1e-3) / 1e9, "gemm_us": gm * 1e3,
+                         "gemm_TOPS": ops / (gm * 1e-3) / 1e12})
+    log(json.dumps(per_proj))
+
+    roofline = {"bound": "mfma", "achieved": gemm_tops, "peak": PEAK_INT8_OPS / 1e12,
+                "unit": "TFLOP/s", "frac": gemm_tops * 1e12 / PEAK_INT8_OPS, "traffic": None,
+                "kernel": "gemm_i8_nk_kernel<F16>",
+                "avg_launch_us": gemm_avg_us,
+                "note": "int8 ops (2*M*N*K) per launch / average launch duration over the four "
+                        "projection GEMMs; peak = 5.0 POP/s dense int8"}
+
+    extras = {}
+    if not args.no_extras:
+        extras["smoothquant_cfg1"] = bench_quantizer(torch, w8a8, dev, gen)
+        log(json.dumps(extras["smoothquant_cfg1"]))
+        extras["gemm_cfg2"] = bench_gemm_4096(torch, w8a8, dev, gen)
+        log(json.dumps(extras["gemm_cfg2"]))
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(projs, args.cpu_rows)
+        log(json.dumps(cpu))
+
+    line = {
+        "metric": "int8 TOPS (%MFMA peak) fused SQ+GEMM; SmoothQuant GB/s (%HBM peak)",
+        "value": value,
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded N(0,1) activations with 0.5% x20 outlier columns, "
+                "U{-127..127} int8 weights)",
+        "config": {"workload": "cfg3 fused SmoothQuant + W8A8 GEMM, Llama-3-8B projections "
+                               "qkv/o_proj/gate_up/down",
+                   "m": args.m, "projections": [[n_, k, n] for (n_, k, n) in LLAMA3_8B],
+                   "parallelism": "single GPU"},
+        "frac_mfma_peak": value * 1e12 / PEAK_INT8_OPS,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "per_projection": per_proj,
+        **extras,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,137 @@
+/*
+ * w8a8.h -- C ABI of the MI355X (gfx950) W8A8 SmoothQuant inference path.
+ *
+ * Every entry point:
+ *   - takes caller-allocated device pointers, plain sizes and an explicit
+ *     hipStream_t (0 = the null stream the reference samples launch on);
+ *   - validates every argument on the host BEFORE any HIP call and returns a
+ *     status code instead of exiting (the reference calls exit(1) from its
+ *     CHECK_HIP macros, rocwmma_smoothquant.cpp:35-37, common.hpp:34-46);
+ *   - is asynchronous with respect to the host: work is enqueued on `stream`.
+ *
+ * Status codes coincide with hipError_t: 0 = success, 1 = invalid argument
+ * (hipErrorInvalidValue), 801 = shape/layout not supported
+ * (hipErrorNotSupported); any other value is the HIP runtime error that the
+ * launch reported.  w8a8_last_error() returns a human-readable message for
+ * the last failing call on the calling thread.
+ *
+ * fp16 tensors are passed as `const void*` / `void*` holding IEEE binary16.
+ */
+#ifndef W8A8_H
+#define W8A8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define W8A8_SUCCESS 0
+#define W8A8_ERROR_INVALID_VALUE 1
+#define W8A8_ERROR_NOT_SUPPORTED 801
+
+/* GEMM operand layouts. */
+#define W8A8_LAYOUT_A_ROW_B_NK 0 /* A [M,K] row-major (lda>=K); B [N,K] K-contiguous (ldb>=K) */
+#define W8A8_LAYOUT_A_COL_B_KN 1 /* A col-major (lda>=M); B [K,N] row-major (ldb>=N): the
+                                    layout of rocwmma_gemm_quantized.cpp:92-95,205 */
+
+/* GEMM output types. */
+#define W8A8_OUT_I32 0 /* raw int32 accumulators (verification mode)            */
+#define W8A8_OUT_F16 1 /* fp16 after the fused per-token x per-channel dequant  */
+
+/* Version / diagnostics. */
+const char* w8a8_version(void);
+const char* w8a8_last_error(void);
+
+/* ------------------------------------------------------------------------- */
+/* Quantizer                                                                  */
+/* ------------------------------------------------------------------------- */
+
+/*
+ * Row-wise smooth-scale + absmax int8 quantization.
+ * Replaces kernel_smoothquant (rocwmma_smoothquant.cpp:58-122), launched at
+ * rocwmma_smoothquant.cpp:153-155 with (dX, dS, dY, dRS, M, N, 127.f).
+ *   x           fp16 [M, ldx]   (ldx = 0 means N)
+ *   smooth_scale fp32 [N]
+ *   y           int8 [M, ldy]   (ldy = 0 means N); row-major, i.e. the A
+ *                               operand of w8a8_gemm in W8A8_LAYOUT_A_ROW_B_NK
+ *   row_scale   fp32 [M]        r[m] = max_n |x*s| / quant_max
+ *   quant_max   in (0, 127]
+ * Any N >= 1 is accepted (the reference needs N % 8 == 0 for its vector loop).
+ */
+int w8a8_smoothquant(const void* x, const float* smooth_scale, int8_t* y, float* row_scale,
+                     uint32_t M, uint32_t N, float quant_max, uint32_t ldx, uint32_t ldy,
+                     hipStream_t stream);
+
+/*
+ * MoE smooth quantization with per-expert smooth scales.
+ * Replaces kernel_moe_smoothquant (rocwmma_moe_smoothquant.cpp:69-131).
+ *   x            fp16 [tokens, hidden]
+ *   smooth_scale fp32 [experts, hidden]
+ *   topk_ids     int32 [tokens, topk]
+ *   qy           int8  [rows, hidden], row_scale fp32 [rows]
+ *   dst_row      NULL  -> pair (t, slot) writes row t*topk + slot (the
+ *                         reference's token-major layout, :91); rows = tokens*topk
+ *                non-NULL -> int32 [tokens*topk] destination row per pair (the
+ *                         expert-sorted layout produced by w8a8_moe_sort), so the
+ *                         grouped GEMM reads its A operand without a gather pass;
+ *                         a negative entry, or one >= rows_out, skips the pair.
+ *   rows_out     rows of qy / row_scale (ignored when dst_row is NULL).
+ * A pair whose expert id is outside [0, experts) writes nothing (:86-87).
+ */
+int w8a8_moe_smoothquant(const void* x, const float* smooth_scale, const int32_t* topk_ids,
+                         int8_t* qy, float* row_scale, uint32_t tokens, uint32_t hidden,
+                         uint32_t topk, uint32_t experts, float quant_max,
+                         const int32_t* dst_row, uint32_t rows_out, hipStream_t stream);
+
+/* ------------------------------------------------------------------------- */
+/* int8 GEMM with fused dequant                                               */
+/* ------------------------------------------------------------------------- */
+
+/*
+ * Bytes of device workspace w8a8_gemm needs for this problem (0 for the
+ * primary layout; the sample layout is repacked K-contiguous into it).
+ */
+size_t w8a8_gemm_workspace_size(uint32_t m, uint32_t n, uint32_t k, int layout);
+
+/*
+ * C = dequant(A . B^T).  Replaces gemm_quant_tensor_scale
+ * (rocwmma_gemm_quantized.cpp:127-195) and implements its documented Mode 2
+ * (:18-26), which the reference does not implement:
+ *   acc[m,n] = sum_k int32(A[m,k]) * int32(B[n,k])      (exact int32)
+ *   out_type W8A8_OUT_I32: C int32 [m, ldc] = acc
+ *   out_type W8A8_OUT_F16: C fp16  [m, ldc] =
+ *       scale_a == NULL && scale_b == NULL:
+ *           half(float(acc) * (tensor_scale_a * tensor_scale_b))   (Mode 1, :189-193)
+ *       otherwise:
+ *           half((float(acc) * sa) * sb),  sa = scale_a ? scale_a[m] : tensor_scale_a,
+ *                                          sb = scale_b ? scale_b[n] : tensor_scale_b
+ * Argument order follows gemm_quant_tensor_scale (m, n, k, a, b, c, lda, ldb, ldc, scales).
+ * Decode shapes (small m) are dispatched to a split-K kernel automatically.
+ */
+int w8a8_gemm(uint32_t m, uint32_t n, uint32_t k, const int8_t* a, const int8_t* b, void* c,
+              uint32_t lda, uint32_t ldb, uint32_t ldc, const float* scale_a,
+              const float* scale_b, float tensor_scale_a, float tensor_scale_b, int out_type,
+              int layout, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Fused SmoothQuant + W8A8 GEMM for one linear layer:
+ *   (q, r) = smoothquant(x, smooth_scale)       q int8 [m, k], r fp32 [m]
+ *   c      = half((float(q . w^T) * r[m]) * scale_w[n])
+ *   x fp16 [m, ldx]; w int8 [n, ldw] (K-contiguous weights); c fp16 [m, ldc].
+ * q and row_scale are caller-provided buffers (m*k bytes, m floats): they are
+ * written, so the caller can reuse the quantized activations for several GEMMs.
+ */
+int w8a8_fused_sq_gemm(const void* x, const float* smooth_scale, const int8_t* w,
+                       const float* scale_w, void* c, uint32_t m, uint32_t n, uint32_t k,
+                       uint32_t ldx, uint32_t ldw, uint32_t ldc, int8_t* q, float* row_scale,
+                       hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* W8A8_H */

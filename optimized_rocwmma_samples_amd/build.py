@@ -1,0 +1,129 @@
+"""Build libw8a8.so (gfx950 HIP kernels + C ABI) and the C++ sample CLIs in-tree.
+
+    python -m optimized_rocwmma_samples_amd.build [--debug] [--verbose] [--no-apps]
+
+Every HIP translation unit is compiled with hipcc for gfx950 only.  The built
+library lands in optimized_rocwmma_samples_amd/lib/, the CLIs in
+optimized_rocwmma_samples_amd/bin/ (both git-ignored, both shipped with the
+tree to the GPU box).  `--debug` builds the CLIs with the CPU-verify switch on,
+the equivalent of the reference's `build.sh -d` (build.sh:43, a Debug build
+leaves NDEBUG undefined and enables the `#if !NDEBUG` check,
+rocwmma_perf_gemm.cpp:736-749).
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+APPS = PKG / "apps"
+LIB_DIR = PKG / "lib"
+BIN_DIR = PKG / "bin"
+OBJ_DIR = PKG / "_build"
+LIB_PATH = LIB_DIR / "libw8a8.so"
+
+ARCH = "gfx950"
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+
+SOURCES = [
+    "capi.cpp",
+    "smoothquant.hip",
+    "gemm_i8.hip",
+]
+
+# -packed-fp32-ops: keep the compiler from emitting packed fp32 VALU ops.
+HIP_FLAGS = [
+    "-std=c++17",
+    "-O3",
+    f"--offload-arch={ARCH}",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-function",
+    "-Wno-unused-command-line-argument",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{ROOT / 'include'}",
+]
+
+
+def hipcc() -> str:
+    cand = shutil.which("hipcc") or os.path.join(ROCM, "bin", "hipcc")
+    if not os.path.exists(cand):
+        raise RuntimeError("hipcc not found; the W8A8 library needs ROCm's hipcc")
+    return cand
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in res.stdout.splitlines() if "packed-fp32-ops" not in l
+                    and "not a recognized feature" not in l and l.strip())
+    if res.returncode != 0:
+        raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n{res.stdout}")
+    if verbose and out:
+        print(out)
+
+
+def _compile(src: Path, obj: Path, verbose: bool, extra: list[str]) -> Path:
+    lang = ["-x", "hip"] if src.suffix in (".hip", ".cpp") else []
+    _run([hipcc(), *lang, *HIP_FLAGS, *extra, "-c", str(src), "-o", str(obj)], verbose)
+    return obj
+
+
+def build_library(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile every HIP source for gfx950 and link lib/libw8a8.so."""
+    OBJ_DIR.mkdir(exist_ok=True)
+    LIB_DIR.mkdir(exist_ok=True)
+    jobs = jobs or min(8, os.cpu_count() or 4)
+    objs = []
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        futs = [ex.submit(_compile, CSRC / s, OBJ_DIR / (Path(s).stem + ".o"), verbose, [])
+                for s in SOURCES]
+        for f in futs:
+            objs.append(f.result())
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+          *map(str, objs)], verbose)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+def build_apps(debug: bool = False, verbose: bool = False) -> list[Path]:
+    """Build the reference-compatible sample CLIs against libw8a8.so."""
+    if not APPS.is_dir():
+        return []
+    BIN_DIR.mkdir(exist_ok=True)
+    outs = []
+    verify = ["-UNDEBUG", "-DW8A8_CPU_VERIFY=1"] if debug else ["-DNDEBUG"]
+    for src in sorted(APPS.glob("*.cpp")):
+        exe = BIN_DIR / src.stem
+        _run([hipcc(), "-x", "hip", *HIP_FLAGS, *verify, "-fopenmp", str(src),
+              "-o", str(exe), f"-L{LIB_DIR}", "-lw8a8", "-Wl,-rpath,$ORIGIN/../lib"],
+             verbose)
+        outs.append(exe)
+    return outs
+
+
+def main(argv: list[str] | None = None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--debug", action="store_true", help="CLIs with the CPU-verify switch")
+    ap.add_argument("--verbose", "-v", action="store_true")
+    ap.add_argument("--no-apps", action="store_true")
+    args = ap.parse_args(argv)
+    lib = build_library(verbose=args.verbose)
+    print(f"built {lib}")
+    if not args.no_apps:
+        for exe in build_apps(debug=args.debug, verbose=args.verbose):
+            print(f"built {exe}")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

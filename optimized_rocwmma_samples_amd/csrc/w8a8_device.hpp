@@ -1,0 +1,84 @@
+// w8a8_device.hpp -- gfx950 device helpers shared by the W8A8 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace w8a8 {
+
+typedef int   v2i __attribute__((ext_vector_type(2)));
+typedef int   v4i __attribute__((ext_vector_type(4)));
+typedef int   v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// DPP controls (GCN/CDNA encoding).
+constexpr int kDppQuadXor1      = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2      = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int kDppRowMirror     = 0x140; // lane i <- lane 15-i inside each row of 16
+constexpr int kDppRowHalfMirror = 0x141; // lane i <- lane 7-i inside each half-row of 8
+
+template <int Ctrl>
+__device__ __forceinline__ float dpp_mov(float v)
+{
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(0, __float_as_int(v), Ctrl, 0xF, 0xF, false));
+}
+
+// Max over all 64 lanes; the result is wave-uniform.  max is exact, so the
+// reduction order cannot change the value.
+__device__ __forceinline__ float wave_max(float v)
+{
+    v = fmaxf(v, dpp_mov<kDppQuadXor1>(v));
+    v = fmaxf(v, dpp_mov<kDppQuadXor2>(v));
+    v = fmaxf(v, dpp_mov<kDppRowHalfMirror>(v));
+    v = fmaxf(v, dpp_mov<kDppRowMirror>(v));
+    float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t h16)
+{
+    _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)h16);
+    return (float)h;
+}
+
+__device__ __forceinline__ uint16_t float_to_half_bits(float f)
+{
+    _Float16 h = (_Float16)f; // v_cvt_f16_f32, round to nearest even
+    return __builtin_bit_cast(uint16_t, h);
+}
+
+// int8 quantization of one smoothed value (reference order: (x*s)*inv, rint,
+// clamp to +-qmax, rocwmma_smoothquant.cpp:110-113).
+__device__ __forceinline__ int quant_i8(float p, float inv, float qmax)
+{
+    float v = p * inv;
+    return (int)fminf(fmaxf(__builtin_rintf(v), -qmax), qmax);
+}
+
+__device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d)
+{
+    return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16)
+           | ((uint32_t)d << 24);
+}
+
+// s_waitcnt vmcnt(N) with expcnt/lgkmcnt left at their maxima (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+
+__device__ __forceinline__ void wait_lgkmcnt0()
+{
+    __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
+}
+
+} // namespace w8a8

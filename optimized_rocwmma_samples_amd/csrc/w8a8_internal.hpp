@@ -1,0 +1,59 @@
+// w8a8_internal.hpp -- launchers shared between the kernel files and the C ABI.
+// Callers (capi.cpp) have validated every argument before these run.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace w8a8 {
+
+// Describes where quantizer row `i` reads from and writes to.
+struct QuantRows {
+    const uint16_t* x;        // fp16 source
+    const float*    s;        // smooth scale (dense: [N]; moe: [experts, N])
+    int8_t*         q;        // int8 destination
+    float*          r;        // row scales
+    uint32_t        rows;     // number of logical rows (dense: M, moe: tokens*topk)
+    uint32_t        n;        // row length
+    uint32_t        ldx, ldq; // strides in elements
+    float           qmax;
+    // MoE gather (all NULL / 0 for the dense quantizer)
+    const int32_t* topk_ids;
+    const int32_t* dst_row;
+    uint32_t       rows_out; // destination rows (bound for dst_row entries)
+    uint32_t       topk;
+    uint32_t       experts;
+};
+
+hipError_t launch_smoothquant(const QuantRows& p, hipStream_t stream);
+
+struct GemmArgs {
+    uint32_t       m, n, k;
+    const int8_t*  a;
+    const int8_t*  b;
+    void*          c;
+    uint32_t       lda, ldb, ldc;
+    const float*   scale_a;
+    const float*   scale_b;
+    float          tsa, tsb;
+    int            out_type; // W8A8_OUT_*
+};
+
+// A row-major [m,k], B [n,k] K-contiguous.  Fast path requirements (checked by
+// the caller through gemm_fast_path_ok): 16-byte aligned a/b, lda/ldb % 16 == 0,
+// k % 16 == 0.
+bool       gemm_fast_path_ok(const GemmArgs& g);
+hipError_t launch_gemm_nk(const GemmArgs& g, hipStream_t stream);
+
+// Generic strided GEMM (any layout/alignment): A(m,k) = a[m*sam + k*sak],
+// B(n,k) = b[n*sbn + k*sbk].  Slow; used for odd shapes.
+hipError_t launch_gemm_generic(const GemmArgs& g, size_t sam, size_t sak, size_t sbn,
+                               size_t sbk, hipStream_t stream);
+
+// Transposing repack: dst[r, c] = src[c*lds_src + r] for r < rows, c < cols,
+// dst row-major with leading dimension ldd (zero-padded up to ldd).
+hipError_t launch_transpose_i8(const int8_t* src, uint32_t lds_src, int8_t* dst, uint32_t ldd,
+                               uint32_t rows, uint32_t cols, hipStream_t stream);
+
+} // namespace w8a8
