@@ -53,6 +53,29 @@ class W8A8Error(RuntimeError):
         self.message = message
 
 
+def _bind_hip_runtime() -> None:
+    """Make libw8a8.so share the HIP runtime of the PyTorch build in use.
+
+    PyTorch-ROCm ships its own libamdhip64.so (SONAME libamdhip64.so.7, but its
+    own libraries NEED the unversioned name).  If libw8a8.so were loaded first,
+    its libamdhip64.so.7 would resolve to /opt/rocm and torch would then load a
+    second HIP + HSA runtime into the process: kernels launched through one
+    runtime are not ordered against copies issued through the other, and two
+    HSA runtimes driving one device crash.  Importing torch first lets the
+    dynamic loader satisfy libamdhip64.so.7 with torch's already-loaded copy.
+    """
+    try:
+        import torch  # noqa: F401
+    except ImportError:  # C++-only users: /opt/rocm's runtime is the only one
+        pass
+
+
+def loaded_hip_runtimes() -> list[str]:
+    """Paths of every libamdhip64 mapped into this process (should be one)."""
+    with open("/proc/self/maps") as f:
+        return sorted({l.split()[-1] for l in f if "libamdhip64" in l})
+
+
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
 
@@ -68,6 +91,7 @@ def load(path: str | Path | None = None) -> ctypes.CDLL:
             raise RuntimeError(
                 f"libw8a8.so not found at {p}; build it with "
                 "`python -m optimized_rocwmma_samples_amd.build` (no fallback exists)")
+        _bind_hip_runtime()
         lib = ctypes.CDLL(str(p))
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(lib, name)

@@ -71,6 +71,10 @@ def ref() -> ctypes.CDLL | None:
     if _ref is None:
         if not REF_SO.exists():
             return None
+        try:  # share torch's HIP runtime (see optimized_rocwmma_samples_amd._lib)
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         lib = ctypes.CDLL(str(REF_SO))
         for name, (res, args) in _REF_SIGS.items():
             f = getattr(lib, name)
