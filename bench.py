@@ -149,8 +149,11 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--m", type=int, default=8192, help="tokens per projection")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-rows", type=int, default=32)
+    ap.add_argument("--cpu-rows", type=int, default=256)
     ap.add_argument("--no-extras", action="store_true", help="skip cfg1/cfg2 side measurements")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a plain 1 GiB device copy (reads 1 GiB, writes 1 GiB) so "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE can be scaled to bytes")
     args = ap.parse_args(argv)
 
     if args.gpus != 1:
@@ -236,6 +239,15 @@ def main(argv=None) -> int:
         log(json.dumps(extras["smoothquant_cfg1"]))
         extras["gemm_cfg2"] = bench_gemm_4096(torch, w8a8, dev, gen)
         log(json.dumps(extras["gemm_cfg2"]))
+
+    if args.calibrate_copy:
+        src = torch.randint(-127, 128, (1 << 30,), generator=gen, device=dev, dtype=torch.int8)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        torch.neg(src, out=dst)  # elementwise kernel: 2^30 bytes in, 2^30 bytes out
+        torch.cuda.synchronize()
+        log("calibration copy: 1073741824 bytes read + 1073741824 bytes written (torch neg)")
+        del src, dst
 
     cpu = None
     if not args.no_cpu_baseline:
