@@ -1,0 +1,445 @@
+// gemm_i8_kernel.hpp -- int8 x int8 -> int32 GEMM tile kernel for gfx950 with a
+// fused per-token x per-channel dequant epilogue, templated on the tile shape.
+//
+// Computation (gemm_quant_tensor_scale, rocwmma_gemm_quantized.cpp:127-195, in
+// its documented Mode 2, :18-26):
+//   acc[m,n] = sum_k A[m,k] * B[n,k]                 (int32, exact)
+//   C[m,n]   = half((float(acc) * sa[m]) * sb[n])    or the int32 acc itself
+// A is [M,K] row-major, B is [N,K] K-contiguous (both operands K-major).
+//
+// Tile hierarchy (Cfg): block BM x BN x BK, WAVES_M x WAVES_N waves, each wave
+// owning a (BM/WAVES_M) x (BN/WAVES_N) tile of 32x32 v_mfma_i32_32x32x32_i8.
+// The MFMA is issued with srcA = B fragment (rows n) and srcB = A fragment
+// (rows m): D[i=n][j=m], so each lane owns one m and runs of 4 consecutive n
+// and the epilogue writes 4 fp16 (8 B) or 4 int32 (16 B) per store.
+//
+// Data movement
+//   * global -> LDS with global_load_lds_dwordx4 (no VGPR staging): one wave
+//     instruction fills 1 KiB of LDS, lane i writing bytes [16i, 16i+16); the
+//     LDS layout is chosen by which global 16-byte chunk each lane fetches.
+//   * An LDS row holds the BK bytes of one m (or n); with C = BK/16 chunks per
+//     row, chunk c of row r is stored at chunk c ^ ((r >> log2(16/C)) & (C-1)).
+//     The 16 lanes of each ds_read_b128 quarter-wave (16 consecutive rows, same
+//     logical chunk) then hit 16 distinct 16-byte bank groups: conflict-free.
+//   * STAGES-deep ring: tiles t+1..t+STAGES-1 are in flight while t computes.
+//     One barrier per BK-deep tile, placed before the last 32-deep MFMA group
+//     so LDS fragment reads always overlap MFMA work.
+//   * Loads are raw buffer loads into LDS: per-lane offsets are fixed, the
+//     tile's k offset is the uniform soffset, and out-of-range rows / k-chunks
+//     use an offset past the buffer, which reads as zeros; edges need no
+//     masking in the main loop (K must be a multiple of 16).
+//   * Block order: hardware block ids go round-robin over the 8 XCDs; they are
+//     remapped so each XCD owns a contiguous run of tiles (shared A/B panels
+//     stay in one L2), grouped GROUP_M tile-rows at a time.
+#pragma once
+
+#include "../../include/w8a8.h"
+#include "w8a8_device.hpp"
+
+#include <mutex>
+
+namespace w8a8 {
+
+namespace gemm {
+
+template <int BM_, int BN_, int BK_, int STAGES_, int WAVES_M_, int WAVES_N_, int GROUP_M_ = 8>
+struct Cfg {
+    static constexpr int kBM      = BM_;
+    static constexpr int kBN      = BN_;
+    static constexpr int kBK      = BK_;
+    static constexpr int kStages  = STAGES_;
+    static constexpr int kWavesM  = WAVES_M_;
+    static constexpr int kWavesN  = WAVES_N_;
+    static constexpr int kGroupM  = GROUP_M_;
+    static constexpr int kWaves   = kWavesM * kWavesN;
+    static constexpr int kThreads = kWaves * kWave;
+    static constexpr int kWaveM   = kBM / kWavesM;
+    static constexpr int kWaveN   = kBN / kWavesN;
+    static constexpr int kTilesM  = kWaveM / 32;
+    static constexpr int kTilesN  = kWaveN / 32;
+    static constexpr int kChunks  = kBK / 16;           // 16-byte chunks per LDS row
+    static constexpr int kSwzShift = kChunks == 8 ? 1 : (kChunks == 4 ? 2 : 3);
+    static constexpr int kRowsPerLoad = kWave / kChunks; // rows one wave-load fills
+    static constexpr int kABytes  = kBM * kBK;
+    static constexpr int kBBytes  = kBN * kBK;
+    static constexpr int kStageBytes = kABytes + kBBytes;
+    static constexpr int kLdsBytes   = kStages * kStageBytes;
+    static constexpr int kLoadsA  = kABytes / 1024 / kWaves; // wave-loads per wave per stage
+    static constexpr int kLoadsB  = kBBytes / 1024 / kWaves;
+    static constexpr int kLoads   = kLoadsA + kLoadsB;
+    static constexpr int kSubK    = kBK / 32;            // 32-deep MFMA groups per tile
+
+    static_assert(kChunks == 2 || kChunks == 4 || kChunks == 8, "BK in {32, 64, 128}");
+    static_assert(kSubK % 2 == 0 || kSubK == 1, "fragment ping-pong needs an even group count");
+    static_assert(kLoadsA * kWaves * 1024 == kABytes && kLoadsB * kWaves * 1024 == kBBytes,
+                  "tile bytes must split evenly into 1 KiB wave-loads");
+    static_assert(kWaveM % 32 == 0 && kWaveN % 32 == 0, "wave tile made of 32x32 MFMA tiles");
+    static_assert(kStages >= 2, "at least double buffering");
+    static_assert(kLoads * (kStages - 1) < 64, "vmcnt counter range");
+    static_assert(kLdsBytes <= 160 * 1024, "gfx950 LDS per workgroup");
+};
+
+struct KArgs {
+    const int8_t* a;
+    const int8_t* b;
+    void*         c;
+    const float*  sa;
+    const float*  sb;
+    uint32_t      m, n, k;
+    uint32_t      lda, ldb, ldc;
+    float         tsa, tsb;
+};
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// sched_group_barrier instruction classes
+constexpr int kSchedMfma   = 0x008;
+constexpr int kSchedVmemRd = 0x020;
+constexpr int kSchedDsRead = 0x100;
+
+// Buffer resource word 3 for gfx9 raw buffers (32-bit data format, no swizzle)
+// and the byte offset that lies past every operand (operands stay < 2 GiB).
+constexpr int      kBufferFlags = 0x00020000;
+constexpr uint32_t kOob         = 0x80000000u;
+
+// Hardware dispatches block ids round-robin over the 8 XCDs.  Return the
+// logical tile id such that each XCD owns a contiguous range of logical ids.
+__device__ __forceinline__ uint32_t xcd_remap(uint32_t bid, uint32_t total)
+{
+    constexpr uint32_t kXcd = 8;
+    const uint32_t     q    = total / kXcd;
+    const uint32_t     r    = total % kXcd;
+    const uint32_t     x    = bid % kXcd;
+    const uint32_t     i    = bid / kXcd;
+    return x * q + min(x, r) + i;
+}
+
+template <int GROUP_M>
+__device__ __forceinline__ void tile_coords(uint32_t lid, uint32_t tiles_m, uint32_t tiles_n,
+                                            uint32_t& tm, uint32_t& tn)
+{
+    const uint32_t per_group = GROUP_M * tiles_n;
+    const uint32_t group     = lid / per_group;
+    const uint32_t first_m   = group * GROUP_M;
+    const uint32_t gsize     = min(tiles_m - first_m, (uint32_t)GROUP_M);
+    const uint32_t in_group  = lid % per_group;
+    tm                       = first_m + in_group % gsize;
+    tn                       = in_group / gsize;
+}
+
+// Barrier between the waves of a block without the release/acquire fences of
+// __syncthreads() (those wait for every outstanding global->LDS load, vmcnt(0),
+// and would serialize the prefetch ring).  LDS hazards are covered by the
+// explicit s_waitcnt calls placed before each barrier.
+__device__ __forceinline__ void block_barrier()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// One 32-deep MFMA group: MFMAs and the DS reads of the next fragments
+// alternate, then the remaining MFMAs follow.  The first MFMA stays ahead of
+// the reads so it waits only on fragments read one group earlier.
+template <int NMFMA, int NDS, int ID>
+__device__ __forceinline__ void interleave_mfma_ds()
+{
+    constexpr int kPairs = NDS < NMFMA ? NDS : NMFMA;
+#pragma unroll
+    for(int i = 0; i < kPairs; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, ID);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, ID);
+    }
+    if constexpr(NMFMA > kPairs)
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, NMFMA - kPairs, ID);
+    if constexpr(NDS > kPairs)
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, NDS - kPairs, ID);
+}
+
+// The group after the barrier also issues the refill of the freed stage:
+// steps of (one MFMA, its share of global->LDS loads, its share of DS reads),
+// then the remaining MFMAs.
+template <int I, int STEPS, int NVMEM, int NDS, int ID>
+__device__ __forceinline__ void interleave_step()
+{
+    if constexpr(I < STEPS) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, ID);
+        constexpr int nv = (I + 1) * NVMEM / STEPS - I * NVMEM / STEPS;
+        constexpr int nd = (I + 1) * NDS / STEPS - I * NDS / STEPS;
+        if constexpr(nv > 0) __builtin_amdgcn_sched_group_barrier(kSchedVmemRd, nv, ID);
+        if constexpr(nd > 0) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, nd, ID);
+        interleave_step<I + 1, STEPS, NVMEM, NDS, ID>();
+    }
+}
+
+template <int NMFMA, int NVMEM, int NDS, int ID>
+__device__ __forceinline__ void interleave_mfma_vmem_ds()
+{
+    constexpr int kSteps = NMFMA;
+    interleave_step<0, kSteps, NVMEM, NDS, ID>();
+}
+
+// Store 4 consecutive-n outputs of one lane.
+template <int OUT>
+__device__ __forceinline__ void store4(const KArgs& p, uint32_t m, uint32_t n, const int* v,
+                                       float sa, const float4& sb, float ab, bool mode1,
+                                       bool vec_ok)
+{
+    if(m >= p.m) return;
+    if constexpr(OUT == W8A8_OUT_I32) {
+        int32_t* dst = reinterpret_cast<int32_t*>(p.c) + (size_t)m * p.ldc + n;
+        if(vec_ok && n + 4 <= p.n) {
+            *reinterpret_cast<int4*>(dst) = make_int4(v[0], v[1], v[2], v[3]);
+        } else {
+            for(int e = 0; e < 4; ++e)
+                if(n + e < p.n) dst[e] = v[e];
+        }
+    } else {
+        const float sbv[4] = {sb.x, sb.y, sb.z, sb.w};
+        uint16_t    h[4];
+#pragma unroll
+        for(int e = 0; e < 4; ++e) {
+            float f = (float)v[e];
+            f       = mode1 ? f * ab : (f * sa) * sbv[e];
+            h[e]    = float_to_half_bits(f);
+        }
+        uint16_t* dst = reinterpret_cast<uint16_t*>(p.c) + (size_t)m * p.ldc + n;
+        if(vec_ok && n + 4 <= p.n) {
+            uint2 pk;
+            pk.x = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+            pk.y = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
+            *reinterpret_cast<uint2*>(dst) = pk;
+        } else {
+            for(int e = 0; e < 4; ++e)
+                if(n + e < p.n) dst[e] = h[e];
+        }
+    }
+}
+
+template <class C, int OUT>
+__global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_tile_kernel(KArgs p, int vec_ok)
+{
+    extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
+
+    const uint32_t tiles_m = (p.m + C::kBM - 1) / C::kBM;
+    const uint32_t tiles_n = (p.n + C::kBN - 1) / C::kBN;
+    uint32_t       tm, tn;
+    tile_coords<C::kGroupM>(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, tm, tn);
+    const uint32_t m0 = tm * C::kBM;
+    const uint32_t n0 = tn * C::kBN;
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); // wave-uniform
+    const int lane = threadIdx.x % kWave;
+    const int wm   = wave / C::kWavesN;
+    const int wn   = wave % C::kWavesN;
+
+    // ---- global -> LDS load descriptors -----------------------------------
+    // Wave-load j of the A (or B) tile fills rows kRowsPerLoad*j ... ; lane l
+    // covers row kRowsPerLoad*j + l / kChunks at physical chunk l % kChunks and
+    // therefore fetches logical chunk (l % kChunks) ^ swizzle(row).
+    // Loads are raw buffer loads: the per-lane byte offset is fixed for the
+    // whole K loop, the tile's k offset travels in the uniform soffset, and a
+    // row past the matrix gets offset kOob, which the buffer range check turns
+    // into zeros (the host keeps each operand under 2 GiB).
+    const int lrow = lane / C::kChunks;
+    uint32_t  va[C::kLoadsA], vb[C::kLoadsB]; // per-lane byte offsets (k0 excluded)
+    int       cha[C::kLoadsA], chb[C::kLoadsB];
+#pragma unroll
+    for(int i = 0; i < C::kLoadsA; ++i) {
+        const uint32_t r = (wave * C::kLoadsA + i) * C::kRowsPerLoad + lrow;
+        cha[i]           = (lane % C::kChunks) ^ ((r >> C::kSwzShift) & (C::kChunks - 1));
+        va[i]            = (m0 + r) < p.m ? (m0 + r) * p.lda + cha[i] * 16 : kOob;
+    }
+#pragma unroll
+    for(int i = 0; i < C::kLoadsB; ++i) {
+        const uint32_t r = (wave * C::kLoadsB + i) * C::kRowsPerLoad + lrow;
+        chb[i]           = (lane % C::kChunks) ^ ((r >> C::kSwzShift) & (C::kChunks - 1));
+        vb[i]            = (n0 + r) < p.n ? (n0 + r) * p.ldb + chb[i] * 16 : kOob;
+    }
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t*>(p.a), 0, (int)(p.m * p.lda), kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t*>(p.b), 0, (int)(p.n * p.ldb), kBufferFlags);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)lds; // LDS byte address of the ring
+
+    auto issue_stage = [&](int stage, uint32_t kt) {
+        const uint32_t k0     = kt * C::kBK;
+        const bool     full_k = k0 + C::kBK <= p.k; // uniform: only a K tail is partial
+        const uint32_t sbase  = lds0 + stage * C::kStageBytes + wave * (C::kLoadsA * 1024);
+        const uint32_t sbaseb = lds0 + stage * C::kStageBytes + C::kABytes
+                                + wave * (C::kLoadsB * 1024);
+#pragma unroll
+        for(int i = 0; i < C::kLoadsA; ++i) {
+            const uint32_t v = (full_k || k0 + cha[i] * 16 < p.k) ? va[i] : kOob;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ra, (lds_void_t*)(uintptr_t)(sbase + i * 1024), 16, v, k0, 0, 0);
+        }
+#pragma unroll
+        for(int i = 0; i < C::kLoadsB; ++i) {
+            const uint32_t v = (full_k || k0 + chb[i] * 16 < p.k) ? vb[i] : kOob;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rb, (lds_void_t*)(uintptr_t)(sbaseb + i * 1024), 16, v, k0, 0, 0);
+        }
+    };
+
+    // ---- LDS -> register fragment offsets ----------------------------------
+    // Fragment row = lane % 32 of a 32-row tile; k-chunk = 2*g + lane / 32 for
+    // MFMA group g.  Both operands use the same lane -> k mapping, so the sum
+    // over k is the full dot product whatever order the MFMA reduces it in.
+    const int frow = lane & 31;
+    const int fswz = (frow >> C::kSwzShift) & (C::kChunks - 1);
+    int       offa[C::kTilesM], offb[C::kTilesN];
+#pragma unroll
+    for(int t = 0; t < C::kTilesM; ++t) offa[t] = (wm * C::kWaveM + t * 32 + frow) * C::kBK;
+#pragma unroll
+    for(int t = 0; t < C::kTilesN; ++t)
+        offb[t] = C::kABytes + (wn * C::kWaveN + t * 32 + frow) * C::kBK;
+    int cofs[C::kSubK];
+#pragma unroll
+    for(int g = 0; g < C::kSubK; ++g) cofs[g] = ((2 * g + (lane >> 5)) ^ fswz) * 16;
+
+    v16i acc[C::kTilesM][C::kTilesN];
+#pragma unroll
+    for(int i = 0; i < C::kTilesM; ++i)
+#pragma unroll
+        for(int j = 0; j < C::kTilesN; ++j) acc[i][j] = v16i{0};
+
+    using FragA = v4i[C::kTilesM];
+    using FragB = v4i[C::kTilesN];
+    auto load_frags = [&](const int8_t* sbase, int g, FragA& af, FragB& bf) {
+#pragma unroll
+        for(int t = 0; t < C::kTilesM; ++t)
+            af[t] = *reinterpret_cast<const v4i*>(sbase + offa[t] + cofs[g]);
+#pragma unroll
+        for(int t = 0; t < C::kTilesN; ++t)
+            bf[t] = *reinterpret_cast<const v4i*>(sbase + offb[t] + cofs[g]);
+    };
+    auto mfma_tile = [&](const FragA& af, const FragB& bf) {
+#pragma unroll
+        for(int i = 0; i < C::kTilesM; ++i)
+#pragma unroll
+            for(int j = 0; j < C::kTilesN; ++j)
+                acc[i][j]
+                    = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], acc[i][j], 0, 0, 0);
+    };
+    constexpr int kMfma = C::kTilesM * C::kTilesN;
+    constexpr int kDs   = C::kTilesM + C::kTilesN;
+
+    const uint32_t nk = (p.k + C::kBK - 1) / C::kBK;
+
+    // ---- prologue: fill every stage of the ring ----------------------------
+    // Tiles past K are still issued (every lane then reads kOob: zeros, no
+    // memory traffic), so each wave always has the same loads in flight and
+    // every wait below is a compile-time count.
+#pragma unroll
+    for(int s = 0; s < C::kStages; ++s) issue_stage(s, s);
+    wait_vmcnt<C::kLoads * (C::kStages - 1)>(); // tile 0 landed
+    block_barrier();
+
+    FragA fa[2];
+    FragB fb[2];
+    load_frags(lds, 0, fa[0], fb[0]);
+
+    // ---- main loop (the last tile is peeled: one path for the waitcnt pass) -
+    // Per tile kt: MFMA groups 0..S-2 read the next group's fragments as they
+    // go; then [all reads of stage kt done, tile kt+1 landed] barrier; the
+    // last group refills stage kt with tile kt+S and reads tile kt+1 group 0.
+    for(uint32_t kt = 0; kt + 1 < nk; ++kt) {
+        const int8_t* sbase = lds + (kt % C::kStages) * C::kStageBytes;
+#pragma unroll
+        for(int g = 0; g + 1 < C::kSubK; ++g) {
+            load_frags(sbase, g + 1, fa[(g + 1) & 1], fb[(g + 1) & 1]);
+            mfma_tile(fa[g & 1], fb[g & 1]);
+            interleave_mfma_ds<kMfma, kDs, 0>();
+        }
+        constexpr int gl = C::kSubK - 1;
+        __builtin_amdgcn_sched_barrier(0);
+        wait_lgkmcnt0(); // this wave's reads of stage kt are done before it is refilled
+        wait_vmcnt<C::kLoads * (C::kStages - 2)>(); // tile kt+1 landed
+        block_barrier();
+        issue_stage(kt % C::kStages, kt + C::kStages);
+        load_frags(lds + ((kt + 1) % C::kStages) * C::kStageBytes, 0, fa[(gl + 1) & 1],
+                   fb[(gl + 1) & 1]);
+        mfma_tile(fa[gl & 1], fb[gl & 1]);
+        interleave_mfma_vmem_ds<kMfma, C::kLoads, kDs, 1>();
+    }
+    {
+        const int8_t* sbase = lds + ((nk - 1) % C::kStages) * C::kStageBytes;
+#pragma unroll
+        for(int g = 0; g + 1 < C::kSubK; ++g) {
+            load_frags(sbase, g + 1, fa[(g + 1) & 1], fb[(g + 1) & 1]);
+            mfma_tile(fa[g & 1], fb[g & 1]);
+        }
+        mfma_tile(fa[(C::kSubK - 1) & 1], fb[(C::kSubK - 1) & 1]);
+    }
+    wait_vmcnt<0>(); // no global->LDS write may outlive the workgroup's LDS
+
+    // ---- epilogue ----------------------------------------------------------
+    // acc[i][j][r]: m = m0 + wm*kWaveM + i*32 + lane%32,
+    //               n = n0 + wn*kWaveN + j*32 + (r/4)*8 + (lane/32)*4 + r%4.
+    const bool  mode1 = (p.sa == nullptr && p.sb == nullptr);
+    const float ab    = p.tsa * p.tsb;
+#pragma unroll
+    for(int i = 0; i < C::kTilesM; ++i) {
+        const uint32_t m  = m0 + wm * C::kWaveM + i * 32 + (lane & 31);
+        float          sa = p.tsa;
+        if(OUT == W8A8_OUT_F16 && p.sa != nullptr && m < p.m) sa = p.sa[m];
+#pragma unroll
+        for(int j = 0; j < C::kTilesN; ++j) {
+#pragma unroll
+            for(int g = 0; g < 4; ++g) {
+                const uint32_t n  = n0 + wn * C::kWaveN + j * 32 + g * 8 + (lane >> 5) * 4;
+                float4         sb = make_float4(p.tsb, p.tsb, p.tsb, p.tsb);
+                if(OUT == W8A8_OUT_F16 && p.sb != nullptr) {
+                    if(vec_ok && n + 4 <= p.n)
+                        sb = *reinterpret_cast<const float4*>(p.sb + n);
+                    else {
+                        if(n + 0 < p.n) sb.x = p.sb[n + 0];
+                        if(n + 1 < p.n) sb.y = p.sb[n + 1];
+                        if(n + 2 < p.n) sb.z = p.sb[n + 2];
+                        if(n + 3 < p.n) sb.w = p.sb[n + 3];
+                    }
+                }
+                const int v[4] = {acc[i][j][g * 4 + 0], acc[i][j][g * 4 + 1],
+                                  acc[i][j][g * 4 + 2], acc[i][j][g * 4 + 3]};
+                store4<OUT>(p, m, n, v, sa, sb, ab, mode1, vec_ok != 0);
+            }
+        }
+    }
+}
+
+// Launch one configuration; the caller has validated the fast-path
+// preconditions (16-byte aligned a/b, lda/ldb/k multiples of 16).
+template <class C, int OUT>
+void raise_lds_limit_once()
+{
+    // Dynamic LDS above 64 KiB: raise the per-kernel limit once per kernel
+    // (best effort; the launch itself reports an error if it cannot be met).
+    static std::once_flag once;
+    std::call_once(once, [] {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_i8_tile_kernel<C, OUT>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
+        (void)hipGetLastError();
+    });
+}
+
+// Launch one configuration; the caller has validated the fast-path
+// preconditions (16-byte aligned a/b, lda/ldb/k multiples of 16).
+template <class C>
+hipError_t launch_cfg(const KArgs& p, int out_type, int vec_ok, hipStream_t stream)
+{
+    const uint32_t tiles = ((p.m + C::kBM - 1) / C::kBM) * ((p.n + C::kBN - 1) / C::kBN);
+    if(out_type == W8A8_OUT_I32) {
+        raise_lds_limit_once<C, W8A8_OUT_I32>();
+        hipLaunchKernelGGL((gemm_i8_tile_kernel<C, W8A8_OUT_I32>), dim3(tiles), dim3(C::kThreads),
+                           C::kLdsBytes, stream, p, vec_ok);
+    } else {
+        raise_lds_limit_once<C, W8A8_OUT_F16>();
+        hipLaunchKernelGGL((gemm_i8_tile_kernel<C, W8A8_OUT_F16>), dim3(tiles), dim3(C::kThreads),
+                           C::kLdsBytes, stream, p, vec_ok);
+    }
+    return hipGetLastError();
+}
+
+} // namespace gemm
+} // namespace w8a8
