@@ -11,8 +11,10 @@ resident in HBM before timing starts.
 
 Also reported: config 1 (standalone quantizer, X fp16 [2048, 4096]) in GB/s
 with buffer sets rotated over >512 MB so the 256 MB MALL cannot serve repeats,
-and config 2 (W8A8 GEMM 4096^3 + dequant) in TOPS.  Per-kernel durations come
-from HIP events recorded on the stream the kernels run on.
+config 2 (W8A8 GEMM 4096^3 + dequant) in TOPS, and config 4 (decode: fused
+SmoothQuant + packed-weight GEMM at M in {1, 16, 64} on the Llama-70B MLP
+weights) in GB/s.  Per-kernel durations come from HIP events recorded on the
+stream the kernels run on.
 
     python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--m 8192] [--no-cpu-baseline]
 """
@@ -142,6 +144,62 @@ def bench_gemm_4096(torch, w8a8, dev, gen, iters=20):
             "TOPS": tops, "frac_mfma": tops * 1e12 / PEAK_INT8_OPS}
 
 
+def bench_decode(torch, w8a8, dev, gen, iters=20):
+    """Config 4: fused SmoothQuant + packed-weight decode GEMM, Llama-70B MLP
+    weights W1 [28672, 8192] and W2 [8192, 28672] at M in {1, 16, 64}.  Two
+    copies of each weight (4 x 235 MB) are used in turn, so consecutive
+    launches never find their weights in the 256 MB MALL."""
+    shapes = [(28672, 8192), (8192, 28672)]
+    weights = {}
+    for n, k in shapes:
+        copies = []
+        for _ in range(2):
+            w = torch.randint(-127, 128, (n, k), generator=gen, device=dev, dtype=torch.int8)
+            copies.append(w8a8.pack_weights(w))
+            del w
+        sb = torch.rand(n, generator=gen, device=dev) * 9e-3 + 1e-3
+        weights[(n, k)] = (copies, sb)
+    results = []
+    for m in (1, 16, 64):
+        bufs = {}
+        for n, k in shapes:
+            x = torch.randn((m, k), generator=gen, device=dev).to(torch.float16)
+            s = torch.rand(k, generator=gen, device=dev) * 1.5 + 0.5
+            bufs[(n, k)] = (x, s, torch.empty((m, k), dtype=torch.int8, device=dev),
+                            torch.empty(m, dtype=torch.float32, device=dev),
+                            torch.empty((m, n), dtype=torch.float16, device=dev))
+        seq = [(sh, c) for c in range(2) for sh in shapes]  # W1a W2a W1b W2b ...
+
+        def launch(sh, c):
+            x, s, q, r, out = bufs[sh]
+            copies, sb = weights[sh]
+            w8a8.fused_sq_gemm_packed(x, s, copies[c], sb, out=out, q=q, row_scale=r)
+
+        for sh, c in seq:
+            launch(sh, c)
+        torch.cuda.synchronize()
+        evs = {sh: [] for sh in shapes}
+        for i in range(iters):
+            for sh, c in seq:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                launch(sh, c)
+                e1.record()
+                evs[sh].append((e0, e1))
+        torch.cuda.synchronize()
+        for (n, k) in shapes:
+            us = sum(a.elapsed_time(b) for a, b in evs[(n, k)]) / len(evs[(n, k)]) * 1e3
+            # algorithmic HBM bytes of the layer: weights once, activations
+            # fp16 in, int8 + row scale round trip, per-channel scales, fp16 out
+            nbytes = n * k + 4 * n + 2 * m * k + 2 * (m * k + 4 * m) + 2 * m * n
+            results.append({"M": m, "N": n, "K": k, "us_per_layer": us,
+                            "GBps": nbytes / (us * 1e-6) / 1e9,
+                            "frac_hbm": nbytes / (us * 1e-6) / PEAK_HBM_BPS,
+                            "TOPS": 2.0 * m * n * k / (us * 1e-6) / 1e12})
+    return {"workload": "cfg4 decode: fused SmoothQuant + packed-weight GEMM (weights "
+                        "rotated over 940 MB)", "layers": results}
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
@@ -228,7 +286,7 @@ def main(argv=None) -> int:
 
     roofline = {"bound": "mfma", "achieved": gemm_tops, "peak": PEAK_INT8_OPS / 1e12,
                 "unit": "TFLOP/s", "frac": gemm_tops * 1e12 / PEAK_INT8_OPS, "traffic": None,
-                "kernel": "gemm_i8_nk_kernel<F16>",
+                "kernel": "gemm_i8_tile_kernel<Cfg<256,256,128,2,2,4>, F16>",
                 "avg_launch_us": gemm_avg_us,
                 "note": "int8 ops (2*M*N*K) per launch / average launch duration over the four "
                         "projection GEMMs; peak = 5.0 POP/s dense int8"}
@@ -239,6 +297,8 @@ def main(argv=None) -> int:
         log(json.dumps(extras["smoothquant_cfg1"]))
         extras["gemm_cfg2"] = bench_gemm_4096(torch, w8a8, dev, gen)
         log(json.dumps(extras["gemm_cfg2"]))
+        extras["decode_cfg4"] = bench_decode(torch, w8a8, dev, gen)
+        log(json.dumps(extras["decode_cfg4"]))
 
     if args.calibrate_copy:
         src = torch.randint(-127, 128, (1 << 30,), generator=gen, device=dev, dtype=torch.int8)

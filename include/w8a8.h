@@ -110,7 +110,11 @@ size_t w8a8_gemm_workspace_size(uint32_t m, uint32_t n, uint32_t k, int layout);
  *           half((float(acc) * sa) * sb),  sa = scale_a ? scale_a[m] : tensor_scale_a,
  *                                          sb = scale_b ? scale_b[n] : tensor_scale_b
  * Argument order follows gemm_quant_tensor_scale (m, n, k, a, b, c, lda, ldb, ldc, scales).
- * Decode shapes (small m) are dispatched to a split-K kernel automatically.
+ * Decode shapes (m <= 64) run a weight-streaming kernel that splits K across
+ * the waves of each block and reduces the int32 partials in LDS: the role of
+ * gemm_splitk_stage1/gemm_splitk_reduce (rocwmma_gemm_splitk.cpp:104-201) and
+ * streamk_gemm_kernel (rocwmma_streamk_gemm.cpp:86-211), in one launch with no
+ * workspace, bit-identical to the full GEMM.
  */
 int w8a8_gemm(uint32_t m, uint32_t n, uint32_t k, const int8_t* a, const int8_t* b, void* c,
               uint32_t lda, uint32_t ldb, uint32_t ldc, const float* scale_a,
@@ -129,6 +133,43 @@ int w8a8_fused_sq_gemm(const void* x, const float* smooth_scale, const int8_t* w
                        const float* scale_w, void* c, uint32_t m, uint32_t n, uint32_t k,
                        uint32_t ldx, uint32_t ldw, uint32_t ldc, int8_t* q, float* row_scale,
                        hipStream_t stream);
+
+/* ------------------------------------------------------------------------- */
+/* Packed ("pre-shuffled") weights                                            */
+/* ------------------------------------------------------------------------- */
+
+/*
+ * Weights packed once into MFMA register order so that every wave-load of the
+ * GEMM reads 1 KiB contiguous: the "pre-shuffled B" that flatmm_kernel's
+ * comment describes (rocwmma_flatmm.cpp:12-16) but its code leaves row-major.
+ * Layout: N padded to 64-row slabs, K to 128-deep k-tiles, 8 KiB per
+ * (slab, k-tile), zero padding.
+ */
+size_t w8a8_pack_weights_size(uint32_t n, uint32_t k);
+
+/* packed <- w (int8 [n, ldw], K-contiguous); packed_bytes >= w8a8_pack_weights_size. */
+int w8a8_pack_weights(const int8_t* w, uint32_t n, uint32_t k, uint32_t ldw, int8_t* packed,
+                      size_t packed_bytes, hipStream_t stream);
+
+/*
+ * w8a8_gemm over packed weights (layout W8A8_LAYOUT_A_ROW_B_NK, B = the packed
+ * buffer of w [n, k]); same outputs bit for bit.  Requires a 16-byte aligned
+ * A with lda % 16 == 0 and k % 16 == 0 (W8A8_ERROR_NOT_SUPPORTED otherwise).
+ * Decode shapes (m <= 64) stream the packed weights at close to HBM rate.
+ */
+int w8a8_gemm_packed(uint32_t m, uint32_t n, uint32_t k, const int8_t* a,
+                     const int8_t* w_packed, void* c, uint32_t lda, uint32_t ldc,
+                     const float* scale_a, const float* scale_b, float tensor_scale_a,
+                     float tensor_scale_b, int out_type, hipStream_t stream);
+
+/*
+ * w8a8_fused_sq_gemm with packed weights: the decode-time linear layer
+ * (smooth-quantize the m token rows, then stream the packed weights once).
+ */
+int w8a8_fused_sq_gemm_packed(const void* x, const float* smooth_scale, const int8_t* w_packed,
+                              const float* scale_w, void* c, uint32_t m, uint32_t n, uint32_t k,
+                              uint32_t ldx, uint32_t ldc, int8_t* q, float* row_scale,
+                              hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -158,3 +158,72 @@ def fused_sq_gemm(x, smooth_scale, w, scale_w, out=None, q=None, row_scale=None)
               m, n, k, x.stride(0), w.stride(0), c.stride(0), _ptr(q), _ptr(r),
               _stream(x.device))
     return c, q, r
+
+
+class PackedWeights:
+    """int8 weights [n, k] packed into MFMA register order (w8a8_pack_weights).
+
+    `data` is the packed uint8-sized device buffer; n and k are the logical
+    weight shape.  Pack once at load time, then run gemm_packed /
+    fused_sq_gemm_packed for every token batch.
+    """
+
+    def __init__(self, data, n: int, k: int):
+        self.data = data
+        self.n = int(n)
+        self.k = int(k)
+
+    @property
+    def shape(self):
+        return (self.n, self.k)
+
+
+def pack_weights_size(n: int, k: int) -> int:
+    return int(library().w8a8_pack_weights_size(n, k))
+
+
+def pack_weights(w, out=None) -> PackedWeights:
+    """Pack int8 weights w [N, K] (K-contiguous rows, any row stride)."""
+    torch = _torch()
+    _require_cuda(w)
+    n, k = w.shape
+    nbytes = pack_weights_size(n, k)
+    buf = out if out is not None else torch.empty(nbytes, dtype=torch.int8, device=w.device)
+    _lib.call("w8a8_pack_weights", _ptr(w), n, k, w.stride(0), _ptr(buf), buf.numel(),
+              _stream(w.device))
+    return PackedWeights(buf, n, k)
+
+
+def gemm_packed(a, pw: PackedWeights, scale_a=None, scale_b=None, tensor_scale_a: float = 1.0,
+                tensor_scale_b: float = 1.0, out_dtype=None, out=None):
+    """gemm(a, w, ...) with w given as PackedWeights; a int8 [M, K] row-major."""
+    torch = _torch()
+    _require_cuda(a, pw.data, scale_a, scale_b)
+    out_dtype = out_dtype or torch.float16
+    m, k = a.shape
+    if k != pw.k:
+        raise ValueError(f"a has K={k}, packed weights K={pw.k}")
+    c = out if out is not None else torch.empty((m, pw.n), dtype=out_dtype, device=a.device)
+    otype = OUT_I32 if c.dtype == torch.int32 else OUT_F16
+    _lib.call("w8a8_gemm_packed", m, pw.n, k, _ptr(a), _ptr(pw.data), _ptr(c), a.stride(0),
+              c.stride(0), _ptr(scale_a), _ptr(scale_b), float(tensor_scale_a),
+              float(tensor_scale_b), otype, _stream(a.device))
+    return c
+
+
+def fused_sq_gemm_packed(x, smooth_scale, pw: PackedWeights, scale_w, out=None, q=None,
+                         row_scale=None):
+    """fused_sq_gemm with PackedWeights: returns (c fp16 [M, N], q, row_scale)."""
+    torch = _torch()
+    _require_cuda(x, smooth_scale, pw.data, scale_w)
+    m, k = x.shape
+    if k != pw.k:
+        raise ValueError(f"x has K={k}, packed weights K={pw.k}")
+    c = out if out is not None else torch.empty((m, pw.n), dtype=torch.float16, device=x.device)
+    q = q if q is not None else torch.empty((m, k), dtype=torch.int8, device=x.device)
+    r = row_scale if row_scale is not None else torch.empty(m, dtype=torch.float32,
+                                                            device=x.device)
+    _lib.call("w8a8_fused_sq_gemm_packed", _ptr(x), _ptr(smooth_scale), _ptr(pw.data),
+              _ptr(scale_w), _ptr(c), m, pw.n, k, x.stride(0), c.stride(0), _ptr(q), _ptr(r),
+              _stream(x.device))
+    return c, q, r

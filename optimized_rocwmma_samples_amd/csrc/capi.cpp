@@ -210,4 +210,71 @@ int w8a8_fused_sq_gemm(const void* x, const float* smooth_scale, const int8_t* w
                      W8A8_LAYOUT_A_ROW_B_NK, nullptr, 0, stream);
 }
 
+size_t w8a8_pack_weights_size(uint32_t n, uint32_t k)
+{
+    if(n == 0 || k == 0) return 0;
+    return w8a8::packed_weight_bytes(n, k);
+}
+
+int w8a8_pack_weights(const int8_t* w, uint32_t n, uint32_t k, uint32_t ldw, int8_t* packed,
+                      size_t packed_bytes, hipStream_t stream)
+{
+    if(!w || !packed) return fail(W8A8_ERROR_INVALID_VALUE, "w8a8_pack_weights: null pointer argument");
+    if(n == 0 || k == 0)
+        return fail(W8A8_ERROR_INVALID_VALUE, "w8a8_pack_weights: n and k must be > 0");
+    if(ldw == 0) ldw = k;
+    if(ldw < k)
+        return fail(W8A8_ERROR_INVALID_VALUE, "w8a8_pack_weights: ldw=%u smaller than k=%u", ldw, k);
+    const size_t need = w8a8::packed_weight_bytes(n, k);
+    if(packed_bytes < need)
+        return fail(W8A8_ERROR_INVALID_VALUE,
+                    "w8a8_pack_weights: packed buffer of %zu bytes, %zu needed", packed_bytes, need);
+    if(reinterpret_cast<uintptr_t>(packed) % 16 != 0)
+        return fail(W8A8_ERROR_INVALID_VALUE, "w8a8_pack_weights: packed must be 16-byte aligned");
+    return hip_status(w8a8::launch_pack_weights(w, n, k, ldw, packed, stream), "w8a8_pack_weights");
+}
+
+int w8a8_gemm_packed(uint32_t m, uint32_t n, uint32_t k, const int8_t* a,
+                     const int8_t* w_packed, void* c, uint32_t lda, uint32_t ldc,
+                     const float* scale_a, const float* scale_b, float tensor_scale_a,
+                     float tensor_scale_b, int out_type, hipStream_t stream)
+{
+    int rc = validate_gemm("w8a8_gemm_packed", m, n, k, a, w_packed, c, lda, k, ldc, out_type,
+                           W8A8_LAYOUT_A_ROW_B_NK);
+    if(rc != W8A8_SUCCESS) return rc;
+    if(reinterpret_cast<uintptr_t>(w_packed) % 16 != 0)
+        return fail(W8A8_ERROR_INVALID_VALUE, "w8a8_gemm_packed: w_packed must be 16-byte aligned");
+    w8a8::GemmArgs g{m, n, k, a, w_packed, c, lda, k, ldc, scale_a, scale_b,
+                     tensor_scale_a, tensor_scale_b, out_type};
+    if(!w8a8::gemm_packed_ok(g))
+        return fail(W8A8_ERROR_NOT_SUPPORTED,
+                    "w8a8_gemm_packed: needs 16-byte aligned A, lda %% 16 == 0, k %% 16 == 0 "
+                    "and A row panels under 2 GiB (m=%u lda=%u k=%u)", m, lda, k);
+    return hip_status(w8a8::launch_gemm_packed(g, stream), "w8a8_gemm_packed");
+}
+
+int w8a8_fused_sq_gemm_packed(const void* x, const float* smooth_scale, const int8_t* w_packed,
+                              const float* scale_w, void* c, uint32_t m, uint32_t n, uint32_t k,
+                              uint32_t ldx, uint32_t ldc, int8_t* q, float* row_scale,
+                              hipStream_t stream)
+{
+    if(!x || !smooth_scale || !w_packed || !scale_w || !c || !q || !row_scale)
+        return fail(W8A8_ERROR_INVALID_VALUE, "w8a8_fused_sq_gemm_packed: null pointer argument");
+    if(m == 0 || n == 0 || k == 0)
+        return fail(W8A8_ERROR_INVALID_VALUE, "w8a8_fused_sq_gemm_packed: m, n, k must be > 0");
+    if(ldx == 0) ldx = k;
+    if(ldc == 0) ldc = n;
+    if(ldx < k || ldc < n)
+        return fail(W8A8_ERROR_INVALID_VALUE,
+                    "w8a8_fused_sq_gemm_packed: ldx=%u must be >= k=%u and ldc=%u >= n=%u", ldx, k,
+                    ldc, n);
+    if(reinterpret_cast<uintptr_t>(q) % 16 != 0 || k % 16 != 0)
+        return fail(W8A8_ERROR_NOT_SUPPORTED,
+                    "w8a8_fused_sq_gemm_packed: needs a 16-byte aligned q and k %% 16 == 0 (k=%u)", k);
+    int rc = w8a8_smoothquant(x, smooth_scale, q, row_scale, m, k, 127.f, ldx, k, stream);
+    if(rc != W8A8_SUCCESS) return rc;
+    return w8a8_gemm_packed(m, n, k, q, w_packed, c, k, ldc, row_scale, scale_w, 1.f, 1.f,
+                            W8A8_OUT_F16, stream);
+}
+
 } // extern "C"

@@ -1,8 +1,12 @@
 // gemm_i8.hip -- launchers of the int8 GEMM: the gfx950 MFMA tile kernel
-// (gemm_i8_kernel.hpp), a generic strided kernel for shapes the tile kernel
-// does not take (k % 16 != 0, unaligned operands) and the repack used for the
-// reference sample's A col-major / B [K,N] layout.
+// (gemm_i8_kernel.hpp), the decode kernel for m <= 64 (gemm_i8_decode_kernel.hpp),
+// the packed-weight tile kernel (gemm_i8_pb_kernel.hpp), a generic strided
+// kernel for shapes the tile kernels do not take (k % 16 != 0, unaligned
+// operands) and the repack used for the reference sample's A col-major /
+// B [K,N] layout.
+#include "gemm_i8_decode_kernel.hpp"
 #include "gemm_i8_kernel.hpp"
+#include "gemm_i8_pb_kernel.hpp"
 #include "w8a8_internal.hpp"
 
 #include <algorithm>
@@ -16,6 +20,16 @@ using gemm::KArgs;
 
 // Production tile configuration.
 using GemmMain = gemm::Cfg<256, 256, 128, 2, 2, 4>;
+// Packed-weight tile configuration (m > kDecodeMaxM).
+using GemmPacked = gemm::PbCfg<256, 4, 2, 4>;
+// Decode configurations: <32-row m tiles, 32-row weight tiles, waves, ring>.
+using DecSmall   = gemm::DecCfg<1, 1, 4, 3>; // m <= 32, or <= 16 packed
+using DecSmallW  = gemm::DecCfg<1, 2, 8, 3>; // packed, 16 < m <= 32, many slabs
+using DecMid     = gemm::DecCfg<2, 1, 8, 3>; // 32 < m <= 64
+using DecMidW    = gemm::DecCfg<2, 2, 8, 2>; // packed, 32 < m <= 64, many slabs
+// A packed GEMM with at least this many 64-row slabs has enough blocks at
+// 64 rows per block to fill the chip; fewer slabs run 32 rows per block.
+constexpr uint32_t kWideSlabs = 384;
 
 // ---------------------------------------------------------------------------
 // Generic strided kernel: one thread per output, any layout / alignment.
@@ -66,22 +80,137 @@ KArgs make_kargs(const GemmArgs& g)
                  g.k,   g.lda, g.ldb, g.ldc,     g.tsa,     g.tsb};
 }
 
+int out_vec_ok(const GemmArgs& g)
+{
+    const size_t esz = g.out_type == W8A8_OUT_I32 ? 4 : 2;
+    return (reinterpret_cast<uintptr_t>(g.c) % (4 * esz) == 0) && (g.ldc % 4 == 0)
+           && (g.scale_b == nullptr || reinterpret_cast<uintptr_t>(g.scale_b) % 16 == 0);
+}
+
+// Sub-problem of rows [n0, n0 + nn) of the weights.  For packed weights n0 is
+// a multiple of the 64-row slab and b points at the slab's packed block.
+KArgs n_panel(const GemmArgs& g, uint32_t n0, uint32_t nn, bool packed)
+{
+    const size_t esz = g.out_type == W8A8_OUT_I32 ? 4 : 2;
+    KArgs        p   = make_kargs(g);
+    p.n              = nn;
+    p.b = packed ? g.b + (size_t)(n0 / gemm::kSlab) * gemm::packed_ktiles(g.k) * gemm::kPackFrags * 1024
+                 : g.b + (size_t)n0 * g.ldb;
+    p.c  = static_cast<int8_t*>(g.c) + (size_t)n0 * esz;
+    p.sb = g.scale_b ? g.scale_b + n0 : nullptr;
+    return p;
+}
+
+// Weight rows per launch so that every buffer resource stays under 2 GiB
+// (a multiple of the 64-row slab).
+uint32_t weight_panel_rows(const GemmArgs& g, bool packed)
+{
+    constexpr size_t kLimit = 0x7FFFFFFFull;
+    size_t           rows;
+    if(packed)
+        rows = kLimit / ((size_t)gemm::packed_ktiles(g.k) * gemm::kPackFrags * 1024) * gemm::kSlab;
+    else
+        rows = (kLimit - g.k) / g.ldb + 1;
+    rows = std::max<size_t>(gemm::kSlab, rows / gemm::kSlab * gemm::kSlab);
+    return (uint32_t)std::min<size_t>(g.n, rows);
+}
+
 } // namespace
+
+bool gemm_decode_ok(const GemmArgs& g)
+{
+    return g.m <= kDecodeMaxM && (uint64_t)(g.m - 1) * g.lda + g.k < 0x7FFFFFFFull;
+}
+
+hipError_t launch_gemm_decode(const GemmArgs& g, bool packed, hipStream_t stream)
+{
+    if(g.m == 0 || g.n == 0) return hipSuccess;
+    const int      vec_ok = out_vec_ok(g);
+    const uint32_t step   = weight_panel_rows(g, packed);
+    const bool     wide   = packed && gemm::packed_slabs(g.n) >= kWideSlabs;
+    for(uint32_t n0 = 0; n0 < g.n; n0 += step) {
+        const KArgs p = n_panel(g, n0, std::min(step, g.n - n0), packed);
+        hipError_t  e;
+        if(packed) {
+            if(g.m <= 16 || (g.m <= 32 && !wide))
+                e = gemm::launch_decode<DecSmall, true>(p, g.out_type, vec_ok, stream);
+            else if(g.m <= 32)
+                e = gemm::launch_decode<DecSmallW, true>(p, g.out_type, vec_ok, stream);
+            else if(!wide)
+                e = gemm::launch_decode<DecMid, true>(p, g.out_type, vec_ok, stream);
+            else
+                e = gemm::launch_decode<DecMidW, true>(p, g.out_type, vec_ok, stream);
+        } else {
+            if(g.m <= 32)
+                e = gemm::launch_decode<DecSmall, false>(p, g.out_type, vec_ok, stream);
+            else
+                e = gemm::launch_decode<DecMid, false>(p, g.out_type, vec_ok, stream);
+        }
+        if(e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_gemm_packed(const GemmArgs& g, hipStream_t stream)
+{
+    if(g.m == 0 || g.n == 0) return hipSuccess;
+    if(gemm_decode_ok(g)) return launch_gemm_decode(g, true, stream);
+    const size_t   esz    = g.out_type == W8A8_OUT_I32 ? 4 : 2;
+    const int      vec_ok = out_vec_ok(g);
+    constexpr size_t kLimit = 0x7FFFFFFFull;
+    const uint32_t mstep  = (uint32_t)std::min<size_t>(
+        g.m, std::max<size_t>(GemmPacked::kBM, kLimit / g.lda / GemmPacked::kBM * GemmPacked::kBM));
+    // the packed tile kernel's blocks cover 256 weight rows: keep panels aligned to that
+    const uint32_t nstep = std::max<uint32_t>(
+        GemmPacked::kBN, weight_panel_rows(g, true) / GemmPacked::kBN * GemmPacked::kBN);
+    for(uint32_t m0 = 0; m0 < g.m; m0 += mstep) {
+        for(uint32_t n0 = 0; n0 < g.n; n0 += nstep) {
+            KArgs p = n_panel(g, n0, std::min(nstep, g.n - n0), true);
+            p.m     = std::min(mstep, g.m - m0);
+            p.a     = g.a + (size_t)m0 * g.lda;
+            p.c     = static_cast<int8_t*>(p.c) + (size_t)m0 * g.ldc * esz;
+            p.sa    = g.scale_a ? g.scale_a + m0 : nullptr;
+            hipError_t e = gemm::launch_pb<GemmPacked>(p, g.out_type, vec_ok, stream);
+            if(e != hipSuccess) return e;
+        }
+    }
+    return hipSuccess;
+}
+
+size_t packed_weight_bytes(uint32_t n, uint32_t k) { return gemm::packed_bytes(n, k); }
+
+hipError_t launch_pack_weights(const int8_t* w, uint32_t n, uint32_t k, uint32_t ldw,
+                               int8_t* packed, hipStream_t stream)
+{
+    return gemm::launch_pack_weights(w, n, k, ldw, packed, stream);
+}
 
 bool gemm_fast_path_ok(const GemmArgs& g)
 {
+    // every launch addresses A and B panels of at least one tile of rows
+    // through buffer resources: a tile's rows must fit in 2 GiB
+    constexpr uint64_t kLimit = 0x7FFFFFFFull;
     return (reinterpret_cast<uintptr_t>(g.a) % 16 == 0)
            && (reinterpret_cast<uintptr_t>(g.b) % 16 == 0) && (g.lda % 16 == 0)
-           && (g.ldb % 16 == 0) && (g.k % 16 == 0);
+           && (g.ldb % 16 == 0) && (g.k % 16 == 0)
+           && (uint64_t)g.lda * GemmMain::kBM <= kLimit && (uint64_t)g.ldb * GemmMain::kBN <= kLimit;
+}
+
+bool gemm_packed_ok(const GemmArgs& g)
+{
+    constexpr uint64_t kLimit = 0x7FFFFFFFull;
+    if(reinterpret_cast<uintptr_t>(g.a) % 16 != 0 || g.lda % 16 != 0 || g.k % 16 != 0) return false;
+    // one packed k-row of a 64-row slab must fit in 2 GiB
+    if((uint64_t)gemm::packed_ktiles(g.k) * gemm::kPackFrags * 1024 > kLimit) return false;
+    return g.m <= kDecodeMaxM ? gemm_decode_ok(g) : (uint64_t)g.lda * GemmPacked::kBM <= kLimit;
 }
 
 hipError_t launch_gemm_nk(const GemmArgs& g, hipStream_t stream)
 {
     if(g.m == 0 || g.n == 0) return hipSuccess;
+    if(gemm_decode_ok(g)) return launch_gemm_decode(g, false, stream);
     const size_t esz    = g.out_type == W8A8_OUT_I32 ? 4 : 2;
-    const int    vec_ok = (reinterpret_cast<uintptr_t>(g.c) % (4 * esz) == 0) && (g.ldc % 4 == 0)
-                       && (g.scale_b == nullptr
-                           || reinterpret_cast<uintptr_t>(g.scale_b) % 16 == 0);
+    const int    vec_ok = out_vec_ok(g);
     // The tile kernel addresses each operand through a buffer resource whose
     // out-of-range offsets read as zero; keep every launch's A and B under
     // 2 GiB by splitting M and N into row panels (multiples of the tile).

@@ -43,8 +43,25 @@ struct GemmArgs {
 // A row-major [m,k], B [n,k] K-contiguous.  Fast path requirements (checked by
 // the caller through gemm_fast_path_ok): 16-byte aligned a/b, lda/ldb % 16 == 0,
 // k % 16 == 0.
+// Small m (decode) is routed to the decode kernel inside launch_gemm_nk.
 bool       gemm_fast_path_ok(const GemmArgs& g);
 hipError_t launch_gemm_nk(const GemmArgs& g, hipStream_t stream);
+
+// Decode kernel (m <= kDecodeMaxM): weights streamed once, split-K across the
+// waves of a block.  `packed`: g.b holds packed weights (g.ldb unused).
+constexpr uint32_t kDecodeMaxM = 64;
+bool       gemm_decode_ok(const GemmArgs& g);
+hipError_t launch_gemm_decode(const GemmArgs& g, bool packed, hipStream_t stream);
+
+// Packed weights: [n, k] int8 rearranged into MFMA register order, 64-row
+// slabs x 128-deep k-tiles of 8 KiB, zero padded (n to 64, k to 128).
+size_t     packed_weight_bytes(uint32_t n, uint32_t k);
+hipError_t launch_pack_weights(const int8_t* w, uint32_t n, uint32_t k, uint32_t ldw,
+                               int8_t* packed, hipStream_t stream);
+// GEMM over packed weights (g.ldb unused).  gemm_packed_ok: 16-byte aligned
+// A, lda % 16 == 0, k % 16 == 0 and every A panel addressable (< 2 GiB).
+bool       gemm_packed_ok(const GemmArgs& g);
+hipError_t launch_gemm_packed(const GemmArgs& g, hipStream_t stream);
 
 // Generic strided GEMM (any layout/alignment): A(m,k) = a[m*sam + k*sak],
 // B(n,k) = b[n*sbn + k*sbk].  Slow; used for odd shapes.

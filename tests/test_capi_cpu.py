@@ -124,6 +124,65 @@ def test_fused_validation(w8a8):
     assert rc == W.ERROR_INVALID_VALUE and "ldx" in msg
 
 
+def test_pack_weights_size(w8a8):
+    # 64-row slabs x 128-deep k-tiles of 8 KiB, zero padded
+    assert W.pack_weights_size(64, 128) == 8192
+    assert W.pack_weights_size(65, 129) == 2 * 2 * 8192
+    assert W.pack_weights_size(28672, 8192) == 28672 * 8192
+    assert W.pack_weights_size(0, 128) == 0
+
+
+def test_pack_weights_validation(w8a8):
+    rc, msg = _status("w8a8_pack_weights", None, 64, 128, 0, FAKE, 8192, None)
+    assert rc == W.ERROR_INVALID_VALUE and "null" in msg
+    rc, msg = _status("w8a8_pack_weights", FAKE, 64, 128, 100, FAKE, 8192, None)
+    assert rc == W.ERROR_INVALID_VALUE and "ldw" in msg
+    rc, msg = _status("w8a8_pack_weights", FAKE, 64, 128, 0, FAKE, 8191, None)
+    assert rc == W.ERROR_INVALID_VALUE and "needed" in msg
+    rc, msg = _status("w8a8_pack_weights", FAKE, 64, 128, 0, ctypes.c_void_p(0x1004), 8192, None)
+    assert rc == W.ERROR_INVALID_VALUE and "aligned" in msg
+
+
+def _packed_args(**kw):
+    base = dict(m=1, n=64, k=64, a=FAKE, w=FAKE, c=FAKE, lda=64, ldc=64, sa=None, sb=None,
+                tsa=1.0, tsb=1.0, out=W.OUT_F16, stream=None)
+    base.update(kw)
+    return list(base.values())
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(w=None), W.ERROR_INVALID_VALUE, "null"),
+    (dict(n=0), W.ERROR_INVALID_VALUE, "must be > 0"),
+    (dict(out=3), W.ERROR_INVALID_VALUE, "out_type"),
+    (dict(lda=32), W.ERROR_INVALID_VALUE, "lda"),
+    (dict(ldc=8), W.ERROR_INVALID_VALUE, "ldc"),
+    (dict(w=ctypes.c_void_p(0x1008)), W.ERROR_INVALID_VALUE, "aligned"),
+    (dict(k=40, lda=48), W.ERROR_NOT_SUPPORTED, "k % 16"),
+    (dict(lda=72), W.ERROR_NOT_SUPPORTED, "lda % 16"),
+    (dict(a=ctypes.c_void_p(0x1001)), W.ERROR_NOT_SUPPORTED, "aligned A"),
+    (dict(m=1000, lda=(1 << 23) + 16), W.ERROR_NOT_SUPPORTED, "2 GiB"),
+    (dict(m=64, lda=(1 << 26) + 16), W.ERROR_NOT_SUPPORTED, "2 GiB"),
+])
+def test_gemm_packed_validation(w8a8, kw, code, needle):
+    rc, msg = _status("w8a8_gemm_packed", *_packed_args(**kw))
+    assert rc == code and needle in msg, msg
+
+
+def test_fused_packed_validation(w8a8):
+    args = [FAKE, FAKE, FAKE, FAKE, FAKE, 4, 64, 64, 0, 0, FAKE, FAKE, None]
+    bad = list(args)
+    bad[3] = None
+    assert _status("w8a8_fused_sq_gemm_packed", *bad)[0] == W.ERROR_INVALID_VALUE
+    bad = list(args)
+    bad[8] = 32  # ldx < k
+    rc, msg = _status("w8a8_fused_sq_gemm_packed", *bad)
+    assert rc == W.ERROR_INVALID_VALUE and "ldx" in msg
+    bad = list(args)
+    bad[7] = 40  # k % 16 != 0
+    rc, msg = _status("w8a8_fused_sq_gemm_packed", *bad)
+    assert rc == W.ERROR_NOT_SUPPORTED and "k % 16" in msg
+
+
 def test_python_layer_raises_w8a8error(w8a8):
     with pytest.raises(W.W8A8Error) as ei:
         _lib.call("w8a8_smoothquant", None, None, None, None, 1, 1, 127.0, 0, 0, None)
