@@ -200,6 +200,31 @@ def bench_decode(torch, w8a8, dev, gen, iters=20):
                         "rotated over 940 MB)", "layers": results}
 
 
+TRAFFIC_PROFILE = ROOT / "profiles" / "gemm_i8_tile_kernel__cfg3_llama3_8b_m8192_and_cfg2.md"
+
+
+def profiled_traffic(projs):
+    """HBM-side bytes per launch of the projection GEMMs, averaged like
+    `achieved`, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+    (scaled by the calibration copy); None when the profile does not cover
+    these grids."""
+    import re
+    if not TRAFFIC_PROFILE.exists():
+        return None, None
+    table = {}
+    for line in TRAFFIC_PROFILE.read_text().splitlines():
+        mt = re.match(r"traffic \S*gemm_i8_tile_kernel\S* grid=(\d+) .* bytes=(\d+)", line)
+        if mt:
+            table[int(mt.group(1))] = int(mt.group(2))
+    per = []
+    for p in projs:
+        grid = -(-p["m"] // 256) * -(-p["n"] // 256) * 512  # 256x256 tiles, 512 threads
+        if grid not in table:
+            return None, None
+        per.append(table[grid])
+    return sum(per) / len(per), per
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
@@ -284,8 +309,16 @@ def main(argv=None) -> int:
                          "gemm_TOPS": ops / (gm * 1e-3) / 1e12})
     log(json.dumps(per_proj))
 
+    traffic, traffic_per = profiled_traffic(projs)
+    algo_bytes = [p["m"] * p["k"] + p["n"] * p["k"] + 2 * p["m"] * p["n"] + 4 * (p["m"] + p["n"])
+                  for p in projs]
     roofline = {"bound": "mfma", "achieved": gemm_tops, "peak": PEAK_INT8_OPS / 1e12,
-                "unit": "TFLOP/s", "frac": gemm_tops * 1e12 / PEAK_INT8_OPS, "traffic": None,
+                "unit": "TFLOP/s", "frac": gemm_tops * 1e12 / PEAK_INT8_OPS, "traffic": traffic,
+                "traffic_per_projection": traffic_per,
+                "algorithmic_bytes_per_projection": algo_bytes,
+                "traffic_source": (f"{TRAFFIC_PROFILE.relative_to(ROOT)} (rocprofv3 FETCH_SIZE x2.0 "
+                                   "+ WRITE_SIZE x1.0, calibrated on a 2^30-byte copy; "
+                                   "FETCH_SIZE includes MALL hits)") if traffic else None,
                 "kernel": "gemm_i8_tile_kernel<Cfg<256,256,128,2,2,4>, F16>",
                 "avg_launch_us": gemm_avg_us,
                 "note": "int8 ops (2*M*N*K) per launch / average launch duration over the four "

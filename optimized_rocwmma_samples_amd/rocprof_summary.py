@@ -2,6 +2,13 @@
 
     python -m optimized_rocwmma_samples_amd.rocprof_summary trace DIR        # kernel trace
     python -m optimized_rocwmma_samples_amd.rocprof_summary pmc DIR [DIR..]  # counters
+    python -m optimized_rocwmma_samples_amd.rocprof_summary traffic FETCH_DIR WRITE_DIR
+
+`traffic` turns FETCH_SIZE and WRITE_SIZE (KiB per dispatch, one run each) into
+bytes per dispatch, scaled by what the same counters read for the calibration
+copy that `bench.py --calibrate-copy` runs (torch neg over 2^30 int8: 2^30
+bytes read, 2^30 bytes written).  Output lines:
+    traffic <kernel> grid=<g> fetch_kib=<f> write_kib=<w> bytes=<scaled total>
 
 Groups dispatches by (kernel, grid size) so the four projection GEMMs of one
 bench step appear as separate rows, and prints per-dispatch averages.
@@ -62,14 +69,59 @@ def pmc(directories: list[str], match: str = "w8a8|gemm|sq_|neg") -> str:
     return "\n".join(out)
 
 
+CALIB_BYTES = 1 << 30
+CALIB_KERNEL = "neg_kernel"
+
+
+def _counter_avgs(directory: str, counter: str):
+    vals = defaultdict(list)
+    for r in _rows(os.path.join(directory, "**", "*counter_collection.csv")):
+        if r["Counter_Name"] != counter:
+            continue
+        name = r.get("Kernel_Name", "")
+        vals[(short_name(name), r.get("Grid_Size", "?"), name)].append(float(r["Counter_Value"]))
+    return {k: sum(v) / len(v) for k, v in vals.items()}
+
+
+def traffic(fetch_dir: str, write_dir: str, match: str = "w8a8|gemm|sq_") -> str:
+    fetch = _counter_avgs(fetch_dir, "FETCH_SIZE")
+    write = _counter_avgs(write_dir, "WRITE_SIZE")
+
+    def calib(vals):
+        # the calibration copy is the only elementwise launch over 2^30 elements
+        cands = [v for (n, g, full), v in vals.items()
+                 if CALIB_KERNEL in full and "elementwise" in full]
+        if not cands:
+            raise SystemExit("calibration copy not found (run bench.py --calibrate-copy)")
+        return CALIB_BYTES / (cands[0] * 1024)
+
+    ff, wf = calib(fetch), calib(write)
+    out = [f"calibration fetch_factor={ff:.4f} write_factor={wf:.4f} "
+           f"(torch neg over 2^30 int8 elements)"]
+    wkeys = {(n, g): v for (n, g, _), v in write.items()}
+    for (name, grid, full), f in sorted(fetch.items()):
+        if not re.search(match, full):
+            continue
+        w = wkeys.get((name, grid), 0.0)
+        total = (f * ff + w * wf) * 1024
+        out.append(f"traffic {name.replace(' ', '')} grid={grid} fetch_kib={f:.1f} "
+                   f"write_kib={w:.1f} bytes={total:.0f}")
+    return "\n".join(out)
+
+
 def main(argv: list[str]) -> int:
-    if len(argv) < 2 or argv[0] not in ("trace", "pmc"):
+    if len(argv) < 2 or argv[0] not in ("trace", "pmc", "traffic"):
         print(__doc__)
         return 2
     if argv[0] == "trace":
         print(trace(argv[1]))
-    else:
+    elif argv[0] == "pmc":
         print(pmc(argv[1:]))
+    else:
+        if len(argv) != 3:
+            print(__doc__)
+            return 2
+        print(traffic(argv[1], argv[2]))
     return 0
 
 
