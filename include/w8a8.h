@@ -171,6 +171,119 @@ int w8a8_fused_sq_gemm_packed(const void* x, const float* smooth_scale, const in
                               uint32_t ldx, uint32_t ldc, int8_t* q, float* row_scale,
                               hipStream_t stream);
 
+/* ------------------------------------------------------------------------- */
+/* Grouped GEMM and MoE                                                       */
+/* ------------------------------------------------------------------------- */
+
+/*
+ * One problem of a grouped GEMM: the fields of w8a8_gemm for the
+ * W8A8_LAYOUT_A_ROW_B_NK layout.  Mirrors GroupDesc
+ * (rocwmma_grouped_gemm.cpp:87-96: A, B, C, M, N, K, lda, ldb, ldc) plus the
+ * dequant scales.  A group with m == 0 contributes nothing.
+ */
+typedef struct w8a8_group_desc {
+    const int8_t* a;       /* [m, lda] */
+    const int8_t* b;       /* [n, ldb] */
+    void*         c;       /* [m, ldc] int32 or fp16 (per out_type) */
+    const float*  scale_a; /* [m] or NULL */
+    const float*  scale_b; /* [n] or NULL */
+    uint32_t      m, n, k;
+    uint32_t      lda, ldb, ldc;
+    float         tensor_scale_a, tensor_scale_b;
+} w8a8_group_desc;
+
+/* Device workspace w8a8_grouped_gemm needs for num_groups descriptors. */
+size_t w8a8_grouped_gemm_workspace_size(uint32_t num_groups);
+
+/*
+ * Runs every group's w8a8_gemm in one launch.  Replaces grouped_gemm_kernel
+ * (rocwmma_grouped_gemm.cpp:104-178), whose host code uploads the descriptor
+ * array with a tile_offset prefix in it (:180-226): here `groups` is a HOST array,
+ * validated, then copied into `workspace` (hipMemcpyAsync on `stream`; the
+ * host array may be reused when the call returns).  Every group needs the
+ * fast-path layout (16-byte aligned a/b, lda, ldb, k multiples of 16) and
+ * m*lda, n*ldb < 2^31 (W8A8_ERROR_NOT_SUPPORTED otherwise).
+ */
+int w8a8_grouped_gemm(const w8a8_group_desc* groups, uint32_t num_groups, int out_type,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Softmax + top-k routing.  Replaces kernel_topk_softmax /
+ * kernel_topk_softmax_large (rocwmma_topk_softmax.cpp:58-193).
+ *   logits  [tokens, experts], fp32 (logits_f16 = 0) or fp16 (logits_f16 = 1;
+ *           the reference's input type, :42)
+ *   topk_weights fp32 [tokens, topk] = softmax probability of each choice
+ *   topk_ids     int32 [tokens, topk], best first; ties go to the lower id.
+ * experts <= 4096, topk <= experts (the reference caps at 64 experts, :172).
+ */
+int w8a8_topk_softmax(const void* logits, int logits_f16, float* topk_weights,
+                      int32_t* topk_ids, uint32_t tokens, uint32_t experts, uint32_t topk,
+                      hipStream_t stream);
+
+/* Entries w8a8_moe_sort needs in sorted_token_ids: tokens*topk + experts*unit_size
+ * (the reference's bound, rocwmma_moe_sorting.cpp:161). */
+size_t w8a8_moe_sort_capacity(uint32_t tokens, uint32_t topk, uint32_t experts,
+                              uint32_t unit_size);
+
+/*
+ * Sorts the (token, slot) pairs by expert.  Replaces kernel_moe_histogram,
+ * kernel_prefix_sum and kernel_moe_scatter (rocwmma_moe_sorting.cpp:53-125)
+ * with the same outputs, made deterministic: inside an expert, pairs keep
+ * ascending order of t*topk + slot.
+ *   expert_count [E], expert_start [E+1] (expert_start[E] = padded total),
+ *   padded_count [E] (count rounded up to unit_size), sorted_token_ids
+ *   [sorted_capacity] (token of each sorted row, -1 in padding), dst_row
+ *   [tokens*topk] (sorted row of each pair, -1 for an id outside [0, E)).
+ * experts <= 1024.  One launch; no memset needed before it.
+ */
+int w8a8_moe_sort(const int32_t* topk_ids, uint32_t tokens, uint32_t topk, uint32_t experts,
+                  uint32_t unit_size, int32_t* expert_count, int32_t* expert_start,
+                  int32_t* padded_count, int32_t* sorted_token_ids, uint32_t sorted_capacity,
+                  int32_t* dst_row, hipStream_t stream);
+
+/*
+ * Expert GEMM over expert-sorted rows (the per-expert GEMMs of
+ * moe_gate_up_silu_kernel, rocwmma_fused_moe.cpp:96-158, as one grouped
+ * launch).  Expert e multiplies rows [expert_start[e], expert_start[e] +
+ * expert_count[e]) of a (int8 [rows, lda]) by its weights
+ * w + e*w_expert_stride (int8 [n, ldw]) into the same rows of c, with
+ *   c = half((float(acc) * scale_a[row]) * scale_w[e*n + col])
+ * (NULL vectors fall back to the tensor scales, as in w8a8_gemm).  The
+ * per-expert arrays are read on the device (the output of w8a8_moe_sort), so
+ * nothing is synchronized with the host; rows outside [0, rows) are never
+ * touched, whatever the arrays hold.
+ */
+int w8a8_moe_gemm(uint32_t experts, uint32_t rows, uint32_t n, uint32_t k, const int8_t* a,
+                  uint32_t lda, const int8_t* w, uint32_t ldw, uint64_t w_expert_stride, void* c,
+                  uint32_t ldc, const float* scale_a, const float* scale_w,
+                  float tensor_scale_a, float tensor_scale_b, const int32_t* expert_start,
+                  const int32_t* expert_count, int out_type, hipStream_t stream);
+
+/*
+ * SiLU(gate) * up requantization between the expert GEMMs: row r of
+ * gate_up (fp16 [rows, ld_gu], gate = columns [0, inter), up = [inter, 2*inter))
+ * gives a = (g / (1 + exp(-g))) * u [* smooth_scale[e*inter + j]] and the
+ * SmoothQuant absmax quantization of a into q (int8 [rows, ldq]) and
+ * row_scale [rows].  Only rows inside some expert's [start, start + count)
+ * are written.  The reference applies SiLU to every output instead
+ * (rocwmma_fused_moe.cpp:153-156); this is the gate*up form.  inter <= 32768.
+ */
+int w8a8_moe_silu_mul_quant(const void* gate_up, uint32_t ld_gu, const float* smooth_scale,
+                            const int32_t* expert_start, const int32_t* expert_count,
+                            uint32_t experts, uint32_t rows, uint32_t inter, int8_t* q,
+                            uint32_t ldq, float* row_scale, float quant_max, hipStream_t stream);
+
+/*
+ * Weighted combine back to token order:
+ *   out[t, j] = half(sum over slots s (ascending) of
+ *                    fma(topk_weights[t, s], float(y[dst_row[t*topk + s], j]), acc))
+ * y fp16 [rows_y, ldy] (expert-sorted rows), out fp16 [tokens, ldo]; pairs
+ * with dst_row outside [0, rows_y) are skipped.
+ */
+int w8a8_moe_combine(const void* y, uint32_t ldy, uint32_t rows_y, const float* topk_weights,
+                     const int32_t* dst_row, uint32_t tokens, uint32_t topk, uint32_t n,
+                     void* out, uint32_t ldo, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -10,6 +10,13 @@ The functions mirror the reference kernels this path replaces:
   moe_smoothquant  <- kernel_moe_smoothquant  (rocwmma_moe_smoothquant.cpp:69-131)
   gemm             <- gemm_quant_tensor_scale (rocwmma_gemm_quantized.cpp:127-195), Mode 2
   fused_sq_gemm    <- smoothquant feeding gemm, one call
+  pack_weights / gemm_packed / fused_sq_gemm_packed
+                   <- the pre-shuffled weights of flatmm (rocwmma_flatmm.cpp:12-16)
+  grouped_gemm     <- grouped_gemm_kernel     (rocwmma_grouped_gemm.cpp:104-178)
+  topk_softmax     <- kernel_topk_softmax     (rocwmma_topk_softmax.cpp:58-193)
+  moe_sort         <- kernel_moe_histogram/prefix_sum/scatter (rocwmma_moe_sorting.cpp:53-125)
+  moe_gemm, moe_silu_mul_quant, moe_combine, moe_ffn
+                   <- the expert FFN chain (rocwmma_fused_moe.cpp:96-211), gate*up form
 """
 from __future__ import annotations
 
@@ -26,7 +33,9 @@ from ._lib import (  # noqa: F401
 
 __all__ = [
     "library", "version", "smoothquant", "moe_smoothquant", "gemm", "gemm_workspace_size",
-    "fused_sq_gemm", "W8A8Error",
+    "fused_sq_gemm", "W8A8Error", "PackedWeights", "pack_weights", "pack_weights_size",
+    "gemm_packed", "fused_sq_gemm_packed", "grouped_gemm", "topk_softmax", "moe_sort",
+    "moe_gemm", "moe_silu_mul_quant", "moe_combine", "moe_ffn",
 ]
 
 
@@ -94,7 +103,7 @@ def moe_smoothquant(x, smooth_scale, topk_ids, quant_max: float = 127.0, dst_row
     tokens, hidden = x.shape
     experts = smooth_scale.shape[0]
     topk = topk_ids.shape[1]
-    nrows = rows if rows is not None else tokens * topk
+    nrows = rows if rows is not None else (out.shape[0] if out is not None else tokens * topk)
     q = out if out is not None else torch.empty((nrows, hidden), dtype=torch.int8,
                                                 device=x.device)
     r = row_scale if row_scale is not None else torch.empty(nrows, dtype=torch.float32,
@@ -227,3 +236,133 @@ def fused_sq_gemm_packed(x, smooth_scale, pw: PackedWeights, scale_w, out=None, 
               _ptr(scale_w), _ptr(c), m, pw.n, k, x.stride(0), c.stride(0), _ptr(q), _ptr(r),
               _stream(x.device))
     return c, q, r
+
+
+def grouped_gemm(problems, out_dtype=None, outs=None):
+    """One launch for several GEMMs.  problems: list of (a, b, scale_a, scale_b)
+    with a int8 [M_g, K_g], b int8 [N_g, K_g] (scales may be None).  Returns the
+    list of outputs (out_dtype torch.float16 or torch.int32)."""
+    torch = _torch()
+    out_dtype = out_dtype or torch.float16
+    descs = (_lib.GroupDesc * len(problems))()
+    results = []
+    dev = None
+    for i, (a, b, sa, sb) in enumerate(problems):
+        _require_cuda(a, b, sa, sb)
+        dev = a.device
+        m, k = a.shape
+        n = b.shape[0]
+        c = outs[i] if outs is not None else torch.empty((m, n), dtype=out_dtype, device=dev)
+        results.append(c)
+        descs[i] = _lib.GroupDesc(a.data_ptr(), b.data_ptr(), c.data_ptr(), _ptr(sa), _ptr(sb),
+                                  m, n, k, a.stride(0), b.stride(0), c.stride(0), 1.0, 1.0)
+    otype = OUT_I32 if results[0].dtype == torch.int32 else OUT_F16
+    ws_bytes = int(library().w8a8_grouped_gemm_workspace_size(len(problems)))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    # the call stages the host descriptors before it returns; the workspace is
+    # freed through torch's caching allocator, which orders reuse on the stream
+    _lib.call("w8a8_grouped_gemm", descs, len(problems), otype, _ptr(ws), ws_bytes, _stream(dev))
+    return results
+
+
+def topk_softmax(logits, topk: int):
+    """logits fp32 or fp16 [T, E] -> (weights fp32 [T, topk], ids int32 [T, topk])."""
+    torch = _torch()
+    _require_cuda(logits)
+    logits = logits.contiguous()
+    t, e = logits.shape
+    w = torch.empty((t, topk), dtype=torch.float32, device=logits.device)
+    ids = torch.empty((t, topk), dtype=torch.int32, device=logits.device)
+    _lib.call("w8a8_topk_softmax", _ptr(logits), 1 if logits.dtype == torch.float16 else 0,
+              _ptr(w), _ptr(ids), t, e, topk, _stream(logits.device))
+    return w, ids
+
+
+def moe_sort(topk_ids, experts: int, unit_size: int = 32):
+    """Stable expert sort of topk_ids int32 [T, k].  Returns a dict with
+    count [E], start [E+1], padded [E], sorted_ids [capacity], dst_row [T*k]."""
+    torch = _torch()
+    _require_cuda(topk_ids)
+    ids = topk_ids.contiguous()
+    t, k = ids.shape
+    cap = int(library().w8a8_moe_sort_capacity(t, k, experts, unit_size))
+    d = ids.device
+    out = dict(count=torch.empty(experts, dtype=torch.int32, device=d),
+               start=torch.empty(experts + 1, dtype=torch.int32, device=d),
+               padded=torch.empty(experts, dtype=torch.int32, device=d),
+               sorted_ids=torch.empty(cap, dtype=torch.int32, device=d),
+               dst_row=torch.empty(t * k, dtype=torch.int32, device=d))
+    _lib.call("w8a8_moe_sort", _ptr(ids), t, k, experts, unit_size, _ptr(out["count"]),
+              _ptr(out["start"]), _ptr(out["padded"]), _ptr(out["sorted_ids"]), cap,
+              _ptr(out["dst_row"]), _stream(d))
+    return out
+
+
+def moe_gemm(a, w, expert_start, expert_count, scale_a=None, scale_w=None, out_dtype=None,
+             out=None, tensor_scale_a: float = 1.0, tensor_scale_b: float = 1.0):
+    """Expert GEMM over expert-sorted rows: a int8 [rows, K], w int8 [E, N, K]."""
+    torch = _torch()
+    _require_cuda(a, w, expert_start, expert_count, scale_a, scale_w)
+    out_dtype = out_dtype or torch.float16
+    rows, k = a.shape
+    e, n, kw = w.shape
+    if kw != k:
+        raise ValueError(f"a has K={k}, weights K={kw}")
+    c = out if out is not None else torch.empty((rows, n), dtype=out_dtype, device=a.device)
+    otype = OUT_I32 if c.dtype == torch.int32 else OUT_F16
+    _lib.call("w8a8_moe_gemm", e, rows, n, k, _ptr(a), a.stride(0), _ptr(w), w.stride(1),
+              w.stride(0), _ptr(c), c.stride(0), _ptr(scale_a), _ptr(scale_w),
+              float(tensor_scale_a), float(tensor_scale_b), _ptr(expert_start),
+              _ptr(expert_count), otype, _stream(a.device))
+    return c
+
+
+def moe_silu_mul_quant(gate_up, expert_start, expert_count, smooth_scale=None,
+                       quant_max: float = 127.0, q=None, row_scale=None):
+    """gate_up fp16 [rows, 2*inter] -> (q int8 [rows, inter], row_scale fp32 [rows])."""
+    torch = _torch()
+    _require_cuda(gate_up, expert_start, expert_count, smooth_scale)
+    rows, two_i = gate_up.shape
+    inter = two_i // 2
+    experts = expert_count.numel()
+    q = q if q is not None else torch.empty((rows, inter), dtype=torch.int8, device=gate_up.device)
+    r = row_scale if row_scale is not None else torch.empty(rows, dtype=torch.float32,
+                                                            device=gate_up.device)
+    _lib.call("w8a8_moe_silu_mul_quant", _ptr(gate_up), gate_up.stride(0), _ptr(smooth_scale),
+              _ptr(expert_start), _ptr(expert_count), experts, rows, inter, _ptr(q), q.stride(0),
+              _ptr(r), float(quant_max), _stream(gate_up.device))
+    return q, r
+
+
+def moe_combine(y, topk_weights, dst_row, out=None):
+    """y fp16 [rows, N] (expert-sorted) -> out fp16 [T, N] = sum_k w * y[dst_row]."""
+    torch = _torch()
+    _require_cuda(y, topk_weights, dst_row)
+    t, k = topk_weights.shape
+    rows, n = y.shape
+    o = out if out is not None else torch.empty((t, n), dtype=torch.float16, device=y.device)
+    _lib.call("w8a8_moe_combine", _ptr(y), y.stride(0), rows, _ptr(topk_weights.contiguous()),
+              _ptr(dst_row), t, k, n, _ptr(o), o.stride(0), _stream(y.device))
+    return o
+
+
+def moe_ffn(x, logits, smooth_scale, w_gate_up, sb_gate_up, w_down, sb_down, topk: int,
+            smooth_scale_down=None, unit_size: int = 32):
+    """Whole expert FFN on one GPU, nine launches, no host synchronization:
+    top-k routing, stable expert sort, MoE SmoothQuant straight into the
+    expert-sorted rows, gate_up expert GEMM, SiLU(gate)*up requantization,
+    down expert GEMM, weighted combine.  Returns (out fp16 [T, H], parts)."""
+    torch = _torch()
+    t, h = x.shape
+    e = w_gate_up.shape[0]
+    w, ids = topk_softmax(logits, topk)
+    srt = moe_sort(ids, e, unit_size)
+    rows = srt["sorted_ids"].numel()
+    qa = torch.empty((rows, h), dtype=torch.int8, device=x.device)
+    ra = torch.empty(rows, dtype=torch.float32, device=x.device)
+    moe_smoothquant(x, smooth_scale, ids, dst_row=srt["dst_row"], rows=rows, out=qa, row_scale=ra)
+    gu = moe_gemm(qa, w_gate_up, srt["start"], srt["count"], ra, sb_gate_up)
+    q2, r2 = moe_silu_mul_quant(gu, srt["start"], srt["count"], smooth_scale_down)
+    y = moe_gemm(q2, w_down, srt["start"], srt["count"], r2, sb_down)
+    out = moe_combine(y, w, srt["dst_row"])
+    return out, dict(weights=w, ids=ids, sort=srt, qa=qa, ra=ra, gate_up=gu, q2=q2, r2=r2, y=y)

@@ -27,6 +27,17 @@ _i32 = ctypes.c_int
 _f32 = ctypes.c_float
 _ptr = ctypes.c_void_p
 _size = ctypes.c_size_t
+_u64 = ctypes.c_uint64
+
+
+class GroupDesc(ctypes.Structure):
+    """w8a8_group_desc (include/w8a8.h)."""
+    _fields_ = [("a", ctypes.c_void_p), ("b", ctypes.c_void_p), ("c", ctypes.c_void_p),
+                ("scale_a", ctypes.c_void_p), ("scale_b", ctypes.c_void_p),
+                ("m", ctypes.c_uint32), ("n", ctypes.c_uint32), ("k", ctypes.c_uint32),
+                ("lda", ctypes.c_uint32), ("ldb", ctypes.c_uint32), ("ldc", ctypes.c_uint32),
+                ("tensor_scale_a", ctypes.c_float), ("tensor_scale_b", ctypes.c_float)]
+
 
 # name -> (restype, argtypes); mirrors include/w8a8.h
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
@@ -46,6 +57,18 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                 _f32, _i32, _ptr]),
     "w8a8_fused_sq_gemm_packed": (_i32, [_ptr, _ptr, _ptr, _ptr, _ptr, _u32, _u32, _u32, _u32,
                                          _u32, _ptr, _ptr, _ptr]),
+    "w8a8_grouped_gemm_workspace_size": (_size, [_u32]),
+    "w8a8_grouped_gemm": (_i32, [ctypes.POINTER(GroupDesc), _u32, _i32, _ptr, _size, _ptr]),
+    "w8a8_topk_softmax": (_i32, [_ptr, _i32, _ptr, _ptr, _u32, _u32, _u32, _ptr]),
+    "w8a8_moe_sort_capacity": (_size, [_u32, _u32, _u32, _u32]),
+    "w8a8_moe_sort": (_i32, [_ptr, _u32, _u32, _u32, _u32, _ptr, _ptr, _ptr, _ptr, _u32, _ptr,
+                             _ptr]),
+    "w8a8_moe_gemm": (_i32, [_u32, _u32, _u32, _u32, _ptr, _u32, _ptr, _u32, _u64, _ptr, _u32,
+                             _ptr, _ptr, _f32, _f32, _ptr, _ptr, _i32, _ptr]),
+    "w8a8_moe_silu_mul_quant": (_i32, [_ptr, _u32, _ptr, _ptr, _ptr, _u32, _u32, _u32, _ptr, _u32,
+                                       _ptr, _f32, _ptr]),
+    "w8a8_moe_combine": (_i32, [_ptr, _u32, _u32, _ptr, _ptr, _u32, _u32, _u32, _ptr, _u32,
+                                _ptr]),
 }
 
 

@@ -36,6 +36,7 @@ SOURCES = [
     "capi.cpp",
     "smoothquant.hip",
     "gemm_i8.hip",
+    "moe.hip",
 ]
 
 # -packed-fp32-ops: keep the compiler from emitting packed fp32 VALU ops.

@@ -8,6 +8,7 @@
 
 #include <cmath>
 #include <cstdarg>
+#include <vector>
 #include <cstdio>
 #include <cstring>
 
@@ -275,6 +276,186 @@ int w8a8_fused_sq_gemm_packed(const void* x, const float* smooth_scale, const in
     if(rc != W8A8_SUCCESS) return rc;
     return w8a8_gemm_packed(m, n, k, q, w_packed, c, k, ldc, row_scale, scale_w, 1.f, 1.f,
                             W8A8_OUT_F16, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Grouped GEMM and MoE
+// ---------------------------------------------------------------------------
+
+size_t w8a8_grouped_gemm_workspace_size(uint32_t num_groups)
+{
+    return ((size_t)num_groups * sizeof(w8a8_group_desc) + 255) / 256 * 256;
+}
+
+int w8a8_grouped_gemm(const w8a8_group_desc* groups, uint32_t num_groups, int out_type,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream)
+{
+    const char* fn = "w8a8_grouped_gemm";
+    if(!groups || num_groups == 0) return fail(W8A8_ERROR_INVALID_VALUE, "%s: no groups", fn);
+    if(out_type != W8A8_OUT_I32 && out_type != W8A8_OUT_F16)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: unknown out_type %d", fn, out_type);
+    if(!workspace || workspace_bytes < w8a8_grouped_gemm_workspace_size(num_groups))
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: workspace of %zu bytes, %zu needed", fn,
+                    workspace_bytes, w8a8_grouped_gemm_workspace_size(num_groups));
+    if(reinterpret_cast<uintptr_t>(workspace) % 64 != 0)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: workspace must be 64-byte aligned", fn);
+    uint64_t   tiles  = 0;
+    int        vec_ok = 1;
+    const size_t esz  = out_type == W8A8_OUT_I32 ? 4 : 2;
+    for(uint32_t i = 0; i < num_groups; ++i) {
+        const w8a8_group_desc& d = groups[i];
+        if(d.m == 0) continue;
+        if(!d.a || !d.b || !d.c)
+            return fail(W8A8_ERROR_INVALID_VALUE, "%s: group %u: null pointer", fn, i);
+        if(d.n == 0 || d.k == 0)
+            return fail(W8A8_ERROR_INVALID_VALUE, "%s: group %u: n and k must be > 0", fn, i);
+        if(d.lda < d.k || d.ldb < d.k || d.ldc < d.n)
+            return fail(W8A8_ERROR_INVALID_VALUE,
+                        "%s: group %u: lda=%u ldb=%u must be >= k=%u and ldc=%u >= n=%u", fn, i,
+                        d.lda, d.ldb, d.k, d.ldc, d.n);
+        if(reinterpret_cast<uintptr_t>(d.a) % 16 || reinterpret_cast<uintptr_t>(d.b) % 16
+           || d.lda % 16 || d.ldb % 16 || d.k % 16)
+            return fail(W8A8_ERROR_NOT_SUPPORTED,
+                        "%s: group %u: needs 16-byte aligned a/b and lda, ldb, k %% 16 == 0", fn, i);
+        if((uint64_t)d.m * d.lda > 0x7FFFFFFFull || (uint64_t)d.n * d.ldb > 0x7FFFFFFFull)
+            return fail(W8A8_ERROR_NOT_SUPPORTED, "%s: group %u: operand over 2 GiB", fn, i);
+        vec_ok = vec_ok && reinterpret_cast<uintptr_t>(d.c) % (4 * esz) == 0 && d.ldc % 4 == 0
+                 && (d.scale_b == nullptr || reinterpret_cast<uintptr_t>(d.scale_b) % 16 == 0);
+        tiles += w8a8::grouped_gemm_tiles(d.m, d.n);
+    }
+    if(tiles > 0x7FFFFFFFull) return fail(W8A8_ERROR_NOT_SUPPORTED, "%s: too many tiles", fn);
+    if(tiles == 0) return hip_status(hipSuccess, fn);
+    hipError_t e = hipMemcpyAsync(workspace, groups, (size_t)num_groups * sizeof(w8a8_group_desc),
+                                  hipMemcpyHostToDevice, stream);
+    if(e == hipSuccess)
+        e = w8a8::launch_grouped_gemm(static_cast<const w8a8_group_desc*>(workspace), num_groups,
+                                      (uint32_t)tiles, out_type, vec_ok, stream);
+    return hip_status(e, fn);
+}
+
+int w8a8_topk_softmax(const void* logits, int logits_f16, float* topk_weights,
+                      int32_t* topk_ids, uint32_t tokens, uint32_t experts, uint32_t topk,
+                      hipStream_t stream)
+{
+    const char* fn = "w8a8_topk_softmax";
+    if(!logits || !topk_weights || !topk_ids)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: null pointer argument", fn);
+    if(tokens == 0 || experts == 0 || topk == 0)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: tokens, experts and topk must be > 0", fn);
+    if(experts > 4096 || topk > experts)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: need topk <= experts <= 4096 (topk=%u experts=%u)",
+                    fn, topk, experts);
+    if(logits_f16 != 0 && logits_f16 != 1)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: logits_f16 must be 0 or 1", fn);
+    return hip_status(w8a8::launch_topk_softmax(logits, logits_f16 == 1, topk_weights, topk_ids,
+                                                tokens, experts, topk, stream),
+                      fn);
+}
+
+size_t w8a8_moe_sort_capacity(uint32_t tokens, uint32_t topk, uint32_t experts, uint32_t unit_size)
+{
+    return (size_t)tokens * topk + (size_t)experts * unit_size;
+}
+
+int w8a8_moe_sort(const int32_t* topk_ids, uint32_t tokens, uint32_t topk, uint32_t experts,
+                  uint32_t unit_size, int32_t* expert_count, int32_t* expert_start,
+                  int32_t* padded_count, int32_t* sorted_token_ids, uint32_t sorted_capacity,
+                  int32_t* dst_row, hipStream_t stream)
+{
+    const char* fn = "w8a8_moe_sort";
+    if(!topk_ids || !expert_count || !expert_start || !padded_count || !sorted_token_ids
+       || !dst_row)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: null pointer argument", fn);
+    if(tokens == 0 || topk == 0 || experts == 0 || unit_size == 0)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: tokens, topk, experts, unit_size must be > 0",
+                    fn);
+    if(experts > 1024) return fail(W8A8_ERROR_INVALID_VALUE, "%s: experts=%u > 1024", fn, experts);
+    const size_t need = w8a8_moe_sort_capacity(tokens, topk, experts, unit_size);
+    if(need > 0x7FFFFFFFull)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: sorted rows overflow int32", fn);
+    if(sorted_capacity < need)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: sorted_capacity=%u, %zu needed", fn,
+                    sorted_capacity, need);
+    return hip_status(w8a8::launch_moe_sort(topk_ids, tokens, topk, experts, unit_size,
+                                            expert_count, expert_start, padded_count,
+                                            sorted_token_ids, sorted_capacity, dst_row, stream),
+                      fn);
+}
+
+int w8a8_moe_gemm(uint32_t experts, uint32_t rows, uint32_t n, uint32_t k, const int8_t* a,
+                  uint32_t lda, const int8_t* w, uint32_t ldw, uint64_t w_expert_stride, void* c,
+                  uint32_t ldc, const float* scale_a, const float* scale_w,
+                  float tensor_scale_a, float tensor_scale_b, const int32_t* expert_start,
+                  const int32_t* expert_count, int out_type, hipStream_t stream)
+{
+    const char* fn = "w8a8_moe_gemm";
+    if(!a || !w || !c || !expert_start || !expert_count)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: null pointer argument", fn);
+    if(experts == 0 || n == 0 || k == 0)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: experts, n, k must be > 0", fn);
+    if(out_type != W8A8_OUT_I32 && out_type != W8A8_OUT_F16)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: unknown out_type %d", fn, out_type);
+    if(lda < k || ldw < k || ldc < n)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: lda=%u ldw=%u must be >= k=%u, ldc=%u >= n=%u",
+                    fn, lda, ldw, k, ldc, n);
+    if(w_expert_stride < (uint64_t)(n - 1) * ldw + k)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: w_expert_stride smaller than one expert", fn);
+    if(reinterpret_cast<uintptr_t>(a) % 16 || reinterpret_cast<uintptr_t>(w) % 16 || lda % 16
+       || ldw % 16 || k % 16 || w_expert_stride % 16)
+        return fail(W8A8_ERROR_NOT_SUPPORTED,
+                    "%s: needs 16-byte aligned a/w, lda, ldw, k, w_expert_stride %% 16 == 0", fn);
+    if((uint64_t)rows * lda > 0x7FFFFFFFull || (uint64_t)n * ldw > 0x7FFFFFFFull)
+        return fail(W8A8_ERROR_NOT_SUPPORTED, "%s: a or one expert's weights over 2 GiB", fn);
+    if(rows == 0) return hip_status(hipSuccess, fn);
+    w8a8::MoeGemmArgs g{a,    w,   c,   scale_a, scale_w, expert_start, expert_count,
+                        rows, experts, n, k, lda, ldw, ldc, w_expert_stride, tensor_scale_a,
+                        tensor_scale_b, out_type};
+    return hip_status(w8a8::launch_moe_gemm(g, stream), fn);
+}
+
+int w8a8_moe_silu_mul_quant(const void* gate_up, uint32_t ld_gu, const float* smooth_scale,
+                            const int32_t* expert_start, const int32_t* expert_count,
+                            uint32_t experts, uint32_t rows, uint32_t inter, int8_t* q,
+                            uint32_t ldq, float* row_scale, float quant_max, hipStream_t stream)
+{
+    const char* fn = "w8a8_moe_silu_mul_quant";
+    if(!gate_up || !expert_start || !expert_count || !q || !row_scale)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: null pointer argument", fn);
+    if(experts == 0 || inter == 0)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: experts and inter must be > 0", fn);
+    if(inter > 32768) return fail(W8A8_ERROR_NOT_SUPPORTED, "%s: inter=%u > 32768", fn, inter);
+    if(ld_gu == 0) ld_gu = 2 * inter;
+    if(ldq == 0) ldq = inter;
+    if(ld_gu < 2 * inter || ldq < inter)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: ld_gu=%u must be >= 2*inter and ldq=%u >= inter",
+                    fn, ld_gu, ldq);
+    if(!valid_qmax(quant_max))
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: quant_max must be in (0, 127]", fn);
+    return hip_status(w8a8::launch_silu_mul_quant(static_cast<const uint16_t*>(gate_up), ld_gu,
+                                                  smooth_scale, expert_start, expert_count,
+                                                  experts, rows, inter, q, ldq, row_scale,
+                                                  quant_max, stream),
+                      fn);
+}
+
+int w8a8_moe_combine(const void* y, uint32_t ldy, uint32_t rows_y, const float* topk_weights,
+                     const int32_t* dst_row, uint32_t tokens, uint32_t topk, uint32_t n,
+                     void* out, uint32_t ldo, hipStream_t stream)
+{
+    const char* fn = "w8a8_moe_combine";
+    if(!y || !topk_weights || !dst_row || !out)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: null pointer argument", fn);
+    if(tokens == 0 || topk == 0 || n == 0)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: tokens, topk, n must be > 0", fn);
+    if(ldy == 0) ldy = n;
+    if(ldo == 0) ldo = n;
+    if(ldy < n || ldo < n)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: ldy=%u / ldo=%u smaller than n=%u", fn, ldy, ldo,
+                    n);
+    return hip_status(w8a8::launch_moe_combine(static_cast<const uint16_t*>(y), ldy, rows_y,
+                                               topk_weights, dst_row, tokens, topk, n,
+                                               static_cast<uint16_t*>(out), ldo, stream),
+                      fn);
 }
 
 } // extern "C"

@@ -216,18 +216,13 @@ __device__ __forceinline__ void store4(const KArgs& p, uint32_t m, uint32_t n, c
     }
 }
 
+// One BM x BN output tile at (m0, n0) of problem p, computed by the whole
+// block; `lds` is the block's kLdsBytes ring.  Shared by the plain, grouped
+// and MoE kernels, which differ only in how a block finds its tile.
 template <class C, int OUT>
-__global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_tile_kernel(KArgs p, int vec_ok)
+__device__ __forceinline__ void gemm_tile(const KArgs& p, uint32_t m0, uint32_t n0, int vec_ok,
+                                          int8_t* lds)
 {
-    extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
-
-    const uint32_t tiles_m = (p.m + C::kBM - 1) / C::kBM;
-    const uint32_t tiles_n = (p.n + C::kBN - 1) / C::kBN;
-    uint32_t       tm, tn;
-    tile_coords<C::kGroupM>(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, tm, tn);
-    const uint32_t m0 = tm * C::kBM;
-    const uint32_t n0 = tn * C::kBN;
-
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); // wave-uniform
     const int lane = threadIdx.x % kWave;
     const int wm   = wave / C::kWavesN;
@@ -406,6 +401,17 @@ __global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_tile_kernel(KArgs p, i
             }
         }
     }
+}
+
+template <class C, int OUT>
+__global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_tile_kernel(KArgs p, int vec_ok)
+{
+    extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
+    const uint32_t tiles_m = (p.m + C::kBM - 1) / C::kBM;
+    const uint32_t tiles_n = (p.n + C::kBN - 1) / C::kBN;
+    uint32_t       tm, tn;
+    tile_coords<C::kGroupM>(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, tm, tn);
+    gemm_tile<C, OUT>(p, tm * C::kBM, tn * C::kBN, vec_ok, lds);
 }
 
 // Launch one configuration; the caller has validated the fast-path

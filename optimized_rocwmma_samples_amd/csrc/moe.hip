@@ -1,0 +1,508 @@
+// moe.hip -- the MoE pieces around the W8A8 GEMM for gfx950: top-k softmax
+// routing, a deterministic expert sort, the SiLU(gate)*up requantization
+// between the two expert GEMMs, the weighted combine back to token order, and
+// the launchers of the grouped / MoE GEMM kernels.
+#include "gemm_i8_grouped_kernel.hpp"
+#include "w8a8_internal.hpp"
+
+#include <algorithm>
+#include <cstddef>
+#include <mutex>
+
+namespace w8a8 {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Top-k softmax (kernel_topk_softmax, rocwmma_topk_softmax.cpp:58-131).
+// One wave per token.  Experts are chosen on the logits (softmax is monotonic,
+// so the choice is exact), highest first, the lower expert index winning ties
+// (the reference's strict '>' keeps the lower lane).  weight =
+// exp(l - max) * (1 / sum_e exp(l_e - max)), as the reference computes it.
+// ---------------------------------------------------------------------------
+constexpr int kTopkWaves = 4;
+
+template <bool F16>
+__device__ __forceinline__ float load_logit(const void* p, size_t i)
+{
+    if constexpr(F16)
+        return half_bits_to_float(static_cast<const uint16_t*>(p)[i]);
+    else
+        return static_cast<const float*>(p)[i];
+}
+
+// (value, index) of the better of two candidates: larger value, then lower index.
+__device__ __forceinline__ void better(float& v, int& i, float ov, int oi)
+{
+    if(ov > v || (ov == v && oi < i)) {
+        v = ov;
+        i = oi;
+    }
+}
+
+template <bool F16>
+__global__ void __launch_bounds__(kTopkWaves* kWave)
+    topk_softmax_kernel(const void* logits, float* topk_w, int32_t* topk_ids, uint32_t tokens,
+                        uint32_t experts, uint32_t topk)
+{
+    const uint32_t tok  = blockIdx.x * kTopkWaves + threadIdx.x / kWave;
+    const int      lane = threadIdx.x % kWave;
+    if(tok >= tokens) return; // uniform per wave
+    const size_t row = (size_t)tok * experts;
+
+    float wmax = -INFINITY;
+    for(uint32_t e = lane; e < experts; e += kWave) wmax = fmaxf(wmax, load_logit<F16>(logits, row + e));
+    wmax = wave_max(wmax);
+    float wsum = 0.f;
+    for(uint32_t e = lane; e < experts; e += kWave) wsum += expf(load_logit<F16>(logits, row + e) - wmax);
+#pragma unroll
+    for(int d = kWave / 2; d > 0; d >>= 1) wsum += __shfl_xor(wsum, d, kWave);
+    const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+
+    // a lane owns experts lane, lane+64, ...: `used` marks the chosen ones
+    uint64_t used = 0;
+    for(uint32_t k = 0; k < topk; ++k) {
+        float bv = -INFINITY;
+        int   bi = 0x7FFFFFFF;
+        int   j  = 0;
+        for(uint32_t e = lane; e < experts; e += kWave, ++j)
+            if(!((used >> j) & 1u)) better(bv, bi, load_logit<F16>(logits, row + e), (int)e);
+#pragma unroll
+        for(int d = kWave / 2; d > 0; d >>= 1) {
+            const float ov = __shfl_xor(bv, d, kWave);
+            const int   oi = __shfl_xor(bi, d, kWave);
+            better(bv, bi, ov, oi);
+        }
+        // every lane now holds the winner; its owner marks it used
+        if(bi != 0x7FFFFFFF && (uint32_t)bi % kWave == (uint32_t)lane)
+            used |= 1ull << ((uint32_t)bi / kWave);
+        if(lane == 0) {
+            const bool ok                          = bi != 0x7FFFFFFF;
+            topk_ids[(size_t)tok * topk + k]       = ok ? bi : -1;
+            topk_w[(size_t)tok * topk + k]         = ok ? expf(bv - wmax) * inv : 0.f;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Expert sort (kernel_moe_histogram / kernel_prefix_sum / kernel_moe_scatter,
+// rocwmma_moe_sorting.cpp:53-125), one workgroup, deterministic: inside an
+// expert, pairs keep ascending flat order t*topk + slot (the reference's
+// atomic scatter gives an arbitrary order, :122-124).  Outputs are the
+// reference's (count, start with start[E] = total, padded count, sorted token
+// ids with -1 in padding) plus dst_row[flat], the sorted row of each pair.
+// ---------------------------------------------------------------------------
+constexpr int kSortThreads = 1024;
+constexpr int kSortWaves   = kSortThreads / kWave;
+
+__global__ void __launch_bounds__(kSortThreads)
+    moe_sort_kernel(const int32_t* __restrict__ ids, uint32_t total, uint32_t topk,
+                    uint32_t experts, uint32_t unit, int32_t* expert_count, int32_t* expert_start,
+                    int32_t* padded_count, int32_t* sorted_ids, uint32_t sorted_cap,
+                    int32_t* dst_row)
+{
+    extern __shared__ int32_t sm[];
+    int32_t*  cnt    = sm;                   // [E]
+    int32_t*  start  = cnt + experts;        // [E + 1]
+    int32_t*  cursor = start + experts + 1;  // [E]
+    int32_t*  wcnt   = cursor + experts;     // [waves][E]
+    const int tid    = threadIdx.x;
+    const int wave   = tid / kWave;
+    const int lane   = tid % kWave;
+
+    for(uint32_t e = tid; e < experts; e += kSortThreads) cnt[e] = cursor[e] = 0;
+    for(uint32_t i = tid; i < experts * kSortWaves; i += kSortThreads) wcnt[i] = 0;
+    __syncthreads();
+    for(uint32_t p = tid; p < total; p += kSortThreads) {
+        const int32_t e = ids[p];
+        if(e >= 0 && (uint32_t)e < experts) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    if(wave == 0) { // padded exclusive prefix, 64 experts per step
+        int32_t carry = 0;
+        for(uint32_t base = 0; base < experts; base += kWave) {
+            const uint32_t e   = base + lane;
+            const int32_t  c   = e < experts ? cnt[e] : 0;
+            const int32_t  pad = (int32_t)(((uint32_t)c + unit - 1) / unit * unit);
+            int32_t        s   = pad;
+#pragma unroll
+            for(int d = 1; d < kWave; d <<= 1) {
+                const int32_t o = __shfl_up(s, d, kWave);
+                if(lane >= d) s += o;
+            }
+            if(e < experts) {
+                start[e]        = carry + s - pad;
+                expert_count[e] = c;
+                expert_start[e] = carry + s - pad;
+                padded_count[e] = pad;
+            }
+            carry += __shfl(s, kWave - 1, kWave);
+        }
+        if(lane == 0) {
+            start[experts]        = carry;
+            expert_start[experts] = carry;
+        }
+    }
+    for(uint32_t i = tid; i < sorted_cap; i += kSortThreads) sorted_ids[i] = -1;
+    __syncthreads();
+
+    for(uint32_t c0 = 0; c0 < total; c0 += kSortThreads) {
+        const uint32_t p     = c0 + tid;
+        const int32_t  e     = p < total ? ids[p] : -1;
+        const bool     valid = e >= 0 && (uint32_t)e < experts;
+        // rank among this wave's earlier lanes with the same expert
+        int      rank    = 0;
+        uint64_t pending = __ballot(valid);
+        while(pending) {
+            const int      leader = __ffsll((unsigned long long)pending) - 1;
+            const int32_t  le     = __shfl(e, leader, kWave);
+            const uint64_t same   = __ballot(valid && e == le);
+            if(valid && e == le) rank = __popcll(same & ((1ull << lane) - 1));
+            if(lane == leader) wcnt[wave * experts + le] = __popcll(same);
+            pending &= ~same;
+        }
+        __syncthreads();
+        if(valid) {
+            int32_t base = cursor[e];
+            for(int w = 0; w < wave; ++w) base += wcnt[w * experts + e];
+            const int32_t slot = start[e] + base + rank;
+            sorted_ids[slot]   = (int32_t)(p / topk);
+            dst_row[p]         = slot;
+        } else if(p < total) {
+            dst_row[p] = -1;
+        }
+        __syncthreads();
+        for(uint32_t x = tid; x < experts; x += kSortThreads) {
+            int32_t s = 0;
+            for(int w = 0; w < kSortWaves; ++w) {
+                s += wcnt[w * experts + x];
+                wcnt[w * experts + x] = 0;
+            }
+            cursor[x] += s;
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// SiLU(gate) * up -> int8 rows for the down GEMM.  Row r of gate_up (fp16,
+// gate in columns [0, inter), up in [inter, 2*inter)) gives
+//   a[j] = (g / (1 + exp(-g))) * u  [* s2[e, j]]
+// and the same absmax quantization as the SmoothQuant kernel.  Rows outside
+// every expert's [start, start + count) (the sort's padding) are skipped.
+// The row stays in registers (CPL 16-byte chunks per lane, WPR waves a row).
+// ---------------------------------------------------------------------------
+constexpr int kSqThreads = 256;
+constexpr int kSqWaves   = kSqThreads / kWave;
+
+struct SiluRows {
+    const uint16_t* gu;
+    uint32_t        ld_gu;
+    const float*    s2; // [experts, inter] or null
+    const int32_t*  expert_start;
+    const int32_t*  expert_count;
+    uint32_t        experts, rows, inter;
+    int8_t*         q;
+    uint32_t        ldq;
+    float*          r;
+    float           qmax;
+};
+
+// Expert holding sorted row `row`, or -1 for padding / out-of-range rows.
+__device__ __forceinline__ int row_expert(const SiluRows& p, uint32_t row)
+{
+    int lo = 0, hi = (int)p.experts - 1, e = -1;
+    while(lo <= hi) { // last expert with start <= row
+        const int mid = (lo + hi) / 2;
+        if(p.expert_start[mid] <= (int32_t)row) {
+            e  = mid;
+            lo = mid + 1;
+        } else {
+            hi = mid - 1;
+        }
+    }
+    if(e < 0 || (int64_t)row >= (int64_t)p.expert_start[e] + p.expert_count[e]) return -1;
+    return e;
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.f + expf(-g))) * u; }
+
+template <int CPL, int WPR, bool VEC>
+__global__ void __launch_bounds__(kSqThreads) silu_quant_kernel(SiluRows p)
+{
+    constexpr int kRowsPerBlock = kSqWaves / WPR;
+    constexpr int kSpan         = CPL * 8 * kWave;
+    const int      wave = threadIdx.x / kWave;
+    const int      lane = threadIdx.x % kWave;
+    const int      rib  = wave / WPR;
+    const int      part = wave % WPR;
+    const uint32_t row  = blockIdx.x * kRowsPerBlock + rib;
+    const int      e    = row < p.rows ? row_expert(p, row) : -1;
+    const bool     valid = e >= 0;
+
+    const uint16_t* g  = p.gu + (size_t)row * p.ld_gu;
+    const uint16_t* u  = g + p.inter;
+    const float*    s2 = p.s2 ? p.s2 + (size_t)e * p.inter : nullptr;
+    const uint32_t  n  = p.inter;
+    const uint32_t  base = part * kSpan + lane * 8;
+    float           pv[CPL * 8];
+    float           amax = 0.f;
+    if(valid) {
+#pragma unroll
+        for(int j = 0; j < CPL; ++j) {
+            const uint32_t c = base + j * (8 * kWave);
+            if(VEC && c + 8 <= n) {
+                const uint4 gr = *reinterpret_cast<const uint4*>(g + c);
+                const uint4 ur = *reinterpret_cast<const uint4*>(u + c);
+                const uint32_t gw[4] = {gr.x, gr.y, gr.z, gr.w};
+                const uint32_t uw[4] = {ur.x, ur.y, ur.z, ur.w};
+#pragma unroll
+                for(int h = 0; h < 4; ++h) {
+                    pv[j * 8 + 2 * h]     = silu_mul(half_bits_to_float(gw[h] & 0xFFFFu),
+                                                     half_bits_to_float(uw[h] & 0xFFFFu));
+                    pv[j * 8 + 2 * h + 1] = silu_mul(half_bits_to_float(gw[h] >> 16),
+                                                     half_bits_to_float(uw[h] >> 16));
+                }
+                if(s2) {
+                    const float4 s0 = *reinterpret_cast<const float4*>(s2 + c);
+                    const float4 s1 = *reinterpret_cast<const float4*>(s2 + c + 4);
+                    pv[j * 8 + 0] *= s0.x;
+                    pv[j * 8 + 1] *= s0.y;
+                    pv[j * 8 + 2] *= s0.z;
+                    pv[j * 8 + 3] *= s0.w;
+                    pv[j * 8 + 4] *= s1.x;
+                    pv[j * 8 + 5] *= s1.y;
+                    pv[j * 8 + 6] *= s1.z;
+                    pv[j * 8 + 7] *= s1.w;
+                }
+            } else {
+#pragma unroll
+                for(int x = 0; x < 8; ++x) {
+                    float a = 0.f;
+                    if(c + x < n) {
+                        a = silu_mul(half_bits_to_float(g[c + x]), half_bits_to_float(u[c + x]));
+                        if(s2) a *= s2[c + x];
+                    }
+                    pv[j * 8 + x] = a;
+                }
+            }
+#pragma unroll
+            for(int x = 0; x < 8; ++x) amax = fmaxf(amax, fabsf(pv[j * 8 + x]));
+        }
+    }
+    amax = wave_max(amax);
+    if constexpr(WPR > 1) {
+        __shared__ float red[kSqWaves];
+        if(lane == 0) red[wave] = amax;
+        __syncthreads();
+#pragma unroll
+        for(int w = 0; w < WPR; ++w) amax = fmaxf(amax, red[rib * WPR + w]);
+    }
+    if(!valid) return;
+    const float qmax = p.qmax;
+    const float rs   = amax / qmax;
+    if(part == 0 && lane == 0) p.r[row] = rs;
+    const float inv  = rs > 0.f ? 1.f / rs : 0.f;
+    int8_t*     qrow = p.q + (size_t)row * p.ldq;
+#pragma unroll
+    for(int j = 0; j < CPL; ++j) {
+        const uint32_t c = base + j * (8 * kWave);
+        int            qi[8];
+#pragma unroll
+        for(int x = 0; x < 8; ++x) qi[x] = quant_i8(pv[j * 8 + x], inv, qmax);
+        if(VEC && c + 8 <= n) {
+            uint2 pk;
+            pk.x = pack4_i8(qi[0], qi[1], qi[2], qi[3]);
+            pk.y = pack4_i8(qi[4], qi[5], qi[6], qi[7]);
+            *reinterpret_cast<uint2*>(qrow + c) = pk;
+        } else {
+#pragma unroll
+            for(int x = 0; x < 8; ++x)
+                if(c + x < n) qrow[c + x] = (int8_t)qi[x];
+        }
+    }
+}
+
+template <int CPL, int WPR>
+hipError_t launch_silu_rows(const SiluRows& p, bool vec, hipStream_t stream)
+{
+    constexpr int kRowsPerBlock = kSqWaves / WPR;
+    const dim3    grid((p.rows + kRowsPerBlock - 1) / kRowsPerBlock);
+    if(vec)
+        hipLaunchKernelGGL((silu_quant_kernel<CPL, WPR, true>), grid, dim3(kSqThreads), 0, stream, p);
+    else
+        hipLaunchKernelGGL((silu_quant_kernel<CPL, WPR, false>), grid, dim3(kSqThreads), 0, stream,
+                           p);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Weighted combine: out[t, n] = half(sum over slots, ascending, of
+// fma(w[t, slot], float(y[dst_row[t*topk + slot], n]), acc)); pairs with
+// dst_row < 0 are skipped.  8 columns per thread.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+    moe_combine_kernel(const uint16_t* __restrict__ y, uint32_t ldy, const float* __restrict__ w,
+                       const int32_t* __restrict__ dst_row, uint32_t tokens, uint32_t topk,
+                       uint32_t n, uint32_t rows_y, uint16_t* __restrict__ out, uint32_t ldo,
+                       int vec)
+{
+    const uint32_t groups = (n + 7) / 8;
+    const size_t   idx    = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if(idx >= (size_t)tokens * groups) return;
+    const uint32_t t  = idx / groups;
+    const uint32_t c0 = (idx % groups) * 8;
+    float          acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for(uint32_t s = 0; s < topk; ++s) {
+        const int32_t r = dst_row[(size_t)t * topk + s];
+        if(r < 0 || (uint32_t)r >= rows_y) continue;
+        const float     ws  = w[(size_t)t * topk + s];
+        const uint16_t* src = y + (size_t)r * ldy + c0;
+        if(vec && c0 + 8 <= n) {
+            const uint4    v    = *reinterpret_cast<const uint4*>(src);
+            const uint32_t h[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for(int x = 0; x < 4; ++x) {
+                acc[2 * x]     = __builtin_fmaf(ws, half_bits_to_float(h[x] & 0xFFFFu), acc[2 * x]);
+                acc[2 * x + 1] = __builtin_fmaf(ws, half_bits_to_float(h[x] >> 16), acc[2 * x + 1]);
+            }
+        } else {
+            for(int x = 0; x < 8; ++x)
+                if(c0 + x < n) acc[x] = __builtin_fmaf(ws, half_bits_to_float(src[x]), acc[x]);
+        }
+    }
+    uint16_t* dst = out + (size_t)t * ldo + c0;
+    if(vec && c0 + 8 <= n) {
+        uint4 v;
+        v.x = (uint32_t)float_to_half_bits(acc[0]) | ((uint32_t)float_to_half_bits(acc[1]) << 16);
+        v.y = (uint32_t)float_to_half_bits(acc[2]) | ((uint32_t)float_to_half_bits(acc[3]) << 16);
+        v.z = (uint32_t)float_to_half_bits(acc[4]) | ((uint32_t)float_to_half_bits(acc[5]) << 16);
+        v.w = (uint32_t)float_to_half_bits(acc[6]) | ((uint32_t)float_to_half_bits(acc[7]) << 16);
+        *reinterpret_cast<uint4*>(dst) = v;
+    } else {
+        for(int x = 0; x < 8; ++x)
+            if(c0 + x < n) dst[x] = float_to_half_bits(acc[x]);
+    }
+}
+
+using GemmGrouped = gemm::Cfg<256, 256, 128, 2, 2, 4>;
+
+} // namespace
+
+static_assert(sizeof(gemm::KArgs) == sizeof(w8a8_group_desc)
+                  && offsetof(gemm::KArgs, m) == offsetof(w8a8_group_desc, m)
+                  && offsetof(gemm::KArgs, tsb) == offsetof(w8a8_group_desc, tensor_scale_b),
+              "w8a8_group_desc must have the device descriptor's layout");
+
+hipError_t launch_topk_softmax(const void* logits, bool f16, float* w, int32_t* ids,
+                               uint32_t tokens, uint32_t experts, uint32_t topk,
+                               hipStream_t stream)
+{
+    const dim3 grid((tokens + kTopkWaves - 1) / kTopkWaves);
+    if(f16)
+        hipLaunchKernelGGL(topk_softmax_kernel<true>, grid, dim3(kTopkWaves * kWave), 0, stream,
+                           logits, w, ids, tokens, experts, topk);
+    else
+        hipLaunchKernelGGL(topk_softmax_kernel<false>, grid, dim3(kTopkWaves * kWave), 0, stream,
+                           logits, w, ids, tokens, experts, topk);
+    return hipGetLastError();
+}
+
+size_t moe_sort_lds_bytes(uint32_t experts)
+{
+    return sizeof(int32_t) * ((size_t)experts * (3 + kSortWaves) + 1);
+}
+
+hipError_t launch_moe_sort(const int32_t* ids, uint32_t tokens, uint32_t topk, uint32_t experts,
+                           uint32_t unit, int32_t* count, int32_t* start, int32_t* padded,
+                           int32_t* sorted_ids, uint32_t sorted_cap, int32_t* dst_row,
+                           hipStream_t stream)
+{
+    const size_t lds = moe_sort_lds_bytes(experts);
+    if(lds > 65536) {
+        static std::once_flag once;
+        std::call_once(once, [] {
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(moe_sort_kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+            (void)hipGetLastError();
+        });
+    }
+    hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(kSortThreads), lds, stream, ids,
+                       tokens * topk, topk, experts, unit, count, start, padded, sorted_ids,
+                       sorted_cap, dst_row);
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_mul_quant(const uint16_t* gu, uint32_t ld_gu, const float* s2,
+                                 const int32_t* expert_start, const int32_t* expert_count,
+                                 uint32_t experts, uint32_t rows, uint32_t inter, int8_t* q,
+                                 uint32_t ldq, float* r, float qmax, hipStream_t stream)
+{
+    if(rows == 0) return hipSuccess;
+    SiluRows p{gu, ld_gu, s2, expert_start, expert_count, experts, rows, inter, q, ldq, r, qmax};
+    const bool vec = reinterpret_cast<uintptr_t>(gu) % 16 == 0 && ld_gu % 8 == 0
+                     && inter % 8 == 0 && (s2 == nullptr || reinterpret_cast<uintptr_t>(s2) % 16 == 0)
+                     && reinterpret_cast<uintptr_t>(q) % 8 == 0 && ldq % 8 == 0;
+    const uint32_t n = inter;
+    if(n <= 512) return launch_silu_rows<1, 1>(p, vec, stream);
+    if(n <= 1024) return launch_silu_rows<2, 1>(p, vec, stream);
+    if(n <= 2048) return launch_silu_rows<4, 1>(p, vec, stream);
+    if(n <= 4096) return launch_silu_rows<8, 1>(p, vec, stream);
+    if(n <= 8192) return launch_silu_rows<16, 1>(p, vec, stream);
+    if(n <= 16384) return launch_silu_rows<16, 2>(p, vec, stream);
+    return launch_silu_rows<16, 4>(p, vec, stream); // inter <= 32768 (host-checked)
+}
+
+hipError_t launch_moe_combine(const uint16_t* y, uint32_t ldy, uint32_t rows_y, const float* w,
+                              const int32_t* dst_row, uint32_t tokens, uint32_t topk, uint32_t n,
+                              uint16_t* out, uint32_t ldo, hipStream_t stream)
+{
+    const size_t threads = (size_t)tokens * ((n + 7) / 8);
+    if(threads == 0) return hipSuccess;
+    const int vec = reinterpret_cast<uintptr_t>(y) % 16 == 0 && ldy % 8 == 0
+                    && reinterpret_cast<uintptr_t>(out) % 16 == 0 && ldo % 8 == 0;
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((uint32_t)((threads + 255) / 256)), dim3(256), 0,
+                       stream, y, ldy, w, dst_row, tokens, topk, n, rows_y, out, ldo, vec);
+    return hipGetLastError();
+}
+
+hipError_t launch_grouped_gemm(const w8a8_group_desc* groups_dev, uint32_t ngroups,
+                               uint32_t total_tiles, int out_type, int vec_ok, hipStream_t stream)
+{
+    return gemm::launch_grouped<GemmGrouped>(reinterpret_cast<const gemm::KArgs*>(groups_dev),
+                                             ngroups, total_tiles, out_type, vec_ok, stream);
+}
+
+uint32_t grouped_gemm_tiles(uint32_t m, uint32_t n)
+{
+    return ((m + GemmGrouped::kBM - 1) / GemmGrouped::kBM)
+           * ((n + GemmGrouped::kBN - 1) / GemmGrouped::kBN);
+}
+
+hipError_t launch_moe_gemm(const MoeGemmArgs& a, hipStream_t stream)
+{
+    gemm::MoeArgs q;
+    q.a            = a.a;
+    q.w            = a.w;
+    q.c            = a.c;
+    q.sa           = a.scale_a;
+    q.sw           = a.scale_w;
+    q.expert_start = a.expert_start;
+    q.expert_count = a.expert_count;
+    q.rows         = a.rows;
+    q.experts      = a.experts;
+    q.n            = a.n;
+    q.k            = a.k;
+    q.lda          = a.lda;
+    q.ldw          = a.ldw;
+    q.ldc          = a.ldc;
+    q.w_stride     = a.w_stride;
+    q.tsa          = a.tsa;
+    q.tsb          = a.tsb;
+    const size_t esz    = a.out_type == W8A8_OUT_I32 ? 4 : 2;
+    const int    vec_ok = reinterpret_cast<uintptr_t>(a.c) % (4 * esz) == 0 && a.ldc % 4 == 0
+                       && (a.scale_w == nullptr
+                           || (reinterpret_cast<uintptr_t>(a.scale_w) % 16 == 0 && a.n % 4 == 0));
+    return gemm::launch_moe<GemmGrouped>(q, a.out_type, vec_ok, stream);
+}
+
+} // namespace w8a8

@@ -2,6 +2,8 @@
 // Callers (capi.cpp) have validated every argument before these run.
 #pragma once
 
+#include "../../include/w8a8.h"
+
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -72,5 +74,46 @@ hipError_t launch_gemm_generic(const GemmArgs& g, size_t sam, size_t sak, size_t
 // dst row-major with leading dimension ldd (zero-padded up to ldd).
 hipError_t launch_transpose_i8(const int8_t* src, uint32_t lds_src, int8_t* dst, uint32_t ldd,
                                uint32_t rows, uint32_t cols, hipStream_t stream);
+
+// ---- MoE (moe.hip) ----------------------------------------------------------
+hipError_t launch_topk_softmax(const void* logits, bool f16, float* w, int32_t* ids,
+                               uint32_t tokens, uint32_t experts, uint32_t topk,
+                               hipStream_t stream);
+
+size_t     moe_sort_lds_bytes(uint32_t experts);
+hipError_t launch_moe_sort(const int32_t* ids, uint32_t tokens, uint32_t topk, uint32_t experts,
+                           uint32_t unit, int32_t* count, int32_t* start, int32_t* padded,
+                           int32_t* sorted_ids, uint32_t sorted_cap, int32_t* dst_row,
+                           hipStream_t stream);
+
+hipError_t launch_silu_mul_quant(const uint16_t* gu, uint32_t ld_gu, const float* s2,
+                                 const int32_t* expert_start, const int32_t* expert_count,
+                                 uint32_t experts, uint32_t rows, uint32_t inter, int8_t* q,
+                                 uint32_t ldq, float* r, float qmax, hipStream_t stream);
+
+hipError_t launch_moe_combine(const uint16_t* y, uint32_t ldy, uint32_t rows_y, const float* w,
+                              const int32_t* dst_row, uint32_t tokens, uint32_t topk, uint32_t n,
+                              uint16_t* out, uint32_t ldo, hipStream_t stream);
+
+// Grouped GEMM over device descriptors (validated by the caller: fast-path
+// alignment, every operand under 2 GiB).
+uint32_t   grouped_gemm_tiles(uint32_t m, uint32_t n);
+hipError_t launch_grouped_gemm(const w8a8_group_desc* groups_dev, uint32_t ngroups,
+                               uint32_t total_tiles, int out_type, int vec_ok, hipStream_t stream);
+
+struct MoeGemmArgs {
+    const int8_t*  a;
+    const int8_t*  w;
+    void*          c;
+    const float*   scale_a;
+    const float*   scale_w;
+    const int32_t* expert_start;
+    const int32_t* expert_count;
+    uint32_t       rows, experts, n, k, lda, ldw, ldc;
+    uint64_t       w_stride;
+    float          tsa, tsb;
+    int            out_type;
+};
+hipError_t launch_moe_gemm(const MoeGemmArgs& a, hipStream_t stream);
 
 } // namespace w8a8

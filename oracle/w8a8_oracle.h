@@ -86,8 +86,11 @@ void w8a8o_dequant_f16(uint32_t M, uint32_t N, const int32_t* acc, uint32_t ldac
 
 /*
  * Softmax + top-k routing (rocwmma_topk_softmax.cpp:58-131), fp32 logits.
- * Selection is made on the logits (softmax is monotonic); ties go to the lower
- * expert index, as the strict '>' at :115-119 does.  weights = exp(l - max) / sum.
+ * Selection is made on the logits (softmax is monotonic); equal logits go to
+ * the lower expert index.  (The reference's shfl_down tree, :111-119, keeps
+ * the left partial on ties, which is not always the lowest index: a tie
+ * between experts 2 and 4 goes to 4.  The build defines ties by index.)
+ * weights = exp(l - max) * (1 / sum), the sum taken in expert order.
  */
 void w8a8o_topk_softmax(const float* logits, float* topk_weights, int32_t* topk_ids,
                         uint32_t tokens, uint32_t experts, uint32_t topk);

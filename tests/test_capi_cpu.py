@@ -183,6 +183,105 @@ def test_fused_packed_validation(w8a8):
     assert rc == W.ERROR_NOT_SUPPORTED and "k % 16" in msg
 
 
+def _desc(**kw):
+    base = dict(a=0x1000, b=0x2000, c=0x3000, scale_a=None, scale_b=None, m=64, n=64, k=64,
+                lda=64, ldb=64, ldc=64, tensor_scale_a=1.0, tensor_scale_b=1.0)
+    base.update(kw)
+    return _lib.GroupDesc(**base)
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(a=None), W.ERROR_INVALID_VALUE, "null"),
+    (dict(k=0), W.ERROR_INVALID_VALUE, "must be > 0"),
+    (dict(ldc=8), W.ERROR_INVALID_VALUE, "ldc"),
+    (dict(k=40, lda=48, ldb=48), W.ERROR_NOT_SUPPORTED, "% 16"),
+    (dict(a=0x1008), W.ERROR_NOT_SUPPORTED, "aligned"),
+    (dict(m=40000, lda=65536), W.ERROR_NOT_SUPPORTED, "2 GiB"),
+])
+def test_grouped_gemm_validation(w8a8, kw, code, needle):
+    descs = (_lib.GroupDesc * 2)(_desc(), _desc(**kw))
+    ws = W.library().w8a8_grouped_gemm_workspace_size(2)
+    assert ws >= 2 * ctypes.sizeof(_lib.GroupDesc) and ws % 256 == 0
+    rc, msg = _status("w8a8_grouped_gemm", descs, 2, W.OUT_F16, ctypes.c_void_p(0x10000), ws, None)
+    assert rc == code and needle in msg and "group 1" in msg, msg
+    rc, msg = _status("w8a8_grouped_gemm", descs, 2, W.OUT_F16, ctypes.c_void_p(0x10000), 8, None)
+    assert rc == W.ERROR_INVALID_VALUE and "workspace" in msg
+    rc, msg = _status("w8a8_grouped_gemm", descs, 0, W.OUT_F16, ctypes.c_void_p(0x10000), ws, None)
+    assert rc == W.ERROR_INVALID_VALUE
+
+
+def test_grouped_gemm_desc_layout(w8a8):
+    # the device reads the descriptors as its own argument block: field offsets are ABI
+    assert ctypes.sizeof(_lib.GroupDesc) == 72
+    assert _lib.GroupDesc.m.offset == 40 and _lib.GroupDesc.tensor_scale_b.offset == 68
+
+
+def test_topk_softmax_validation(w8a8):
+    ok = [FAKE, 0, FAKE, FAKE, 16, 8, 2, None]
+    bad = list(ok); bad[0] = None
+    assert _status("w8a8_topk_softmax", *bad)[0] == W.ERROR_INVALID_VALUE
+    bad = list(ok); bad[6] = 9
+    rc, msg = _status("w8a8_topk_softmax", *bad)
+    assert rc == W.ERROR_INVALID_VALUE and "topk" in msg
+    bad = list(ok); bad[5] = 5000; bad[6] = 2
+    assert _status("w8a8_topk_softmax", *bad)[0] == W.ERROR_INVALID_VALUE
+    bad = list(ok); bad[1] = 2
+    assert _status("w8a8_topk_softmax", *bad)[0] == W.ERROR_INVALID_VALUE
+
+
+def test_moe_sort_validation(w8a8):
+    assert W.library().w8a8_moe_sort_capacity(4096, 2, 8, 32) == 4096 * 2 + 8 * 32
+    ok = [FAKE, 100, 2, 8, 32, FAKE, FAKE, FAKE, FAKE, 200 + 256, FAKE, None]
+    bad = list(ok); bad[9] = 200 + 255
+    rc, msg = _status("w8a8_moe_sort", *bad)
+    assert rc == W.ERROR_INVALID_VALUE and "capacity" in msg
+    bad = list(ok); bad[3] = 2000
+    assert _status("w8a8_moe_sort", *bad)[0] == W.ERROR_INVALID_VALUE
+    bad = list(ok); bad[5] = None
+    assert _status("w8a8_moe_sort", *bad)[0] == W.ERROR_INVALID_VALUE
+    bad = list(ok); bad[4] = 0
+    assert _status("w8a8_moe_sort", *bad)[0] == W.ERROR_INVALID_VALUE
+
+
+def _moe_gemm_args(**kw):
+    base = dict(e=8, rows=512, n=256, k=128, a=FAKE, lda=128, w=FAKE, ldw=128, ws=256 * 128,
+                c=FAKE, ldc=256, sa=None, sw=None, tsa=1.0, tsb=1.0, st=FAKE, cnt=FAKE,
+                out=W.OUT_F16, stream=None)
+    base.update(kw)
+    return list(base.values())
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(st=None), W.ERROR_INVALID_VALUE, "null"),
+    (dict(e=0), W.ERROR_INVALID_VALUE, "> 0"),
+    (dict(ldw=64), W.ERROR_INVALID_VALUE, "ldw"),
+    (dict(ws=1000), W.ERROR_INVALID_VALUE, "stride"),
+    (dict(k=40, lda=48, ldw=48, ws=256 * 48), W.ERROR_NOT_SUPPORTED, "% 16"),
+    (dict(rows=1 << 24, lda=256, k=256, ldw=256, ws=256 * 256), W.ERROR_NOT_SUPPORTED, "2 GiB"),
+    (dict(out=5), W.ERROR_INVALID_VALUE, "out_type"),
+])
+def test_moe_gemm_validation(w8a8, kw, code, needle):
+    rc, msg = _status("w8a8_moe_gemm", *_moe_gemm_args(**kw))
+    assert rc == code and needle in msg, msg
+
+
+def test_moe_silu_and_combine_validation(w8a8):
+    ok = [FAKE, 0, None, FAKE, FAKE, 8, 64, 256, FAKE, 0, FAKE, 127.0, None]
+    bad = list(ok); bad[1] = 300  # ld_gu < 2*inter
+    rc, msg = _status("w8a8_moe_silu_mul_quant", *bad)
+    assert rc == W.ERROR_INVALID_VALUE and "ld_gu" in msg
+    bad = list(ok); bad[7] = 40000
+    assert _status("w8a8_moe_silu_mul_quant", *bad)[0] == W.ERROR_NOT_SUPPORTED
+    bad = list(ok); bad[11] = 0.0
+    assert _status("w8a8_moe_silu_mul_quant", *bad)[0] == W.ERROR_INVALID_VALUE
+    okc = [FAKE, 0, 100, FAKE, FAKE, 10, 2, 64, FAKE, 0, None]
+    bad = list(okc); bad[1] = 32
+    rc, msg = _status("w8a8_moe_combine", *bad)
+    assert rc == W.ERROR_INVALID_VALUE and "ldy" in msg
+    bad = list(okc); bad[4] = None
+    assert _status("w8a8_moe_combine", *bad)[0] == W.ERROR_INVALID_VALUE
+
+
 def test_python_layer_raises_w8a8error(w8a8):
     with pytest.raises(W.W8A8Error) as ei:
         _lib.call("w8a8_smoothquant", None, None, None, None, 1, 1, 127.0, 0, 0, None)

@@ -273,3 +273,86 @@ def test_moe_sort_stable_brute_force():
         assert (seg[members.size:] == -1).all()
         assert np.array_equal(dst[members], start[ex] + np.arange(members.size))
     assert start[e] == padded.sum() and dst[3 * k + 1] == -1
+
+
+# ------------------------------------------------------- MoE activation
+def _silu_f64(g, u):
+    g = g.astype(np.float64)
+    return g / (1.0 + np.exp(-g)) * u.astype(np.float64)
+
+
+def test_silu_mul_quant_closed_forms():
+    inter = 40
+    gu = np.zeros((4, 2 * inter), np.float16)
+    # row 0: gate 0 -> silu 0 -> all-zero row: r = 0, q = 0
+    gu[0, inter:] = 3.0
+    # row 1: up 0 -> zero row
+    gu[1, :inter] = 2.0
+    # row 2: gate 32: 1 + exp(-32) rounds to 1 in fp32, so silu(32) = 32 exactly
+    gu[2, 5], gu[2, inter + 5] = 32.0, 1.0     # a = 32
+    gu[2, 6], gu[2, inter + 6] = 32.0, -0.25   # a = -8 -> -8 * 127/32 = -31.75 -> -32
+    # row 3: silu(-1) = silu(1) - 1: gate +-1 with up 1 gives two known magnitudes
+    gu[3, 0], gu[3, inter + 0] = 1.0, 1.0
+    gu[3, 1], gu[3, inter + 1] = -1.0, 1.0
+    q, r = O.silu_mul_quant(gu)
+    assert (q[:2] == 0).all() and (r[:2] == 0).all()
+    assert r[2] == np.float32(32.0) / np.float32(127.0)
+    assert q[2, 5] == 127 and q[2, 6] == -32
+    assert (np.delete(q[2], [5, 6]) == 0).all()
+    s1 = 1.0 / (1.0 + np.exp(-1.0))  # silu(1)
+    assert q[3, 0] == 127 and q[3, 1] == -round(127 * (1 - s1) / s1)  # -46.7 -> -47
+    # s2 scales each column before the absmax
+    s2 = np.ones(inter, np.float32)
+    s2[6] = 4.0
+    q2, r2 = O.silu_mul_quant(gu[2:3], s2)
+    assert r2[0] == r[2] and q2[0, 6] == -127 and q2[0, 5] == 127
+
+
+def test_silu_mul_quant_invariants_random():
+    inter = 1000
+    gu = G.normal(21, G.TID_X, (6, 2 * inter))
+    s2 = G.uniform(21, G.TID_S, (inter,), 0.5, 2.0)
+    q, r = O.silu_mul_quant(gu, s2)
+    a = _silu_f64(gu[:, :inter], gu[:, inter:]) * s2
+    np.testing.assert_allclose(r, np.abs(a).max(1) / 127.0, rtol=1e-6)
+    assert (np.abs(q) <= 127).all() and (np.abs(q).max(1) == 127).all()
+    # each q within half a step of a / r (plus float rounding of a and 1/r)
+    dev = np.abs(q - a / r[:, None])
+    assert dev.max() <= 0.5 + 1e-4
+    assert (np.sign(q) * np.sign(a) >= 0).all()
+
+
+def test_moe_combine_exact_rational():
+    # the oracle adds fma(w, y, acc) slot by slot: one rounding to fp32 per
+    # slot.  Here every w*y + acc is exact in float64 (checked with Fraction),
+    # so float64 arithmetic followed by one cast to fp32 is that fma.
+    from fractions import Fraction
+    t, k, n = 5, 3, 7
+    rng = np.random.default_rng(7)
+    y = rng.standard_normal((12, n)).astype(np.float16)
+    w = rng.random((t, k)).astype(np.float32)
+    dst = rng.integers(0, 12, (t * k)).astype(np.int32)
+    dst[4] = -1  # skipped pair
+    out = O.moe_combine(y, w, dst)
+    for ti in range(t):
+        for j in range(n):
+            acc = np.float32(0)
+            for s in range(k):
+                d = dst[ti * k + s]
+                if d < 0:
+                    continue
+                wide = float(w[ti, s]) * float(y[d, j]) + float(acc)
+                exact = Fraction(float(w[ti, s])) * Fraction(float(y[d, j])) + Fraction(float(acc))
+                assert Fraction(wide) == exact
+                acc = np.float32(wide)
+            assert out[ti, j] == np.float16(acc)
+
+
+def test_moe_combine_closed_forms():
+    y = G.normal(3, G.TID_X, (6, 16))
+    w = np.array([[1.0, 0.0], [0.5, 0.5], [1.0, 1.0]], np.float32)
+    dst = np.array([4, 0, 2, 2, -1, 5], np.int32)
+    out = O.moe_combine(y, w, dst)
+    assert np.array_equal(out[0].view(np.uint16), y[4].view(np.uint16))  # 1*y + 0*y'
+    assert np.array_equal(out[1].view(np.uint16), y[2].view(np.uint16))  # mean of equal rows
+    assert np.array_equal(out[2].view(np.uint16), y[5].view(np.uint16))  # invalid slot skipped
