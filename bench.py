@@ -13,8 +13,9 @@ Also reported: config 1 (standalone quantizer, X fp16 [2048, 4096]) in GB/s
 with buffer sets rotated over >512 MB so the 256 MB MALL cannot serve repeats,
 config 2 (W8A8 GEMM 4096^3 + dequant) in TOPS, and config 4 (decode: fused
 SmoothQuant + packed-weight GEMM at M in {1, 16, 64} on the Llama-70B MLP
-weights) in GB/s.  Per-kernel durations come from HIP events recorded on the
-stream the kernels run on.
+weights) in GB/s, and config 5 (Mixtral-shaped MoE FFN chain) in TOPS.
+Per-kernel durations come from HIP events recorded on the stream the kernels
+run on.
 
     python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--m 8192] [--no-cpu-baseline]
 """
@@ -225,6 +226,74 @@ def profiled_traffic(projs):
     return sum(per) / len(per), per
 
 
+def bench_moe(torch, w8a8, dev, gen, iters=10):
+    """Config 5: Mixtral-8x7B-shaped MoE FFN, 4096 tokens, hidden 4096, ffn
+    14336, 8 experts, top-2.  One iteration = routing, sort, MoE SmoothQuant
+    into expert-sorted rows, gate_up expert GEMM, SiLU(gate)*up requant, down
+    expert GEMM, combine; ops = 2 * 8192 rows * (28672*4096 + 4096*14336)."""
+    t, h, inter, e, k = 4096, 4096, 14336, 8, 2
+    x = torch.randn((t, h), generator=gen, device=dev)
+    cols = torch.randperm(h, generator=gen, device=dev)[: round(0.005 * h)]
+    x[:, cols] *= 20.0
+    x = x.to(torch.float16)
+    logits = torch.randn((t, e), generator=gen, device=dev)
+    s = torch.rand((e, h), generator=gen, device=dev) * 1.5 + 0.5
+    wgu = torch.randint(-127, 128, (e, 2 * inter, h), generator=gen, device=dev, dtype=torch.int8)
+    sgu = torch.rand((e, 2 * inter), generator=gen, device=dev) * 9e-3 + 1e-3
+    wd = torch.randint(-127, 128, (e, h, inter), generator=gen, device=dev, dtype=torch.int8)
+    sd = torch.rand((e, h), generator=gen, device=dev) * 9e-3 + 1e-3
+    cap = int(w8a8.library().w8a8_moe_sort_capacity(t, k, e, 32))
+    qa = torch.empty((cap, h), dtype=torch.int8, device=dev)
+    ra = torch.empty(cap, dtype=torch.float32, device=dev)
+    gu = torch.empty((cap, 2 * inter), dtype=torch.float16, device=dev)
+    q2 = torch.empty((cap, inter), dtype=torch.int8, device=dev)
+    r2 = torch.empty(cap, dtype=torch.float32, device=dev)
+    y = torch.empty((cap, h), dtype=torch.float16, device=dev)
+    out = torch.empty((t, h), dtype=torch.float16, device=dev)
+    stages = ["route", "sort", "quant", "gate_up", "silu_quant", "down", "combine"]
+
+    def chain(ev=None):
+        mark = (lambda i: ev[i].record()) if ev is not None else (lambda i: None)
+        mark(0)
+        w, ids = w8a8.topk_softmax(logits, k)
+        mark(1)
+        srt = w8a8.moe_sort(ids, e, 32)
+        mark(2)
+        w8a8.moe_smoothquant(x, s, ids, dst_row=srt["dst_row"], rows=cap, out=qa, row_scale=ra)
+        mark(3)
+        w8a8.moe_gemm(qa, wgu, srt["start"], srt["count"], ra, sgu, out=gu)
+        mark(4)
+        w8a8.moe_silu_mul_quant(gu, srt["start"], srt["count"], q=q2, row_scale=r2)
+        mark(5)
+        w8a8.moe_gemm(q2, wd, srt["start"], srt["count"], r2, sd, out=y)
+        mark(6)
+        w8a8.moe_combine(y, w, srt["dst_row"], out=out)
+        mark(7)
+
+    for _ in range(2):
+        chain()
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)]
+           for _ in range(iters)]
+    for i in range(iters):
+        chain(evs[i])
+    torch.cuda.synchronize()
+    per = {st: sum(ev[j].elapsed_time(ev[j + 1]) for ev in evs) / iters * 1e3
+           for j, st in enumerate(stages)}
+    total_us = sum(evs[i][0].elapsed_time(evs[i][-1]) for i in range(iters)) / iters * 1e3
+    rows = t * k
+    ops_gu = 2.0 * rows * 2 * inter * h
+    ops_d = 2.0 * rows * h * inter
+    return {"workload": "cfg5 MoE FFN, Mixtral-8x7B shape: 4096 tokens, hidden 4096, ffn 14336, "
+                        "8 experts, top-2 (routing -> sort -> quant -> gate_up -> SiLU*up requant "
+                        "-> down -> combine)",
+            "us_per_layer": total_us, "TOPS": (ops_gu + ops_d) / (total_us * 1e-6) / 1e12,
+            "stage_us": per,
+            "gate_up_TOPS": ops_gu / (per["gate_up"] * 1e-6) / 1e12,
+            "down_TOPS": ops_d / (per["down"] * 1e-6) / 1e12,
+            "frac_mfma": (ops_gu + ops_d) / (total_us * 1e-6) / PEAK_INT8_OPS}
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
@@ -332,6 +401,8 @@ def main(argv=None) -> int:
         log(json.dumps(extras["gemm_cfg2"]))
         extras["decode_cfg4"] = bench_decode(torch, w8a8, dev, gen)
         log(json.dumps(extras["decode_cfg4"]))
+        extras["moe_cfg5"] = bench_moe(torch, w8a8, dev, gen)
+        log(json.dumps(extras["moe_cfg5"]))
 
     if args.calibrate_copy:
         src = torch.randint(-127, 128, (1 << 30,), generator=gen, device=dev, dtype=torch.int8)

@@ -1,0 +1,91 @@
+// rocwmma_fused_moe -- the MoE expert FFN on MI355X: routing, stable sort,
+// per-expert SmoothQuant straight into expert-sorted rows, gate_up expert GEMM,
+// SiLU(gate)*up requantization, down expert GEMM, weighted combine.
+// Configurations and result line of the reference sample
+// (rocwmma_fused_moe.cpp:227-245):
+//   [FusedMoE] tokens=<T> hidden=<H> inter=<I> experts=<E> topk=<k>  <ms> ms  <TF> TFlops/s
+// FLOPs = 2 * T * k * (2I * H + H * I): each routed row through both GEMMs
+// (the sample counts K_gate_up for both GEMMs and assumes uniform routing, :163-165, :225).
+// `rocwmma_fused_moe [tokens hidden inter experts topk]`.
+#include "common.hpp"
+
+static void test_fused_moe(uint32_t t, uint32_t h, uint32_t inter, uint32_t e, uint32_t k,
+                           bool verify)
+{
+    const uint64_t seed = app::config_seed(5);
+    auto           hx   = app::gen_activations(seed, t, h);
+    auto           hl   = app::gen_normal(seed, app::kLogits, (size_t)t * e);
+    auto           hs   = app::gen_uniform(seed, app::kExpertS, (size_t)e * h, 0.5, 2.0);
+    auto           hwgu = app::gen_int8(seed, app::kB, (size_t)e * 2 * inter * h);
+    auto           hsgu = app::gen_uniform(seed, app::kSb, (size_t)e * 2 * inter, 1e-3, 1e-2);
+    auto           hwd  = app::gen_int8(seed, app::kWDown, (size_t)e * h * inter);
+    auto           hsd  = app::gen_uniform(seed, app::kSbDown, (size_t)e * h, 1e-3, 1e-2);
+    const uint32_t cap  = (uint32_t)w8a8_moe_sort_capacity(t, k, e, 32);
+    app::Dev<uint16_t> dx(hx), gu((size_t)cap * 2 * inter), y((size_t)cap * h), out((size_t)t * h);
+    app::Dev<float>    dl(hl), ds(hs), dsgu(hsgu), dsd(hsd), w((size_t)t * k), ra(cap), r2(cap);
+    app::Dev<int8_t>   dwgu(hwgu), dwd(hwd), qa((size_t)cap * h), q2((size_t)cap * inter);
+    app::Dev<int32_t>  ids((size_t)t * k), cnt(e), st(e + 1), pad(e), srt(cap), dst((size_t)t * k);
+    auto fn = [&] {
+        CHECK_W8A8(w8a8_topk_softmax(dl.p, 0, w.p, ids.p, t, e, k, nullptr));
+        CHECK_W8A8(w8a8_moe_sort(ids.p, t, k, e, 32, cnt.p, st.p, pad.p, srt.p, cap, dst.p, nullptr));
+        CHECK_W8A8(w8a8_moe_smoothquant(dx.p, ds.p, ids.p, qa.p, ra.p, t, h, k, e, 127.f, dst.p,
+                                        cap, nullptr));
+        CHECK_W8A8(w8a8_moe_gemm(e, cap, 2 * inter, h, qa.p, h, dwgu.p, h, (uint64_t)2 * inter * h,
+                                 gu.p, 2 * inter, ra.p, dsgu.p, 1.f, 1.f, st.p, cnt.p,
+                                 W8A8_OUT_F16, nullptr));
+        CHECK_W8A8(w8a8_moe_silu_mul_quant(gu.p, 2 * inter, nullptr, st.p, cnt.p, e, cap, inter,
+                                           q2.p, inter, r2.p, 127.f, nullptr));
+        CHECK_W8A8(w8a8_moe_gemm(e, cap, h, inter, q2.p, inter, dwd.p, inter, (uint64_t)h * inter,
+                                 y.p, h, r2.p, dsd.p, 1.f, 1.f, st.p, cnt.p, W8A8_OUT_F16,
+                                 nullptr));
+        CHECK_W8A8(w8a8_moe_combine(y.p, h, cap, w.p, dst.p, t, k, h, out.p, h, nullptr));
+    };
+    const double ms    = app::bench_ms(fn, 3, 10);
+    const double flops = 2.0 * t * k * (2.0 * inter * h + (double)h * inter);
+    std::cout << "[FusedMoE] tokens=" << t << " hidden=" << h << " inter=" << inter
+              << " experts=" << e << " topk=" << k << "  " << ms << " ms  "
+              << flops / (ms * 1e-3) / 1e12 << " TFlops/s\n";
+    if(verify) { // the two expert GEMMs on sampled rows of every expert, from the GPU's inputs
+        const auto c = cnt.download(), s = st.download();
+        const auto gqa = qa.download(), gq2 = q2.download();
+        const auto gra = ra.download(), gr2 = r2.download();
+        const auto ggu = gu.download(), gy = y.download();
+        size_t     bad = 0;
+        for(uint32_t x = 0; x < e; ++x) {
+            if(c[x] == 0) continue;
+            std::vector<size_t> rows;
+            for(size_t r : app::sample_rows(c[x], 8)) rows.push_back(s[x] + r);
+            const auto a1 = app::cpu_gemm_i32(gqa.data(), hwgu.data() + (size_t)x * 2 * inter * h,
+                                              cap, 2 * inter, h, rows);
+            const auto a2 = app::cpu_gemm_i32(gq2.data(), hwd.data() + (size_t)x * h * inter, cap,
+                                              h, inter, rows);
+            for(size_t ri = 0; ri < rows.size(); ++ri) {
+                for(uint32_t j = 0; j < 2 * inter; ++j)
+                    bad += ggu[rows[ri] * 2 * inter + j]
+                           != app::cpu_dequant(a1[ri * 2 * inter + j], gra[rows[ri]],
+                                               hsgu[(size_t)x * 2 * inter + j]);
+                for(uint32_t j = 0; j < h; ++j)
+                    bad += gy[rows[ri] * h + j]
+                           != app::cpu_dequant(a2[ri * h + j], gr2[rows[ri]], hsd[(size_t)x * h + j]);
+            }
+        }
+        app::report(bad == 0, "expert GEMM mismatches on sampled rows=" + std::to_string(bad));
+    }
+}
+
+int main(int argc, char* argv[])
+{
+    const app::Options o = app::parse(argc, argv);
+    app::banner("W8A8 MoE FFN (MI355X gfx950)");
+    if(o.pos.size() >= 5) {
+        test_fused_moe(std::atoi(o.pos[0].c_str()), std::atoi(o.pos[1].c_str()),
+                       std::atoi(o.pos[2].c_str()), std::atoi(o.pos[3].c_str()),
+                       std::atoi(o.pos[4].c_str()), o.verify);
+        return 0;
+    }
+    test_fused_moe(3328, 4096, 14336, 8, 2, o.verify);
+    test_fused_moe(3328, 4096, 14336, 32, 5, o.verify);
+    test_fused_moe(3328, 7168, 2048, 64, 6, o.verify);
+    test_fused_moe(4096, 4096, 14336, 8, 2, o.verify);
+    return 0;
+}

@@ -101,15 +101,18 @@ def build_apps(debug: bool = False, verbose: bool = False) -> list[Path]:
     if not APPS.is_dir():
         return []
     BIN_DIR.mkdir(exist_ok=True)
-    outs = []
     verify = ["-UNDEBUG", "-DW8A8_CPU_VERIFY=1"] if debug else ["-DNDEBUG"]
-    for src in sorted(APPS.glob("*.cpp")):
+
+    def one(src: Path) -> Path:
         exe = BIN_DIR / src.stem
-        _run([hipcc(), "-x", "hip", *HIP_FLAGS, *verify, "-fopenmp", str(src),
-              "-o", str(exe), f"-L{LIB_DIR}", "-lw8a8", "-Wl,-rpath,$ORIGIN/../lib"],
-             verbose)
-        outs.append(exe)
-    return outs
+        # host-only programs: no device code, so no offload target
+        _run([hipcc(), "-x", "hip", "--offload-host-only", "-std=c++17", "-O3", "-Wall",
+              f"-I{ROOT / 'include'}", *verify, "-fopenmp", str(src), "-o", str(exe),
+              f"-L{LIB_DIR}", "-lw8a8", "-Wl,-rpath,$ORIGIN/../lib"], verbose)
+        return exe
+
+    with cf.ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 4)) as ex:
+        return list(ex.map(one, sorted(APPS.glob("*.cpp"))))
 
 
 def main(argv: list[str] | None = None) -> int:
