@@ -5,7 +5,15 @@
 //   p = float(x[row, n]) * s[n];  r = max|p| / qmax;  inv = r > 0 ? 1/r : 0
 //   q[row, n] = int8(clamp(rint(p * inv), -qmax, qmax))
 //
-// Design (HBM-bound: 3 bytes moved per element):
+// Two kernels, the same per-element operations (bit-identical results):
+//   * sq_stream_kernel (dense rows, 16-byte aligned, N % 8 == 0, N <= 32768):
+//     s staged once per block in LDS, one block per CU walking the rows with
+//     a grid stride and double-buffering them in registers (described at the
+//     kernel);
+//   * sq_rows_kernel / sq_twopass_kernel: everything else (the MoE gather,
+//     unaligned or odd-length rows, very long rows).
+//
+// sq_rows_kernel (HBM-bound: 3 bytes moved per element):
 //   * One wavefront owns a row segment of CPL*512 elements; WPR wavefronts
 //     share a row.  Each lane issues CPL 16-byte loads (8 fp16) so a wave
 //     instruction reads 1 KiB contiguous, and the whole segment is in flight
@@ -18,6 +26,9 @@
 //     contiguous bytes), straight into the row-major A operand of the GEMM.
 #include "w8a8_device.hpp"
 #include "w8a8_internal.hpp"
+
+#include <algorithm>
+#include <mutex>
 
 namespace w8a8 {
 namespace {
@@ -160,6 +171,214 @@ __global__ void __launch_bounds__(kSqThreads) sq_twopass_kernel(QuantRows p)
         qrow[c] = (int8_t)quant_i8(half_bits_to_float(src.x[c]) * src.s[c], inv, p.qmax);
 }
 
+// ---------------------------------------------------------------------------
+// Streaming quantizer for the dense case (aligned rows, N % 8 == 0, N <= 32768).
+//   * s is staged once per block in LDS, permuted so that each ds_read_b128 of
+//     a wave reads 1 KiB contiguous (conflict-free); rows then never re-read
+//     s from L2, and no register holds it.
+//   * A group of WPR waves owns one row at a time (CPL 16-byte chunks per
+//     lane), the block's groups walk the rows with a grid stride, and each
+//     wave loads its next row into a second register buffer while it reduces
+//     and quantizes the current one: HBM reads stay in flight across rows.
+//   * The smoothed values are recomputed from x and the LDS copy of s in the
+//     quantize pass instead of being kept in registers, so a wave holds only
+//     2 x CPL x 4 VGPRs of row data.
+// Results are bit-identical to sq_rows_kernel: same per-element operations.
+// ---------------------------------------------------------------------------
+
+template <int CPL, int WPR, int THREADS>
+__global__ void __launch_bounds__(THREADS) sq_stream_kernel(QuantRows p, uint32_t iters)
+{
+    constexpr int kStreamThreads = THREADS;
+    constexpr int kStreamWaves   = THREADS / kWave;
+    extern __shared__ __attribute__((aligned(16))) float s_lds[]; // kSpan * WPR floats
+    __shared__ float red[2][kStreamWaves];
+    constexpr int      kGroups = kStreamWaves / WPR;
+    static_assert(kStreamWaves % WPR == 0, "whole row groups per block");
+    constexpr int      kSpan   = CPL * 8 * kWave; // columns one wave covers
+    constexpr uint32_t kOobOff = 0x80000000u;     // past every buffer: loads 0, stores dropped
+    const int      wave = threadIdx.x / kWave;
+    const int      lane = threadIdx.x % kWave;
+    const int      grp  = wave / WPR;
+    const int      part = wave % WPR;
+    const uint32_t n    = p.n;
+    const uint32_t base = part * kSpan + lane * 8;
+
+    // Operands through buffer resources: rows past the end and columns past N
+    // use an offset beyond the buffer (loads read 0, stores are dropped), so
+    // the hot loop has no branches and every wave always has exactly CPL loads
+    // per row in flight; the wait before a row is processed then leaves the
+    // next row's loads outstanding.
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(p.x), 0, (int)((p.rows - 1) * p.ldx * 2 + n * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        p.q, 0, (int)((p.rows - 1) * p.ldq + n), 0x00020000);
+
+    uint32_t coff[CPL]; // byte offset of each chunk in a row, or kOobOff
+#pragma unroll
+    for(int j = 0; j < CPL; ++j) {
+        const uint32_t c = base + j * (8 * kWave);
+        coff[j]          = c < n ? c : kOobOff;
+    }
+
+    using Row = v4i[CPL];
+    Row  xa, xb;
+    auto load_row = [&](Row& dst, uint32_t r) {
+        const bool     ok   = r < p.rows;
+        const uint32_t roff = r * p.ldx * 2;
+#pragma unroll
+        for(int j = 0; j < CPL; ++j)
+            dst[j] = __builtin_amdgcn_raw_buffer_load_b128(
+                rx, (ok && coff[j] != kOobOff) ? roff + coff[j] * 2 : kOobOff, 0, 0);
+    };
+    // LDS offset of this lane's s values; made opaque once per row (below) so
+    // the compiler re-reads s from LDS instead of pinning CPL*8 registers to it
+    // for the whole kernel, which would cap the CU at one block
+    uint32_t s_off = (part * kSpan + lane * 4) * 4;
+    auto smoothed = [&](const v4i& raw, int j, float (&v)[8]) {
+        const float4 s0 = *reinterpret_cast<const float4*>(
+            reinterpret_cast<const char*>(s_lds) + s_off + j * 2048);
+        const float4 s1 = *reinterpret_cast<const float4*>(
+            reinterpret_cast<const char*>(s_lds) + s_off + j * 2048 + 1024);
+        v[0] = half_bits_to_float((uint32_t)raw.x & 0xFFFFu) * s0.x;
+        v[1] = half_bits_to_float((uint32_t)raw.x >> 16) * s0.y;
+        v[2] = half_bits_to_float((uint32_t)raw.y & 0xFFFFu) * s0.z;
+        v[3] = half_bits_to_float((uint32_t)raw.y >> 16) * s0.w;
+        v[4] = half_bits_to_float((uint32_t)raw.z & 0xFFFFu) * s1.x;
+        v[5] = half_bits_to_float((uint32_t)raw.z >> 16) * s1.y;
+        v[6] = half_bits_to_float((uint32_t)raw.w & 0xFFFFu) * s1.z;
+        v[7] = half_bits_to_float((uint32_t)raw.w >> 16) * s1.w;
+    };
+    auto process = [&](const Row& x, uint32_t r, int parity) {
+        asm volatile("" : "+v"(s_off));
+        // columns past N hold x = 0 and s = 0: they add nothing to the max
+        float amax = 0.f;
+#pragma unroll
+        for(int j = 0; j < CPL; ++j) {
+            float v[8];
+            smoothed(x[j], j, v);
+#pragma unroll
+            for(int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+        }
+        amax = wave_max(amax);
+        if constexpr(WPR > 1) {
+            if(lane == 0) red[parity][wave] = amax;
+            __syncthreads();
+#pragma unroll
+            for(int w = 0; w < WPR; ++w) amax = fmaxf(amax, red[parity][grp * WPR + w]);
+        }
+        // recompute x*s in the quantize pass rather than keep CPL*8 products live
+        asm volatile("" : "+v"(s_off));
+        const bool  valid = r < p.rows;
+        const float qmax  = p.qmax;
+        const float rs    = amax / qmax;
+        if(valid && part == 0 && lane == 0) p.r[r] = rs;
+        const float    inv  = rs > 0.f ? 1.f / rs : 0.f;
+        const uint32_t qoff = r * p.ldq;
+#pragma unroll
+        for(int j = 0; j < CPL; ++j) {
+            float v[8];
+            smoothed(x[j], j, v);
+            v2i pk;
+            pk.x = (int)pack4_i8(quant_i8(v[0], inv, qmax), quant_i8(v[1], inv, qmax),
+                                 quant_i8(v[2], inv, qmax), quant_i8(v[3], inv, qmax));
+            pk.y = (int)pack4_i8(quant_i8(v[4], inv, qmax), quant_i8(v[5], inv, qmax),
+                                 quant_i8(v[6], inv, qmax), quant_i8(v[7], inv, qmax));
+            __builtin_amdgcn_raw_buffer_store_b64(
+                pk, rq, (valid && coff[j] != kOobOff) ? qoff + coff[j] : kOobOff, 0, 0);
+        }
+    };
+
+    const uint32_t stride = gridDim.x * kGroups;
+    uint32_t       row    = blockIdx.x * kGroups + grp;
+
+    // The first row's loads go out before s is staged, so the two fetches
+    // overlap.  s lands in LDS permuted so that each ds_read_b128 of a wave
+    // reads 1 KiB contiguous (conflict-free): column c = part*kSpan + j*512 +
+    // l*8 + e of a row sits at part*kSpan + j*512 + (e/4)*256 + l*4 + e%4.
+    // Columns past N are stored as 0.
+    load_row(xa, row);
+    {
+        constexpr int kTotal = kSpan * WPR;
+        constexpr int kS4    = (kTotal + kStreamThreads * 4 - 1) / (kStreamThreads * 4);
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(p.s), 0, (int)(n * 4), 0x00020000);
+        v4i sv[kS4];
+#pragma unroll
+        for(int i = 0; i < kS4; ++i) {
+            const uint32_t c4 = (i * kStreamThreads + threadIdx.x) * 4;
+            sv[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, c4 < n ? c4 * 4 : kOobOff, 0, 0);
+        }
+#pragma unroll
+        for(int i = 0; i < kS4; ++i) {
+            const uint32_t c4 = (i * kStreamThreads + threadIdx.x) * 4;
+            if(c4 < (uint32_t)kTotal) {
+                const uint32_t c    = c4 & ~7u;
+                const uint32_t slot = (c / 512) * 512 + ((c4 & 4u) ? 256u : 0u) + ((c % 512) / 8) * 4;
+                *reinterpret_cast<v4i*>(s_lds + slot) = sv[i];
+            }
+        }
+    }
+    __syncthreads();
+
+    // every wave runs the same `iters` steps, so the barriers stay uniform
+    // (sched_barrier: the next row's loads are issued before the wait for the
+    // current row, never sunk below it by the scheduler)
+    for(uint32_t it = 0; it < iters; it += 2) {
+        load_row(xb, row + stride);
+        __builtin_amdgcn_sched_barrier(0);
+        process(xa, row, 0);
+        row += stride;
+        if(it + 1 >= iters) break;
+        load_row(xa, row + stride);
+        __builtin_amdgcn_sched_barrier(0);
+        process(xb, row, 1);
+        row += stride;
+    }
+}
+
+// THREADS per block, BPC resident blocks per CU (the grid is BPC x CUs, each
+// block walking rows with a grid stride).
+template <int CPL, int WPR, int THREADS, int BPC = 1>
+hipError_t launch_stream(const QuantRows& p, hipStream_t stream)
+{
+    constexpr int  kGroups = THREADS / kWave / WPR;
+    const size_t   lds     = (size_t)CPL * 512 * WPR * sizeof(float);
+    static int     max_blocks = [] {
+        int dev = 0, cus = 256;
+        if(hipGetDevice(&dev) == hipSuccess)
+            (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        return cus * BPC;
+    }();
+    if(lds > 65536) {
+        static std::once_flag once;
+        std::call_once(once, [] {
+            (void)hipFuncSetAttribute(
+                reinterpret_cast<const void*>(sq_stream_kernel<CPL, WPR, THREADS>),
+                hipFuncAttributeMaxDynamicSharedMemorySize, 131072);
+            (void)hipGetLastError();
+        });
+    }
+    // x is addressed through a 32-bit buffer offset: launch row panels whose
+    // x span stays under 2 GiB
+    const uint32_t panel = (uint32_t)std::min<uint64_t>(p.rows, 0x7FFFFFFFull / ((uint64_t)p.ldx * 2));
+    for(uint32_t r0 = 0; r0 < p.rows; r0 += panel) {
+        QuantRows q = p;
+        q.rows      = std::min(panel, p.rows - r0);
+        q.x         = p.x + (size_t)r0 * p.ldx;
+        q.q         = p.q + (size_t)r0 * p.ldq;
+        q.r         = p.r + r0;
+        const uint32_t need   = (q.rows + kGroups - 1) / kGroups;
+        const uint32_t blocks = std::max<uint32_t>(1, std::min<uint32_t>(need, (uint32_t)max_blocks));
+        const uint32_t iters  = (q.rows + blocks * kGroups - 1) / (blocks * kGroups);
+        hipLaunchKernelGGL((sq_stream_kernel<CPL, WPR, THREADS>), dim3(blocks), dim3(THREADS), lds,
+                           stream, q, iters);
+        const hipError_t e = hipGetLastError();
+        if(e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 template <int CPL, int WPR, bool MOE>
 hipError_t launch_rows(const QuantRows& p, bool vec, hipStream_t stream)
 {
@@ -182,6 +401,20 @@ hipError_t dispatch(const QuantRows& p, hipStream_t stream)
                      && (reinterpret_cast<uintptr_t>(p.s) % 16 == 0) && (!MOE || p.n % 4 == 0)
                      && (reinterpret_cast<uintptr_t>(p.q) % 8 == 0) && (p.ldq % 8 == 0);
     const uint32_t n = p.n;
+    if constexpr(!MOE) {
+        // aligned dense rows: the streaming kernel (s in LDS, rows double-buffered)
+        if(vec && n % 8 == 0) {
+            // (configurations chosen by a sweep on MI355X over CPL, WPR,
+            // block size and blocks per CU, cache-warm and cache-cold)
+            if(n <= 512) return launch_stream<1, 1, 512>(p, stream);
+            if(n <= 1024) return launch_stream<2, 1, 512>(p, stream);
+            if(n <= 2048) return launch_stream<4, 1, 512>(p, stream);
+            if(n <= 4096) return launch_stream<4, 2, 512>(p, stream);
+            if(n <= 8192) return launch_stream<4, 4, 512, 2>(p, stream);
+            if(n <= 16384) return launch_stream<8, 4, 512>(p, stream);
+            if(n <= 32768) return launch_stream<4, 16, 1024>(p, stream);
+        }
+    }
     if(n <= 512) return launch_rows<1, 1, MOE>(p, vec, stream);
     if(n <= 1024) return launch_rows<2, 1, MOE>(p, vec, stream);
     if(n <= 2048) return launch_rows<4, 1, MOE>(p, vec, stream);
