@@ -71,17 +71,19 @@ __global__ void __launch_bounds__(256) pack_weights_kernel(const int8_t* __restr
     reinterpret_cast<int4*>(out)[idx] = v;
 }
 
-template <int BM_, int STAGES_, int DIST_, int GROUP_M_ = 8>
+template <int BM_, int STAGES_, int DIST_, int GROUP_M_ = 8, int WAVES_M_ = 1>
 struct PbCfg {
     static constexpr int kBM      = BM_;
-    static constexpr int kBN      = 4 * kSlab; // 4 waves x one slab each
+    static constexpr int kBN      = 4 * kSlab; // 4 waves along N x one slab each
     static constexpr int kBK      = kPackK;
     static constexpr int kStages  = STAGES_;
     static constexpr int kDist    = DIST_;    // B prefetch distance in k-tiles
     static constexpr int kGroupM  = GROUP_M_;
-    static constexpr int kWaves   = 4;
+    static constexpr int kWavesM  = WAVES_M_; // waves along M, BM / WAVES_M rows each
+    static constexpr int kWaves   = 4 * kWavesM;
     static constexpr int kThreads = kWaves * kWave;
-    static constexpr int kTilesM  = kBM / 32;
+    static constexpr int kWaveM   = kBM / kWavesM;
+    static constexpr int kTilesM  = kWaveM / 32;
     static constexpr int kTilesN  = kSlab / 32; // 2
     static constexpr int kChunks  = kBK / 16;   // 8 chunks per LDS row
     static constexpr int kSwzShift = 1;         // swizzle = (row >> 1) & 7
@@ -94,6 +96,8 @@ struct PbCfg {
     static constexpr int kRing    = kDist + 1;                   // B register buffers
 
     static_assert(kLoadsA * kWaves * 1024 == kStageBytes, "A tile splits into wave-loads");
+    static_assert(kWaveM % 32 == 0, "wave rows made of 32-row MFMA tiles");
+    static_assert(kRing == 2 || kRing == 3, "B ring depth");
     static_assert(kLdsBytes <= 160 * 1024, "gfx950 LDS per workgroup");
     static_assert(kLoadsA * (kStages - 1) + kLoadsB * (kDist + 1) < 64, "vmcnt range");
 };
@@ -113,6 +117,8 @@ __global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_pb_kernel(KArgs p, int
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int lane = threadIdx.x % kWave;
+    const int wm   = wave / 4; // rows wm*kWaveM ...
+    const int wn   = wave % 4; // slab n0/64 + wn
     const uint32_t nkt = packed_ktiles(p.k);
 
     // ---- A: global -> LDS (swizzled rows of 128 bytes) --------------------
@@ -142,7 +148,7 @@ __global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_pb_kernel(KArgs p, int
     };
 
     // ---- B: packed weights -> VGPR ring ------------------------------------
-    const uint32_t slab = n0 / kSlab + wave;
+    const uint32_t slab = n0 / kSlab + wn;
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<int8_t*>(p.b), 0, (int)packed_bytes(p.n, p.k), kBufferFlags);
     const uint32_t vbl = slab * nkt * (kPackFrags * 1024) + lane * 16; // per-lane offset
@@ -164,7 +170,7 @@ __global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_pb_kernel(KArgs p, int
     const int fswz = (frow >> C::kSwzShift) & (C::kChunks - 1);
     int       offa[C::kTilesM];
 #pragma unroll
-    for(int t = 0; t < C::kTilesM; ++t) offa[t] = (t * 32 + frow) * C::kBK;
+    for(int t = 0; t < C::kTilesM; ++t) offa[t] = (wm * C::kWaveM + t * 32 + frow) * C::kBK;
     int cofs[C::kSubK];
 #pragma unroll
     for(int g = 0; g < C::kSubK; ++g) cofs[g] = ((2 * g + (lane >> 5)) ^ fswz) * 16;
@@ -230,32 +236,39 @@ __global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_pb_kernel(KArgs p, int
         interleave_mfma_vmem_ds<kMfma, C::kLoadsA + C::kLoadsB, C::kTilesM, 1>();
     };
 
-    static_assert(C::kRing == 3, "loop body below is unrolled for a 3-deep B ring");
     uint32_t kt = 0;
-    for(; kt + 3 <= nkt; kt += 3) {
-        step(kt + 0, bq[0], bq[2]);
-        step(kt + 1, bq[1], bq[0]);
-        step(kt + 2, bq[2], bq[1]);
+    if constexpr(C::kRing == 3) {
+        for(; kt + 3 <= nkt; kt += 3) {
+            step(kt + 0, bq[0], bq[2]);
+            step(kt + 1, bq[1], bq[0]);
+            step(kt + 2, bq[2], bq[1]);
+        }
+        if(kt < nkt) step(kt, bq[0], bq[2]);
+        if(kt + 1 < nkt) step(kt + 1, bq[1], bq[0]);
+    } else {
+        for(; kt + 2 <= nkt; kt += 2) {
+            step(kt + 0, bq[0], bq[1]);
+            step(kt + 1, bq[1], bq[0]);
+        }
+        if(kt < nkt) step(kt, bq[0], bq[1]);
     }
-    if(kt < nkt) step(kt, bq[0], bq[2]);
-    if(kt + 1 < nkt) step(kt + 1, bq[1], bq[0]);
     wait_vmcnt<0>(); // no global->LDS write may outlive the workgroup's LDS
 
     // ---- epilogue ----------------------------------------------------------
-    // acc[i][j][r]: m = m0 + i*32 + lane%32,
-    //               n = n0 + wave*64 + j*32 + (r/4)*8 + (lane/32)*4 + r%4.
+    // acc[i][j][r]: m = m0 + wm*kWaveM + i*32 + lane%32,
+    //               n = n0 + wn*64 + j*32 + (r/4)*8 + (lane/32)*4 + r%4.
     const bool  mode1 = (p.sa == nullptr && p.sb == nullptr);
     const float ab    = p.tsa * p.tsb;
 #pragma unroll
     for(int i = 0; i < C::kTilesM; ++i) {
-        const uint32_t m  = m0 + i * 32 + (lane & 31);
+        const uint32_t m  = m0 + wm * C::kWaveM + i * 32 + (lane & 31);
         float          sa = p.tsa;
         if(OUT == W8A8_OUT_F16 && p.sa != nullptr && m < p.m) sa = p.sa[m];
 #pragma unroll
         for(int j = 0; j < C::kTilesN; ++j) {
 #pragma unroll
             for(int g = 0; g < 4; ++g) {
-                const uint32_t n  = n0 + wave * kSlab + j * 32 + g * 8 + (lane >> 5) * 4;
+                const uint32_t n  = n0 + wn * kSlab + j * 32 + g * 8 + (lane >> 5) * 4;
                 float4         sb = make_float4(p.tsb, p.tsb, p.tsb, p.tsb);
                 if(OUT == W8A8_OUT_F16 && p.sb != nullptr) {
                     if(vec_ok && n + 4 <= p.n)
