@@ -170,6 +170,40 @@ def bench_quantizer_sweep(torch, w8a8, dev, gen):
     return out
 
 
+def bench_rmsnorm_sq(torch, w8a8, dev, gen, iters=12):
+    """Add+RMSNorm fused with the quantizer at the cfg3 token count: the
+    residual stream x + res -> x_out and the int8 A operand of the next GEMM
+    (q, row scale), M = 8192 rows of hidden 4096.  Three buffer sets (700 MB)
+    used in turn, so every launch reads HBM; the unfused chain (Add+RMSNorm
+    writing fp16 y, then the quantizer reading it) is timed the same way."""
+    m, n = 8192, 4096
+    sets = []
+    for _ in range(3):
+        x = torch.randn((m, n), generator=gen, device=dev).to(torch.float16)
+        r = torch.randn((m, n), generator=gen, device=dev).to(torch.float16)
+        sets.append((x, r, torch.empty_like(x), torch.empty((m, n), dtype=torch.int8, device=dev),
+                     torch.empty(m, dtype=torch.float32, device=dev)))
+    g = torch.rand(n, generator=gen, device=dev) + 0.5
+    s = torch.rand(n, generator=gen, device=dev) * 1.5 + 0.5
+    y = torch.empty((m, n), dtype=torch.float16, device=dev)
+
+    def fused(b):
+        w8a8.add_rmsnorm_smoothquant(b[0], g, s, residual=b[1], x_out=b[2], q=b[3], row_scale=b[4])
+
+    def chain(b):
+        w8a8.add_rmsnorm_smoothquant(b[0], g, residual=b[1], x_out=b[2], y=y)
+        w8a8.smoothquant(y, s, out=b[3], row_scale=b[4])
+
+    t_fused = graph_us(torch, [(lambda b=sets[i % 3]: fused(b)) for i in range(iters)])
+    t_chain = graph_us(torch, [(lambda b=sets[i % 3]: chain(b)) for i in range(iters)])
+    nbytes = 2 * m * n * 3 + m * n + 4 * m + 8 * n  # x, res in; x_out, q, r out; gamma, s
+    return {"workload": "Add+RMSNorm -> SmoothQuant, M=8192 hidden=4096 (Llama-3-8B layer input)",
+            "bytes_per_launch": nbytes, "us_per_launch": t_fused,
+            "GBps": nbytes / (t_fused * 1e-6) / 1e9,
+            "frac_hbm": nbytes / (t_fused * 1e-6) / PEAK_HBM_BPS,
+            "unfused_chain_us": t_chain, "speedup_vs_unfused": t_chain / t_fused}
+
+
 def bench_gemm_4096(torch, w8a8, dev, gen, iters=20):
     m = n = k = 4096
     a = torch.randint(-127, 128, (m, k), generator=gen, device=dev, dtype=torch.int8)
@@ -432,6 +466,8 @@ def main(argv=None) -> int:
         log(json.dumps(extras["smoothquant_cfg1"]))
         extras["smoothquant_sweep"] = bench_quantizer_sweep(torch, w8a8, dev, gen)
         log(json.dumps(extras["smoothquant_sweep"]))
+        extras["rmsnorm_smoothquant"] = bench_rmsnorm_sq(torch, w8a8, dev, gen)
+        log(json.dumps(extras["rmsnorm_smoothquant"]))
         extras["gemm_cfg2"] = bench_gemm_4096(torch, w8a8, dev, gen)
         log(json.dumps(extras["gemm_cfg2"]))
         extras["decode_cfg4"] = bench_decode(torch, w8a8, dev, gen)

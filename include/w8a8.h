@@ -87,6 +87,35 @@ int w8a8_moe_smoothquant(const void* x, const float* smooth_scale, const int32_t
                          uint32_t topk, uint32_t experts, float quant_max,
                          const int32_t* dst_row, uint32_t rows_out, hipStream_t stream);
 
+/*
+ * RMSNorm, optionally after a residual add, fused with the quantizer: the
+ * normalised row goes to int8 + row scale without an fp16 round trip through
+ * HBM.  Replaces kernel_add_rmsnorm2d_fwd (rocwmma_rmsnorm2d.cpp:127-186) or,
+ * with residual = NULL, kernel_rmsnorm2d_fwd (:57-120), followed by
+ * kernel_smoothquant (rocwmma_smoothquant.cpp:58-122) on their fp16 output.
+ *   x, residual  fp16 [M, ldx]    (ldx = 0 means N; residual NULL = plain RMSNorm)
+ *   gamma        fp32 [N]
+ *   smooth_scale fp32 [N], or NULL for no quantization (q, row_scale NULL too)
+ *   x_out        fp16 [M, ldx] = half(x + residual), or NULL; needs a residual;
+ *                may be x or residual itself (updated in place)
+ *   y            fp16 [M, ldy] normalised row (ldy = 0 means N), or NULL
+ *   q, row_scale int8 [M, ldq] (ldq = 0 means N), fp32 [M]
+ *   eps >= 0 (the reference uses 1e-5), quant_max in (0, 127]
+ * Per row, in fp32:
+ *   v = float(x) [+ float(residual)];  rstd = rsqrt(sum_n v^2 / N + eps)
+ *   u = residual ? float(half(v)) : v  (the reference normalises the saved sum, :173-182)
+ *   y = half((u * rstd) * gamma[n]);   q, row_scale = quantizer(y, smooth_scale)
+ * At least one of x_out, y, q must be given.  The sum of squares is an fp32
+ * sum in this kernel's order, so y may differ from the reference's by one
+ * fp16 ulp where the two sums round differently; q and row_scale are exactly
+ * w8a8_smoothquant of this call's y.
+ */
+int w8a8_add_rmsnorm_smoothquant(const void* x, const void* residual, const float* gamma,
+                                 const float* smooth_scale, void* x_out, void* y, int8_t* q,
+                                 float* row_scale, uint32_t M, uint32_t N, float eps,
+                                 float quant_max, uint32_t ldx, uint32_t ldy, uint32_t ldq,
+                                 hipStream_t stream);
+
 /* ------------------------------------------------------------------------- */
 /* int8 GEMM with fused dequant                                               */
 /* ------------------------------------------------------------------------- */

@@ -35,7 +35,8 @@ __all__ = [
     "library", "version", "smoothquant", "moe_smoothquant", "gemm", "gemm_workspace_size",
     "fused_sq_gemm", "W8A8Error", "PackedWeights", "pack_weights", "pack_weights_size",
     "gemm_packed", "fused_sq_gemm_packed", "grouped_gemm", "topk_softmax", "moe_sort",
-    "moe_gemm", "moe_silu_mul_quant", "moe_combine", "moe_ffn",
+    "moe_gemm", "moe_silu_mul_quant", "moe_combine", "moe_ffn", "add_rmsnorm_smoothquant",
+    "rmsnorm", "add_rmsnorm",
 ]
 
 
@@ -87,6 +88,75 @@ def smoothquant(x, smooth_scale, quant_max: float = 127.0, out=None, row_scale=N
     _lib.call("w8a8_smoothquant", _ptr(x), _ptr(smooth_scale.contiguous()), _ptr(q), _ptr(r),
               m, n, float(quant_max), x.stride(0), q.stride(0), _stream(x.device))
     return q, r
+
+
+def _rows2d(name, t, n=None):
+    torch = _torch()
+    if t.dim() != 2 or t.dtype != torch.float16 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be a 2-D fp16 tensor with unit column stride")
+    if n is not None and t.shape[1] != n:
+        raise ValueError(f"{name} must have {n} columns")
+
+
+def add_rmsnorm_smoothquant(x, gamma, smooth_scale=None, residual=None, eps: float = 1e-5,
+                            quant_max: float = 127.0, x_out=None, want_y: bool = False,
+                            y=None, q=None, row_scale=None):
+    """RMSNorm of x (after `x + residual` when a residual is given) fused with
+    the quantizer.
+
+    Returns (x_out, y, q, row_scale); entries not requested are None.  x_out
+    (= half(x + residual)) is produced when a residual is given; pass
+    x_out=x (or =residual) to update in place.  y (the fp16 normalised row)
+    is produced when want_y or y is given; q / row_scale when smooth_scale is
+    given.  x, residual and x_out must share one row stride.
+    """
+    torch = _torch()
+    _require_cuda(x, gamma, smooth_scale, residual, x_out, y, q, row_scale)
+    _rows2d("x", x)
+    m, n = x.shape
+    if gamma.dtype != torch.float32 or gamma.numel() != n:
+        raise ValueError("gamma must be fp32 with N elements")
+    if residual is not None:
+        _rows2d("residual", residual, n)
+        if residual.shape != x.shape or residual.stride(0) != x.stride(0):
+            raise ValueError("residual must match x in shape and row stride")
+        if x_out is None:
+            x_out = torch.empty_like(x)
+        _rows2d("x_out", x_out, n)
+        if x_out.shape != x.shape or x_out.stride(0) != x.stride(0):
+            raise ValueError("x_out must match x in shape and row stride")
+    elif x_out is not None:
+        raise ValueError("x_out needs a residual")
+    if want_y and y is None:
+        y = torch.empty((m, n), dtype=torch.float16, device=x.device)
+    if y is not None:
+        _rows2d("y", y, n)
+    if smooth_scale is not None:
+        if smooth_scale.dtype != torch.float32 or smooth_scale.numel() != n:
+            raise ValueError("smooth_scale must be fp32 with N elements")
+        if q is None:
+            q = torch.empty((m, n), dtype=torch.int8, device=x.device)
+        if row_scale is None:
+            row_scale = torch.empty(m, dtype=torch.float32, device=x.device)
+        smooth_scale = smooth_scale.contiguous()
+    else:
+        q = row_scale = None
+    _lib.call("w8a8_add_rmsnorm_smoothquant", _ptr(x), _ptr(residual), _ptr(gamma.contiguous()),
+              _ptr(smooth_scale), _ptr(x_out), _ptr(y), _ptr(q), _ptr(row_scale), m, n,
+              float(eps), float(quant_max), x.stride(0), y.stride(0) if y is not None else 0,
+              q.stride(0) if q is not None else 0, _stream(x.device))
+    return x_out, y, q, row_scale
+
+
+def rmsnorm(x, gamma, eps: float = 1e-5):
+    """fp16 RMSNorm y = half((x * rstd) * gamma) (kernel_rmsnorm2d_fwd's output)."""
+    return add_rmsnorm_smoothquant(x, gamma, eps=eps, want_y=True)[1]
+
+
+def add_rmsnorm(x, residual, gamma, eps: float = 1e-5):
+    """(x_out, y) of kernel_add_rmsnorm2d_fwd: x_out = half(x + residual), y = RMSNorm(x_out)."""
+    x_out, y, _, _ = add_rmsnorm_smoothquant(x, gamma, residual=residual, eps=eps, want_y=True)
+    return x_out, y
 
 
 def moe_smoothquant(x, smooth_scale, topk_ids, quant_max: float = 127.0, dst_row=None,

@@ -46,6 +46,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "w8a8_smoothquant": (_i32, [_ptr, _ptr, _ptr, _ptr, _u32, _u32, _f32, _u32, _u32, _ptr]),
     "w8a8_moe_smoothquant": (_i32, [_ptr, _ptr, _ptr, _ptr, _ptr, _u32, _u32, _u32, _u32, _f32,
                                     _ptr, _u32, _ptr]),
+    "w8a8_add_rmsnorm_smoothquant": (_i32, [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _u32,
+                                            _u32, _f32, _f32, _u32, _u32, _u32, _ptr]),
     "w8a8_gemm_workspace_size": (_size, [_u32, _u32, _u32, _i32]),
     "w8a8_gemm": (_i32, [_u32, _u32, _u32, _ptr, _ptr, _ptr, _u32, _u32, _u32, _ptr, _ptr, _f32,
                          _f32, _i32, _i32, _ptr, _size, _ptr]),

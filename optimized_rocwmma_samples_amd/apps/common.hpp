@@ -125,7 +125,7 @@ struct Dev {
 // h(seed, tid, i) = splitmix64 finalizer of (seed ^ tid << 56) + (i + 1) * golden
 enum Tid : uint64_t {
     kX = 1, kS = 2, kOutlier = 3, kA = 4, kB = 5, kSa = 6, kSb = 7, kLogits = 8, kExpertS = 9,
-    kWDown = 10, kSbDown = 11
+    kWDown = 10, kSbDown = 11, kResidual = 12, kGamma = 13
 };
 
 inline uint64_t h64(uint64_t seed, uint64_t tid, uint64_t i)

@@ -64,6 +64,7 @@ declare -a ALL_SAMPLES=(
     "rocwmma_smoothquant|3328 8192|SmoothQuant FP16->INT8 N=8192"
     "rocwmma_smoothquant|2048 4096|SmoothQuant config 1 (2048x4096)"
     "rocwmma_moe_smoothquant||MoE SmoothQuant (per-expert scale)"
+    "rocwmma_rmsnorm2d|3328 4096|RMSNorm2D + Add+RMSNorm fused (+ SmoothQuant)"
     "rocwmma_gemm_quantized||W8A8 int8 GEMM (per-token x per-channel dequant)"
     "rocwmma_gemm_quantized|--sample-layout|W8A8 int8 GEMM, sample layout + tensor scales"
     "w8a8_fused_sq_gemm||Fused SmoothQuant + GEMM, Llama-3-8B projections"

@@ -37,6 +37,7 @@ SOURCES = [
     "smoothquant.hip",
     "gemm_i8.hip",
     "moe.hip",
+    "rmsnorm_sq.hip",
 ]
 
 # -packed-fp32-ops: keep the compiler from emitting packed fp32 VALU ops.

@@ -113,6 +113,58 @@ int w8a8_moe_smoothquant(const void* x, const float* smooth_scale, const int32_t
     return hip_status(w8a8::launch_smoothquant(p, stream), "w8a8_moe_smoothquant");
 }
 
+int w8a8_add_rmsnorm_smoothquant(const void* x, const void* residual, const float* gamma,
+                                 const float* smooth_scale, void* x_out, void* y, int8_t* q,
+                                 float* row_scale, uint32_t M, uint32_t N, float eps,
+                                 float quant_max, uint32_t ldx, uint32_t ldy, uint32_t ldq,
+                                 hipStream_t stream)
+{
+    const char* fn = "w8a8_add_rmsnorm_smoothquant";
+    if(!x || !gamma) return fail(W8A8_ERROR_INVALID_VALUE, "%s: x and gamma must be given", fn);
+    if(M == 0 || N == 0 || M > 0x7FFFFFFFu)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: M and N must be > 0, M < 2^31 (M=%u N=%u)", fn,
+                    M, N);
+    const bool quant = smooth_scale || q || row_scale;
+    if(quant && !(smooth_scale && q && row_scale))
+        return fail(W8A8_ERROR_INVALID_VALUE,
+                    "%s: smooth_scale, q and row_scale must be given together", fn);
+    if(x_out && !residual)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: x_out needs a residual", fn);
+    if(!x_out && !y && !quant)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: no output requested", fn);
+    if(!(std::isfinite(eps) && eps >= 0.f))
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: eps must be finite and >= 0, got %g", fn,
+                    (double)eps);
+    if(quant && !valid_qmax(quant_max))
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: quant_max must be in (0, 127], got %g", fn,
+                    (double)quant_max);
+    if(ldx == 0) ldx = N;
+    if(ldy == 0) ldy = N;
+    if(ldq == 0) ldq = N;
+    if(ldx < N || ldy < N || ldq < N)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: ldx=%u / ldy=%u / ldq=%u smaller than N=%u",
+                    fn, ldx, ldy, ldq, N);
+    if((uint64_t)ldx * 2 > 0x7FFFFFFFull || (uint64_t)ldy * 2 > 0x7FFFFFFFull)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: a row must stay under 2 GiB", fn);
+    w8a8::NormRows p{};
+    p.x     = static_cast<const uint16_t*>(x);
+    p.res   = static_cast<const uint16_t*>(residual);
+    p.gamma = gamma;
+    p.s     = smooth_scale;
+    p.x_out = static_cast<uint16_t*>(x_out);
+    p.y     = static_cast<uint16_t*>(y);
+    p.q     = q;
+    p.r     = row_scale;
+    p.rows  = M;
+    p.n     = N;
+    p.ldx   = ldx;
+    p.ldy   = ldy;
+    p.ldq   = ldq;
+    p.eps   = eps;
+    p.qmax  = quant ? quant_max : 127.f;
+    return hip_status(w8a8::launch_rmsnorm_sq(p, stream), fn);
+}
+
 static uint32_t round_up16(uint32_t v) { return (v + 15u) & ~15u; }
 
 size_t w8a8_gemm_workspace_size(uint32_t m, uint32_t n, uint32_t k, int layout)

@@ -41,6 +41,22 @@ __device__ __forceinline__ float wave_max(float v)
     return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
+// Sum over all 64 lanes in a fixed order (quad butterflies, half-row and row
+// mirrors, then the four row totals left to right); the result is
+// wave-uniform and the same on every call for the same inputs.
+__device__ __forceinline__ float wave_sum(float v)
+{
+    v += dpp_mov<kDppQuadXor1>(v);
+    v += dpp_mov<kDppQuadXor2>(v);
+    v += dpp_mov<kDppRowHalfMirror>(v);
+    v += dpp_mov<kDppRowMirror>(v);
+    float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return ((r0 + r1) + r2) + r3;
+}
+
 __device__ __forceinline__ float half_bits_to_float(uint32_t h16)
 {
     _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)h16);
@@ -51,6 +67,17 @@ __device__ __forceinline__ uint16_t float_to_half_bits(float f)
 {
     _Float16 h = (_Float16)f; // v_cvt_f16_f32, round to nearest even
     return __builtin_bit_cast(uint16_t, h);
+}
+
+// fp16 of an fp32 result, rounded in two IEEE steps: the producing operation
+// rounds to fp32, then the conversion rounds to fp16.  The empty asm makes the
+// fp32 value opaque, so the compiler cannot fold the producing multiply or add
+// into a mixed-precision FMA that rounds to fp16 once (which differs where the
+// fp32 result lands exactly between two fp16 values).
+__device__ __forceinline__ uint16_t float_to_half_bits_2step(float f)
+{
+    asm("" : "+v"(f));
+    return float_to_half_bits(f);
 }
 
 // int8 quantization of one smoothed value (reference order: (x*s)*inv, rint,

@@ -30,6 +30,23 @@ struct QuantRows {
 
 hipError_t launch_smoothquant(const QuantRows& p, hipStream_t stream);
 
+// RMSNorm (+ residual add) fused with the quantizer (rmsnorm_sq.hip).  x,
+// residual and x_out share the row stride ldx; residual, x_out, y, s, q and r
+// may be NULL as w8a8_add_rmsnorm_smoothquant documents.
+struct NormRows {
+    const uint16_t* x;
+    const uint16_t* res;
+    const float*    gamma;
+    const float*    s;
+    uint16_t*       x_out;
+    uint16_t*       y;
+    int8_t*         q;
+    float*          r;
+    uint32_t        rows, n, ldx, ldy, ldq;
+    float           eps, qmax;
+};
+hipError_t launch_rmsnorm_sq(const NormRows& p, hipStream_t stream);
+
 struct GemmArgs {
     uint32_t       m, n, k;
     const int8_t*  a;

@@ -24,6 +24,7 @@ _M2 = np.uint64(0x94D049BB133111EB)
 
 TID_X, TID_S, TID_OUTLIER, TID_A, TID_B, TID_SA, TID_SB = 1, 2, 3, 4, 5, 6, 7
 TID_LOGITS, TID_EXPERT_S, TID_W_DOWN, TID_SB_DOWN = 8, 9, 10, 11
+TID_RESIDUAL, TID_GAMMA = 12, 13  # RMSNorm residual stream and weight
 
 _CHUNK = 1 << 22
 
@@ -112,3 +113,12 @@ def activations(seed: int, m: int, k: int, outlier_frac: float = 0.005,
         z[:, cols] *= outlier_scale
         out[r0:r1] = z.astype(np.float16)
     return out
+
+
+def rmsnorm_inputs(seed: int, m: int, n: int):
+    """RMSNorm inputs: x activation-like fp16 [m, n] (outlier columns included),
+    residual N(0,1) fp16 [m, n], gamma fp32 U[0.5, 1.5] [n]."""
+    x = activations(seed, m, n)
+    res = normal(seed, TID_RESIDUAL, (m, n))
+    gamma = uniform(seed, TID_GAMMA, (n,), 0.5, 1.5)
+    return x, res, gamma

@@ -34,6 +34,12 @@ int ref_kernel_topk_softmax(const void* logits_f16, float* w, int32_t* idx, uint
 int ref_moe_sorting(const int32_t* ids, uint32_t tokens, uint32_t topk, uint32_t experts,
                     uint32_t unit_size, int32_t* count, int32_t* start, int32_t* padded,
                     int32_t* sorted, int32_t* scatter_ws);
+/* kernel_rmsnorm2d_fwd (rocwmma_rmsnorm2d.cpp:57-120), grid(M) x 256 as at :215-217. */
+int ref_kernel_rmsnorm2d(const void* x, const float* gamma, void* y, uint32_t M, uint32_t N,
+                         uint32_t ldx, uint32_t ldy, float eps);
+/* kernel_add_rmsnorm2d_fwd (rocwmma_rmsnorm2d.cpp:127-186), grid(M) x 256 as at :243-245. */
+int ref_kernel_add_rmsnorm2d(const void* x, const void* residual, const float* gamma, void* y,
+                             void* x_out, uint32_t M, uint32_t N, float eps);
 #ifdef __cplusplus
 }
 #endif

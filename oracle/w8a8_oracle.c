@@ -124,6 +124,51 @@ void w8a8o_moe_smoothquant(const uint16_t* x, const float* s, const int32_t* top
 }
 
 /* ------------------------------------------------------------------------- */
+/* RMSNorm (+ residual) -> quantizer                                          */
+/* ------------------------------------------------------------------------- */
+void w8a8o_rmsnorm_smoothquant(const uint16_t* x, const uint16_t* res, const float* gamma,
+                               const float* s, uint16_t* x_out, uint16_t* y, int8_t* q,
+                               float* r, uint32_t M, uint32_t N, float eps, float quant_max,
+                               uint32_t ldx, uint32_t ldy, uint32_t ldq)
+{
+#pragma omp parallel
+    {
+        float*    v  = (float*)malloc(sizeof(float) * N);
+        uint16_t* yh = (uint16_t*)malloc(sizeof(uint16_t) * N);
+#pragma omp for schedule(static)
+        for(long m = 0; m < (long)M; ++m) {
+            const uint16_t* xr = x + (size_t)m * ldx;
+            const uint16_t* rr = res ? res + (size_t)m * ldx : NULL;
+            /* :157-160 / :79-80: v = x (+ residual) in fp32; squares summed */
+            double ss = 0.0;
+            for(uint32_t n = 0; n < N; ++n) {
+                v[n] = w8a8o_half_to_float(xr[n]);
+                if(rr) v[n] += w8a8o_half_to_float(rr[n]);
+                ss += (double)v[n] * (double)v[n];
+            }
+            /* :170 / :99: rstd = rsqrt(sum / N + eps), each step in fp32 */
+            const float mean = (float)ss / (float)N;
+            const float rstd = (float)(1.0 / sqrt((double)(mean + eps)));
+            for(uint32_t n = 0; n < N; ++n) {
+                float u = v[n];
+                if(rr) {
+                    /* :159 x_out = half(v); :173-180 normalises the saved x_out */
+                    const uint16_t h = w8a8o_float_to_half(v[n]);
+                    if(x_out) x_out[(size_t)m * ldx + n] = h;
+                    u = w8a8o_half_to_float(h);
+                }
+                /* :182 / :112: f * rstd * gamma, rounded to fp16 */
+                yh[n] = w8a8o_float_to_half((u * rstd) * gamma[n]);
+                if(y) y[(size_t)m * ldy + n] = yh[n];
+            }
+            if(q) quant_row(yh, s, N, quant_max, q + (size_t)m * ldq, &r[m]);
+        }
+        free(v);
+        free(yh);
+    }
+}
+
+/* ------------------------------------------------------------------------- */
 /* int8 GEMM (gemm_cpu_h semantics)                                           */
 /* ------------------------------------------------------------------------- */
 void w8a8o_gemm_i8_i32(uint32_t M, uint32_t N, uint32_t K,

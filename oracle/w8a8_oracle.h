@@ -55,6 +55,29 @@ void w8a8o_moe_smoothquant(const uint16_t* x, const float* s, const int32_t* top
                            uint32_t tokens, uint32_t hidden, uint32_t topk,
                            uint32_t experts, float quant_max, const int32_t* dst_row);
 
+/*
+ * RMSNorm, optionally after a residual add, then the quantizer on its fp16
+ * output.  Restates kernel_add_rmsnorm2d_fwd (rocwmma_rmsnorm2d.cpp:127-186)
+ * or, with res == NULL, kernel_rmsnorm2d_fwd (:57-120), followed by
+ * kernel_smoothquant:
+ *   v[n]   = float(x[m,n]) (+ float(res[m,n]))            (:157-158 / :79-80)
+ *   x_out  = half(v)                                      (:159)
+ *   rstd   = rsqrt(float(sum_n v^2) / N + eps)            (:170 / :99)
+ *   u[n]   = res ? float(x_out[m,n]) : v[n]               (:173-180)
+ *   y[m,n] = half((u * rstd) * gamma[n])                  (:182 / :112)
+ *   q, r   = w8a8o_smoothquant(y, s)                      (when q != NULL)
+ * The sum of squares is taken in float64 (the reference sums in fp32 in its
+ * thread and wave order, which no CPU order reproduces) and the reciprocal
+ * square root is correctly rounded (the reference's rsqrtf is the GPU's).
+ * Where the reference's N % 2048 != 0 tail loop counts columns twice
+ * (kernel_rmsnorm2d_fwd, :83-85 after :74-82) this restates the intended sum.
+ * x_out, y, q may each be NULL; x, res, x_out share ldx.
+ */
+void w8a8o_rmsnorm_smoothquant(const uint16_t* x, const uint16_t* res, const float* gamma,
+                               const float* s, uint16_t* x_out, uint16_t* y, int8_t* q,
+                               float* r, uint32_t M, uint32_t N, float eps, float quant_max,
+                               uint32_t ldx, uint32_t ldy, uint32_t ldq);
+
 /* Operand layouts of the int8 GEMM. */
 enum {
     W8A8O_LAYOUT_A_ROW_B_NK = 0, /* A [M,K] row-major (lda>=K), B [N,K] K-contiguous (ldb>=K) */

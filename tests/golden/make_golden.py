@@ -3,8 +3,10 @@
 compiled from /root/reference by oracle/Makefile) on seeded inputs.
 
   python tests/golden/make_golden.py --cpu            # gemm_cpu_h fixtures (runs here)
-  python tests/golden/make_golden.py --gpu --out DIR  # kernel_smoothquant / kernel_moe_smoothquant
-                                                      # outputs recorded on an MI355X
+  python tests/golden/make_golden.py --gpu --out DIR  # kernel_smoothquant / kernel_moe_smoothquant /
+                                                      # kernel_(add_)rmsnorm2d_fwd outputs
+                                                      # recorded on an MI355X
+  python tests/golden/make_golden.py --rmsnorm --out DIR  # the RMSNorm ones only
 
 The .npz files hold inputs and expected outputs only (data, no code).  The
 CPU oracle tests compare against them (tests/test_oracle_cpu.py).
@@ -83,10 +85,38 @@ def gpu_fixtures(out: Path) -> None:
     print("wrote", path, flush=True)
 
 
+def gpu_rmsnorm_fixtures(out: Path) -> None:
+    import torch
+
+    assert O.ref() is not None, "oracle/_ref not built"
+    dev = torch.device("cuda:0")
+    eps = 1e-5
+    # add + rmsnorm: rows of whole 8-element vectors (the reference has no tail)
+    for (m, n) in [(8, 4096), (4, 8192), (6, 2048)]:
+        seed = 0x4D50 + n
+        x, res, gamma = G.rmsnorm_inputs(seed, m, n)
+        xo, y = O.ref_rmsnorm2d_gpu(*(torch.from_numpy(v).to(dev) for v in (x, gamma)), eps=eps,
+                                    residual=torch.from_numpy(res).to(dev))
+        path = out / f"add_rmsnorm2d_ref_{m}x{n}.npz"
+        np.savez_compressed(path, x=x, res=res, gamma=gamma, x_out=xo.cpu().numpy(),
+                            y=y.cpu().numpy(), eps=eps)
+        print("wrote", path, flush=True)
+    # plain rmsnorm; N = 1024 is the reference's own sweep size, where its
+    # tail loop adds every column twice
+    for (m, n) in [(8, 4096), (4, 1024)]:
+        seed = 0x4D60 + n
+        x, _, gamma = G.rmsnorm_inputs(seed, m, n)
+        _, y = O.ref_rmsnorm2d_gpu(*(torch.from_numpy(v).to(dev) for v in (x, gamma)), eps=eps)
+        path = out / f"rmsnorm2d_ref_{m}x{n}.npz"
+        np.savez_compressed(path, x=x, gamma=gamma, y=y.cpu().numpy(), eps=eps)
+        print("wrote", path, flush=True)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--cpu", action="store_true")
     ap.add_argument("--gpu", action="store_true")
+    ap.add_argument("--rmsnorm", action="store_true", help="only the RMSNorm reference fixtures")
     ap.add_argument("--out", default=str(HERE))
     a = ap.parse_args()
     out = Path(a.out)
@@ -95,6 +125,8 @@ def main() -> int:
         cpu_fixtures(out)
     if a.gpu:
         gpu_fixtures(out)
+    if a.gpu or a.rmsnorm:
+        gpu_rmsnorm_fixtures(out)
     return 0
 
 

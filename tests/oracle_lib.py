@@ -31,6 +31,8 @@ _ORACLE_SIGS = {
     "w8a8o_moe_sort": (None, [_p, _u32, _u32, _u32, _u32, _p, _p, _p, _p, _p]),
     "w8a8o_silu_mul_quant": (None, [_p, _u32, _u32, _u32, _p, _f32, _p, _p, _u32]),
     "w8a8o_moe_combine": (None, [_p, _u32, _p, _p, _u32, _u32, _u32, _p, _u32]),
+    "w8a8o_rmsnorm_smoothquant": (None, [_p, _p, _p, _p, _p, _p, _p, _p, _u32, _u32, _f32, _f32,
+                                         _u32, _u32, _u32]),
 }
 
 _REF_SIGS = {
@@ -41,6 +43,8 @@ _REF_SIGS = {
     "ref_kernel_moe_smoothquant": (_i32, [_p, _p, _p, _p, _p, _u32, _u32, _u32, _u32, _f32]),
     "ref_kernel_topk_softmax": (_i32, [_p, _p, _p, _u32, _u32, _u32]),
     "ref_moe_sorting": (_i32, [_p, _u32, _u32, _u32, _u32, _p, _p, _p, _p, _p]),
+    "ref_kernel_rmsnorm2d": (_i32, [_p, _p, _p, _u32, _u32, _u32, _u32, _f32]),
+    "ref_kernel_add_rmsnorm2d": (_i32, [_p, _p, _p, _p, _p, _u32, _u32, _f32]),
 }
 
 _oracle = None
@@ -225,3 +229,43 @@ def moe_combine(y: np.ndarray, weights: np.ndarray, dst_row: np.ndarray):
     out = np.zeros((t, n), dtype=np.uint16)
     oracle().w8a8o_moe_combine(_a(y.view(np.uint16)), n, _a(w), _a(d), t, k, n, _a(out), n)
     return out.view(np.float16)
+
+
+def rmsnorm_smoothquant(x: np.ndarray, gamma: np.ndarray, s=None, res=None, eps: float = 1e-5,
+                        quant_max: float = 127.0):
+    """(x_out, y, q, r) of the RMSNorm (+ residual) -> quantizer restatement;
+    x_out is None without a residual, q and r are None without s."""
+    x = np.ascontiguousarray(x, dtype=np.float16)
+    g = np.ascontiguousarray(gamma, dtype=np.float32)
+    m, n = x.shape
+    rr = None if res is None else np.ascontiguousarray(res, dtype=np.float16)
+    s_ = None if s is None else np.ascontiguousarray(s, dtype=np.float32)
+    xo = None if rr is None else np.zeros((m, n), dtype=np.float16)
+    y = np.zeros((m, n), dtype=np.float16)
+    q = None if s_ is None else np.zeros((m, n), dtype=np.int8)
+    r = None if s_ is None else np.zeros(m, dtype=np.float32)
+    p = lambda a: None if a is None else _a(a)  # noqa: E731
+    oracle().w8a8o_rmsnorm_smoothquant(_a(x), p(rr), _a(g), p(s_), p(xo), _a(y), p(q), p(r), m,
+                                       n, eps, quant_max, n, n, n)
+    return xo, y, q, r
+
+
+def ref_rmsnorm2d_gpu(x, gamma, eps: float = 1e-5, residual=None):
+    """Run the reference's own kernel_rmsnorm2d_fwd / kernel_add_rmsnorm2d_fwd
+    (oracle/_ref) on device tensors; returns (x_out or None, y) as tensors."""
+    import torch
+    lib = ref()
+    assert lib is not None, "oracle/_ref not built"
+    m, n = x.shape
+    y = torch.zeros_like(x)
+    torch.cuda.synchronize()
+    if residual is None:
+        rc = lib.ref_kernel_rmsnorm2d(x.data_ptr(), gamma.data_ptr(), y.data_ptr(), m, n, n, n,
+                                      eps)
+        xo = None
+    else:
+        xo = torch.zeros_like(x)
+        rc = lib.ref_kernel_add_rmsnorm2d(x.data_ptr(), residual.data_ptr(), gamma.data_ptr(),
+                                          y.data_ptr(), xo.data_ptr(), m, n, eps)
+    assert rc == 0, rc
+    return xo, y

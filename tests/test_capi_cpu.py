@@ -286,3 +286,33 @@ def test_python_layer_raises_w8a8error(w8a8):
     with pytest.raises(W.W8A8Error) as ei:
         _lib.call("w8a8_smoothquant", None, None, None, None, 1, 1, 127.0, 0, 0, None)
     assert ei.value.code == W.ERROR_INVALID_VALUE
+
+
+def _norm_args(**kw):
+    a = dict(x=FAKE, res=FAKE, gamma=FAKE, s=FAKE, x_out=FAKE, y=None, q=FAKE, r=FAKE, M=4, N=64,
+             eps=1e-5, qmax=127.0, ldx=0, ldy=0, ldq=0, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+@pytest.mark.parametrize("kw,needle", [
+    (dict(x=None), "x and gamma"),
+    (dict(gamma=None), "x and gamma"),
+    (dict(M=0), "M and N"),
+    (dict(N=0), "M and N"),
+    (dict(q=None), "together"),
+    (dict(s=None), "together"),
+    (dict(r=None), "together"),
+    (dict(res=None), "needs a residual"),
+    (dict(x_out=None, s=None, q=None, r=None), "no output"),
+    (dict(eps=-1.0), "eps"),
+    (dict(eps=float("nan")), "eps"),
+    (dict(qmax=0.0), "quant_max"),
+    (dict(qmax=200.0), "quant_max"),
+    (dict(ldx=10), "smaller than N"),
+    (dict(ldq=63), "smaller than N"),
+    (dict(y=FAKE, ldy=5), "smaller than N"),
+])
+def test_add_rmsnorm_smoothquant_validation(w8a8, kw, needle):
+    rc, msg = _status("w8a8_add_rmsnorm_smoothquant", *_norm_args(**kw))
+    assert rc == W.ERROR_INVALID_VALUE and needle in msg, msg

@@ -356,3 +356,121 @@ def test_moe_combine_closed_forms():
     assert np.array_equal(out[0].view(np.uint16), y[4].view(np.uint16))  # 1*y + 0*y'
     assert np.array_equal(out[1].view(np.uint16), y[2].view(np.uint16))  # mean of equal rows
     assert np.array_equal(out[2].view(np.uint16), y[5].view(np.uint16))  # invalid slot skipped
+
+
+# ------------------------------------------------------------ RMSNorm -> quantizer
+def test_rmsnorm_reference_default_fills():
+    # test_rmsnorm / test_add_rmsnorm fills (rocwmma_rmsnorm2d.cpp:204-205, 228-229):
+    # x = 0.5 (or 0.3 + 0.2), gamma = 1, eps = 1e-5: every y rounds to 1.0, so
+    # the quantizer gives q = 127 and r = fl(1 / 127)
+    n = 4096
+    g = np.ones(n, np.float32)
+    _, y, _, _ = O.rmsnorm_smoothquant(np.full((3, n), 0.5, np.float16), g)
+    assert (y == 1.0).all()
+    xo, y, q, r = O.rmsnorm_smoothquant(np.full((3, n), 0.3, np.float16), g,
+                                        np.ones(n, np.float32),
+                                        res=np.full((3, n), 0.2, np.float16))
+    assert (xo == np.float16(np.float32(np.float16(0.3)) + np.float32(np.float16(0.2)))).all()
+    assert (y == 1.0).all() and (q == 127).all()
+    assert (r == np.float32(1.0) / np.float32(127.0)).all()
+
+
+def test_rmsnorm_closed_forms_eps0():
+    n = 4096
+    gamma = (np.arange(n) % 7 + 1).astype(np.float32) * 0.25  # fp16-exact weights
+    # one-hot row a*e_0: rstd = sqrt(N)/|a| -> y[0] = sign(a) * 64 * gamma[0]
+    x = np.zeros((2, n), np.float16)
+    x[0, 0], x[1, 5] = 3.0, -0.75
+    _, y, _, _ = O.rmsnorm_smoothquant(x, gamma, eps=0.0)
+    assert y[0, 0] == 64 * gamma[0] and y[1, 5] == -64 * gamma[5]
+    assert np.count_nonzero(y) == 2
+    # |x| = 2^k everywhere: rstd = 2^-k exactly -> y = sign(x) * gamma
+    for k in (-6, 0, 5):
+        sign = np.where(np.arange(n) % 3 == 0, -1.0, 1.0)
+        x = (sign * 2.0 ** k).astype(np.float16)[None, :]
+        _, y, _, _ = O.rmsnorm_smoothquant(x, gamma, eps=0.0)
+        assert np.array_equal(y[0], (sign * gamma).astype(np.float16))
+
+
+def test_rmsnorm_scale_invariance_and_residual_cancel():
+    m, n = 6, 2048
+    x, res, gamma = G.rmsnorm_inputs(11, m, n)
+    for k in (-3, 2):  # scaling by 2^k and RMSNorm is scale invariant
+        xk = (x.astype(np.float32) * 2.0 ** k).astype(np.float16)
+        xk = np.where(np.abs(xk) >= 2.0 ** -14, xk, 0).astype(np.float16)  # keep it exact:
+        xs = np.where(np.abs(xk) > 0, x, 0).astype(np.float16)            # no subnormals
+        _, y0, _, _ = O.rmsnorm_smoothquant(xs, gamma, eps=0.0)
+        _, yk, _, _ = O.rmsnorm_smoothquant(xk, gamma, eps=0.0)
+        assert np.array_equal(yk.view(np.uint16), y0.view(np.uint16))
+    # x + (-x) = 0: r = 0, q = 0, y = 0 (eps keeps rstd finite)
+    s = G.uniform(11, G.TID_S, (n,), 0.5, 2.0)
+    xo, y, q, r = O.rmsnorm_smoothquant(x, gamma, s, res=-x)
+    assert (xo == 0).all() and (y == 0).all() and (q == 0).all() and (r == 0).all()
+
+
+def test_rmsnorm_quant_stage_is_smoothquant_of_y():
+    m, n = 5, 4096
+    x, res, gamma = G.rmsnorm_inputs(12, m, n)
+    s = G.uniform(12, G.TID_S, (n,), 0.5, 2.0)
+    xo, y, q, r = O.rmsnorm_smoothquant(x, gamma, s, res=res)
+    q2, r2 = O.smoothquant(y, s)
+    assert np.array_equal(q, q2) and np.array_equal(r.view(np.uint32), r2.view(np.uint32))
+    # the residual form normalises half(x + res) but takes the sum of squares
+    # of the unrounded x + res (rocwmma_rmsnorm2d.cpp:158-160): against plain
+    # RMSNorm of x_out it differs only through rstd, by one fp16 ulp at most
+    _, y3, _, _ = O.rmsnorm_smoothquant(xo, gamma)
+    assert ulp16(y, y3).max() <= 1
+
+
+def test_rmsnorm_against_float64_within_one_ulp():
+    m, n = 16, 4096
+    x, res, gamma = G.rmsnorm_inputs(13, m, n)
+    _, y, _, _ = O.rmsnorm_smoothquant(x, gamma, eps=1e-5)
+    v = x.astype(np.float64)
+    exact = v / np.sqrt((v * v).mean(axis=1, keepdims=True) + 1e-5) * gamma
+    assert ulp16(y, exact.astype(np.float16)).max() <= 1
+
+
+def ulp16(a, b):
+    ia = a.view(np.int16).astype(np.int32)
+    ib = b.view(np.int16).astype(np.int32)
+    ia = np.where(ia < 0, -32768 - ia, ia)
+    ib = np.where(ib < 0, -32768 - ib, ib)
+    return np.abs(ia - ib)
+
+
+@pytest.mark.parametrize("path", _golden("add_rmsnorm2d_ref_*.npz") or [None])
+def test_add_rmsnorm_matches_reference_kernel_golden(path):
+    if path is None:
+        pytest.skip("no reference-kernel fixtures recorded yet")
+    d = np.load(path)
+    xo, y, _, _ = O.rmsnorm_smoothquant(d["x"], d["gamma"], res=d["res"], eps=float(d["eps"]))
+    # x + residual rounded to fp16 is exact arithmetic: bit for bit
+    assert np.array_equal(xo.view(np.uint16), d["x_out"].view(np.uint16))
+    # the sum of squares is summed in another order (and rsqrt rounded
+    # differently): one fp16 ulp at most, on a small fraction of elements
+    du = ulp16(y, d["y"])
+    assert du.max() <= 1 and (du > 0).mean() < 0.01
+
+
+@pytest.mark.parametrize("path", _golden("rmsnorm2d_ref_*.npz") or [None])
+def test_rmsnorm_matches_reference_kernel_golden(path):
+    if path is None:
+        pytest.skip("no reference-kernel fixtures recorded yet")
+    d = np.load(path)
+    x, g, eps = d["x"], d["gamma"], float(d["eps"])
+    _, y, _, _ = O.rmsnorm_smoothquant(x, g, eps=eps)
+    n = x.shape[1]
+    if n % 2048 == 0:
+        du = ulp16(y, d["y"])
+        assert du.max() <= 1 and (du > 0).mean() < 0.01
+    else:
+        # the reference's tail loop (rocwmma_rmsnorm2d.cpp:83-85) adds the
+        # columns of the last partial 2048-chunk a second time: here (N < 2048)
+        # every column, so its rstd is rsqrt(2 * mean + eps)
+        v = x.astype(np.float64)
+        twice = v / np.sqrt(2 * (v * v).mean(axis=1, keepdims=True) + eps) * g
+        assert ulp16(d["y"], twice.astype(np.float16)).max() <= 1
+        ratio = np.abs(d["y"].astype(np.float64)) / np.maximum(np.abs(y.astype(np.float64)), 1e-3)
+        big = np.abs(y) > 0.1
+        assert np.allclose(ratio[big], 1 / np.sqrt(2), rtol=2e-3)
