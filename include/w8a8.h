@@ -180,6 +180,32 @@ size_t w8a8_pack_weights_size(uint32_t n, uint32_t k);
 int w8a8_pack_weights(const int8_t* w, uint32_t n, uint32_t k, uint32_t ldw, int8_t* packed,
                       size_t packed_bytes, hipStream_t stream);
 
+/* Smooth-scale folding modes of w8a8_quantize_weights. */
+#define W8A8_FOLD_MULTIPLY 0 /* w[n,k] * smooth_scale[k]                               */
+#define W8A8_FOLD_DIVIDE 1   /* w[n,k] / smooth_scale[k]: the weight side of activations
+                                quantized as x * smooth_scale, so (x*s) . (w/s)^T = x . w^T */
+
+/*
+ * Offline weight preparation: SmoothQuant folding, per-output-channel absmax
+ * int8 quantization and (optionally) packing, in one pass over the fp16
+ * weights.  The reference has no weight-side routine (its samples take int8
+ * weights as given); per row n this is the quantizer of
+ * rocwmma_smoothquant.cpp:74-121 applied to the folded weights:
+ *   p[k]       = float(w[n,k]) (* or /) smooth_scale[k]   (smooth_scale NULL: p = float(w))
+ *   scale_w[n] = max_k |p[k]| / quant_max;  inv = scale_w[n] > 0 ? 1 / scale_w[n] : 0
+ *   w_q[n,k]   = int8(clamp(rint(p[k] * inv), -quant_max, quant_max))
+ * so FOLD_MULTIPLY gives exactly w8a8_smoothquant(w, smooth_scale).
+ *   w          fp16 [n, ldw] (ldw = 0 means k)
+ *   packed = 0 w_q int8 [n, ldq] row-major (ldq = 0 means k); out_bytes >= (n-1)*ldq + k
+ *   packed = 1 w_q in the w8a8_pack_weights layout (ldq unused);
+ *              out_bytes >= w8a8_pack_weights_size(n, k)
+ *   scale_w    fp32 [n]: the per-channel scale the GEMMs take as scale_b
+ */
+int w8a8_quantize_weights(const void* w, uint32_t n, uint32_t k, uint32_t ldw,
+                          const float* smooth_scale, int fold, float quant_max, int8_t* w_q,
+                          uint32_t ldq, int packed, size_t out_bytes, float* scale_w,
+                          hipStream_t stream);
+
 /*
  * w8a8_gemm over packed weights (layout W8A8_LAYOUT_A_ROW_B_NK, B = the packed
  * buffer of w [n, k]); same outputs bit for bit.  Requires a 16-byte aligned

@@ -24,6 +24,8 @@ from . import _lib
 from ._lib import (  # noqa: F401
     ERROR_INVALID_VALUE,
     ERROR_NOT_SUPPORTED,
+    FOLD_DIVIDE,
+    FOLD_MULTIPLY,
     LAYOUT_A_COL_B_KN,
     LAYOUT_A_ROW_B_NK,
     OUT_F16,
@@ -36,7 +38,7 @@ __all__ = [
     "fused_sq_gemm", "W8A8Error", "PackedWeights", "pack_weights", "pack_weights_size",
     "gemm_packed", "fused_sq_gemm_packed", "grouped_gemm", "topk_softmax", "moe_sort",
     "moe_gemm", "moe_silu_mul_quant", "moe_combine", "moe_ffn", "add_rmsnorm_smoothquant",
-    "rmsnorm", "add_rmsnorm",
+    "rmsnorm", "add_rmsnorm", "quantize_weights",
 ]
 
 
@@ -271,6 +273,37 @@ def pack_weights(w, out=None) -> PackedWeights:
     _lib.call("w8a8_pack_weights", _ptr(w), n, k, w.stride(0), _ptr(buf), buf.numel(),
               _stream(w.device))
     return PackedWeights(buf, n, k)
+
+
+def quantize_weights(w, smooth_scale=None, fold: int = FOLD_DIVIDE, packed: bool = True,
+                     quant_max: float = 127.0, out=None, scale_w=None):
+    """Offline weight preparation from fp16 w [N, K]: fold the smooth scale
+    (FOLD_DIVIDE: w / s, the weight side of activations quantized as x * s;
+    FOLD_MULTIPLY: w * s), quantize each output channel to int8 with an absmax
+    scale, and pack (default) for gemm_packed / fused_sq_gemm_packed.
+
+    Returns (PackedWeights or int8 [N, K] tensor, scale_w fp32 [N])."""
+    torch = _torch()
+    _require_cuda(w, smooth_scale, out, scale_w)
+    if w.dim() != 2 or w.dtype != torch.float16 or w.stride(1) != 1:
+        raise ValueError("w must be a 2-D fp16 tensor with unit column stride")
+    n, k = w.shape
+    if smooth_scale is not None:
+        if smooth_scale.dtype != torch.float32 or smooth_scale.numel() != k:
+            raise ValueError("smooth_scale must be fp32 with K elements")
+        smooth_scale = smooth_scale.contiguous()
+    sb = scale_w if scale_w is not None else torch.empty(n, dtype=torch.float32, device=w.device)
+    if packed:
+        buf = out if out is not None else torch.empty(pack_weights_size(n, k), dtype=torch.int8,
+                                                      device=w.device)
+        ldq, nbytes = 0, buf.numel()
+    else:
+        buf = out if out is not None else torch.empty((n, k), dtype=torch.int8, device=w.device)
+        ldq, nbytes = buf.stride(0), (n - 1) * buf.stride(0) + k
+    _lib.call("w8a8_quantize_weights", _ptr(w), n, k, w.stride(0), _ptr(smooth_scale), int(fold),
+              float(quant_max), _ptr(buf), ldq, 1 if packed else 0, nbytes, _ptr(sb),
+              _stream(w.device))
+    return (PackedWeights(buf, n, k) if packed else buf), sb
 
 
 def gemm_packed(a, pw: PackedWeights, scale_a=None, scale_b=None, tensor_scale_a: float = 1.0,

@@ -22,6 +22,9 @@ LAYOUT_A_COL_B_KN = 1
 OUT_I32 = 0
 OUT_F16 = 1
 
+FOLD_MULTIPLY = 0
+FOLD_DIVIDE = 1
+
 _u32 = ctypes.c_uint32
 _i32 = ctypes.c_int
 _f32 = ctypes.c_float
@@ -48,6 +51,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                     _ptr, _u32, _ptr]),
     "w8a8_add_rmsnorm_smoothquant": (_i32, [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _u32,
                                             _u32, _f32, _f32, _u32, _u32, _u32, _ptr]),
+    "w8a8_quantize_weights": (_i32, [_ptr, _u32, _u32, _u32, _ptr, _i32, _f32, _ptr, _u32, _i32,
+                                     _size, _ptr, _ptr]),
     "w8a8_gemm_workspace_size": (_size, [_u32, _u32, _u32, _i32]),
     "w8a8_gemm": (_i32, [_u32, _u32, _u32, _ptr, _ptr, _ptr, _u32, _u32, _u32, _ptr, _ptr, _f32,
                          _f32, _i32, _i32, _ptr, _size, _ptr]),

@@ -38,6 +38,7 @@ SOURCES = [
     "gemm_i8.hip",
     "moe.hip",
     "rmsnorm_sq.hip",
+    "weights.hip",
 ]
 
 # -packed-fp32-ops: keep the compiler from emitting packed fp32 VALU ops.

@@ -165,6 +165,56 @@ int w8a8_add_rmsnorm_smoothquant(const void* x, const void* residual, const floa
     return hip_status(w8a8::launch_rmsnorm_sq(p, stream), fn);
 }
 
+int w8a8_quantize_weights(const void* w, uint32_t n, uint32_t k, uint32_t ldw,
+                          const float* smooth_scale, int fold, float quant_max, int8_t* w_q,
+                          uint32_t ldq, int packed, size_t out_bytes, float* scale_w,
+                          hipStream_t stream)
+{
+    const char* fn = "w8a8_quantize_weights";
+    if(!w || !w_q || !scale_w)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: null pointer argument", fn);
+    if(n == 0 || k == 0 || n > 0x7FFFFF00u)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: n and k must be > 0, n < 2^31 (n=%u k=%u)",
+                    fn, n, k);
+    if(fold != W8A8_FOLD_MULTIPLY && fold != W8A8_FOLD_DIVIDE)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: unknown fold mode %d", fn, fold);
+    if(packed != 0 && packed != 1)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: packed must be 0 or 1", fn);
+    if(!valid_qmax(quant_max))
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: quant_max must be in (0, 127], got %g", fn,
+                    (double)quant_max);
+    if(ldw == 0) ldw = k;
+    if(ldq == 0) ldq = k;
+    if(ldw < k) return fail(W8A8_ERROR_INVALID_VALUE, "%s: ldw=%u smaller than k=%u", fn, ldw, k);
+    if(packed) {
+        const size_t need = w8a8::packed_weight_bytes(n, k);
+        if(out_bytes < need)
+            return fail(W8A8_ERROR_INVALID_VALUE, "%s: packed output needs %zu bytes, got %zu", fn,
+                        need, out_bytes);
+        if(reinterpret_cast<uintptr_t>(w_q) % 16)
+            return fail(W8A8_ERROR_INVALID_VALUE, "%s: packed output must be 16-byte aligned", fn);
+    } else {
+        if(ldq < k)
+            return fail(W8A8_ERROR_INVALID_VALUE, "%s: ldq=%u smaller than k=%u", fn, ldq, k);
+        const size_t need = (size_t)(n - 1) * ldq + k;
+        if(out_bytes < need)
+            return fail(W8A8_ERROR_INVALID_VALUE, "%s: output needs %zu bytes, got %zu", fn, need,
+                        out_bytes);
+    }
+    w8a8::WeightQuant p{};
+    p.w    = static_cast<const uint16_t*>(w);
+    p.s    = smooth_scale;
+    p.q    = w_q;
+    p.sb   = scale_w;
+    p.n    = n;
+    p.k    = k;
+    p.ldw  = ldw;
+    p.ldq  = ldq;
+    p.qmax = quant_max;
+    return hip_status(
+        w8a8::launch_quantize_weights(p, fold == W8A8_FOLD_DIVIDE, packed == 1, stream), fn);
+}
+
 static uint32_t round_up16(uint32_t v) { return (v + 15u) & ~15u; }
 
 size_t w8a8_gemm_workspace_size(uint32_t m, uint32_t n, uint32_t k, int layout)

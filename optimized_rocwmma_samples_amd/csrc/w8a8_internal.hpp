@@ -77,6 +77,19 @@ hipError_t launch_gemm_decode(const GemmArgs& g, bool packed, hipStream_t stream
 size_t     packed_weight_bytes(uint32_t n, uint32_t k);
 hipError_t launch_pack_weights(const int8_t* w, uint32_t n, uint32_t k, uint32_t ldw,
                                int8_t* packed, hipStream_t stream);
+// Fold + per-channel quantization of fp16 weights (weights.hip); packed:
+// write the packed layout (zero padding included), else row-major [n, ldq].
+struct WeightQuant {
+    const uint16_t* w;
+    const float*    s;
+    int8_t*         q;
+    float*          sb;
+    uint32_t        n, k, ldw, ldq;
+    float           qmax;
+};
+hipError_t launch_quantize_weights(const WeightQuant& p, bool divide, bool packed,
+                                   hipStream_t stream);
+
 // GEMM over packed weights (g.ldb unused).  gemm_packed_ok: 16-byte aligned
 // A, lda % 16 == 0, k % 16 == 0 and every A panel addressable (< 2 GiB).
 bool       gemm_packed_ok(const GemmArgs& g);

@@ -124,6 +124,34 @@ void w8a8o_moe_smoothquant(const uint16_t* x, const float* s, const int32_t* top
 }
 
 /* ------------------------------------------------------------------------- */
+/* weight quantization (fold + per-channel absmax)                            */
+/* ------------------------------------------------------------------------- */
+void w8a8o_quantize_weights(const uint16_t* w, const float* s, int divide, float quant_max,
+                            int8_t* q, float* sb, uint32_t N, uint32_t K, uint32_t ldw,
+                            uint32_t ldq)
+{
+#pragma omp parallel
+    {
+        float* p = (float*)malloc(sizeof(float) * K);
+#pragma omp for schedule(static)
+        for(long n = 0; n < (long)N; ++n) {
+            const uint16_t* wr   = w + (size_t)n * ldw;
+            float           amax = 0.f;
+            for(uint32_t k = 0; k < K; ++k) {
+                p[k] = w8a8o_half_to_float(wr[k]);
+                if(s) p[k] = divide ? p[k] / s[k] : p[k] * s[k];
+                amax = fmaxf(amax, fabsf(p[k]));
+            }
+            const float rs  = amax / quant_max;
+            const float inv = (rs > 0.f) ? (1.f / rs) : 0.f;
+            sb[n]           = rs;
+            for(uint32_t k = 0; k < K; ++k) q[(size_t)n * ldq + k] = quant_one(p[k], inv, quant_max);
+        }
+        free(p);
+    }
+}
+
+/* ------------------------------------------------------------------------- */
 /* RMSNorm (+ residual) -> quantizer                                          */
 /* ------------------------------------------------------------------------- */
 void w8a8o_rmsnorm_smoothquant(const uint16_t* x, const uint16_t* res, const float* gamma,

@@ -78,6 +78,18 @@ void w8a8o_rmsnorm_smoothquant(const uint16_t* x, const uint16_t* res, const flo
                                float* r, uint32_t M, uint32_t N, float eps, float quant_max,
                                uint32_t ldx, uint32_t ldy, uint32_t ldq);
 
+/*
+ * Offline weight quantization (the weight side of the path; the reference has
+ * no such routine): per output channel n, the quantizer of
+ * rocwmma_smoothquant.cpp:74-121 on p[k] = float(w[n,k]) * s[k] (divide = 0)
+ * or float(w[n,k]) / s[k] (divide = 1), or p = float(w) when s == NULL:
+ *   sb[n] = max_k |p| / quant_max;  q[n,k] = int8(clamp(rint(p * inv)))
+ * Row-major output [n, ldq].
+ */
+void w8a8o_quantize_weights(const uint16_t* w, const float* s, int divide, float quant_max,
+                            int8_t* q, float* sb, uint32_t N, uint32_t K, uint32_t ldw,
+                            uint32_t ldq);
+
 /* Operand layouts of the int8 GEMM. */
 enum {
     W8A8O_LAYOUT_A_ROW_B_NK = 0, /* A [M,K] row-major (lda>=K), B [N,K] K-contiguous (ldb>=K) */

@@ -31,6 +31,7 @@ _ORACLE_SIGS = {
     "w8a8o_moe_sort": (None, [_p, _u32, _u32, _u32, _u32, _p, _p, _p, _p, _p]),
     "w8a8o_silu_mul_quant": (None, [_p, _u32, _u32, _u32, _p, _f32, _p, _p, _u32]),
     "w8a8o_moe_combine": (None, [_p, _u32, _p, _p, _u32, _u32, _u32, _p, _u32]),
+    "w8a8o_quantize_weights": (None, [_p, _p, _i32, _f32, _p, _p, _u32, _u32, _u32, _u32]),
     "w8a8o_rmsnorm_smoothquant": (None, [_p, _p, _p, _p, _p, _p, _p, _p, _u32, _u32, _f32, _f32,
                                          _u32, _u32, _u32]),
 }
@@ -269,3 +270,15 @@ def ref_rmsnorm2d_gpu(x, gamma, eps: float = 1e-5, residual=None):
                                           y.data_ptr(), xo.data_ptr(), m, n, eps)
     assert rc == 0, rc
     return xo, y
+
+
+def quantize_weights(w: np.ndarray, s=None, divide: bool = True, quant_max: float = 127.0):
+    """(q int8 [N, K], sb fp32 [N]) of the weight-quantization restatement."""
+    w = np.ascontiguousarray(w, dtype=np.float16)
+    n, k = w.shape
+    s_ = None if s is None else np.ascontiguousarray(s, dtype=np.float32)
+    q = np.zeros((n, k), dtype=np.int8)
+    sb = np.zeros(n, dtype=np.float32)
+    oracle().w8a8o_quantize_weights(_a(w.view(np.uint16)), None if s_ is None else _a(s_),
+                                    1 if divide else 0, quant_max, _a(q), _a(sb), n, k, k, k)
+    return q, sb

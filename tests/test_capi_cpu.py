@@ -316,3 +316,30 @@ def _norm_args(**kw):
 def test_add_rmsnorm_smoothquant_validation(w8a8, kw, needle):
     rc, msg = _status("w8a8_add_rmsnorm_smoothquant", *_norm_args(**kw))
     assert rc == W.ERROR_INVALID_VALUE and needle in msg, msg
+
+
+def _wq_args(**kw):
+    a = dict(w=FAKE, n=8, k=64, ldw=0, s=FAKE, fold=1, qmax=127.0, q=ctypes.c_void_p(0x2000),
+             ldq=0, packed=1, out_bytes=1 << 20, sb=FAKE, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+@pytest.mark.parametrize("kw,needle", [
+    (dict(w=None), "null"),
+    (dict(q=None), "null"),
+    (dict(sb=None), "null"),
+    (dict(n=0), "must be > 0"),
+    (dict(k=0), "must be > 0"),
+    (dict(fold=2), "fold mode"),
+    (dict(packed=3), "packed"),
+    (dict(qmax=-1.0), "quant_max"),
+    (dict(ldw=10), "ldw"),
+    (dict(out_bytes=100), "packed output needs"),
+    (dict(q=ctypes.c_void_p(0x2008)), "16-byte aligned"),
+    (dict(packed=0, ldq=32), "ldq"),
+    (dict(packed=0, out_bytes=8 * 64 - 1), "output needs"),
+])
+def test_quantize_weights_validation(w8a8, kw, needle):
+    rc, msg = _status("w8a8_quantize_weights", *_wq_args(**kw))
+    assert rc == W.ERROR_INVALID_VALUE and needle in msg, msg

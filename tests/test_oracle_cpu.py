@@ -474,3 +474,57 @@ def test_rmsnorm_matches_reference_kernel_golden(path):
         ratio = np.abs(d["y"].astype(np.float64)) / np.maximum(np.abs(y.astype(np.float64)), 1e-3)
         big = np.abs(y) > 0.1
         assert np.allclose(ratio[big], 1 / np.sqrt(2), rtol=2e-3)
+
+
+# ------------------------------------------------------------ weight quantization
+def test_quantize_weights_multiply_is_the_quantizer():
+    # FOLD_MULTIPLY is the activation quantizer (pinned to the reference
+    # kernel's outputs above) applied to weight rows
+    w = G.normal(21, G.TID_B, (37, 1000))
+    s = G.uniform(21, G.TID_S, (1000,), 0.5, 2.0)
+    q, sb = O.quantize_weights(w, s, divide=False)
+    q2, r2 = O.smoothquant(w, s)
+    assert np.array_equal(q, q2) and np.array_equal(sb.view(np.uint32), r2.view(np.uint32))
+    q3, sb3 = O.quantize_weights(w, None)
+    q4, r4 = O.smoothquant(w, np.ones(1000, np.float32))
+    assert np.array_equal(q3, q4) and np.array_equal(sb3, r4)
+
+
+def test_quantize_weights_divide_closed_forms():
+    n, k = 19, 640
+    w = G.normal(22, G.TID_B, (n, k))
+    # dividing by 2^j is multiplying by 2^-j exactly
+    j = (np.arange(k) % 5 - 2).astype(np.float32)
+    qd, sbd = O.quantize_weights(w, (2.0 ** j).astype(np.float32), divide=True)
+    qm, sbm = O.quantize_weights(w, (2.0 ** -j).astype(np.float32), divide=False)
+    assert np.array_equal(qd, qm) and np.array_equal(sbd, sbm)
+    # invariants for a general s
+    s = G.uniform(22, G.TID_S, (k,), 0.5, 2.0)
+    q, sb = O.quantize_weights(w, s, divide=True)
+    p = w.astype(np.float32) / s
+    assert np.allclose(sb, np.abs(p).max(axis=1) / 127, rtol=1e-6)
+    assert (np.abs(q).max(axis=1) == 127).all()
+    assert ((np.sign(q) == np.sign(p)) | (q == 0)).all()
+    assert (np.abs(q - p / sb[:, None]) <= 0.5 + 1e-4).all()
+
+
+def test_smoothing_preserves_the_product():
+    # (x * s) . (w / s)^T = x . w^T: quantizing both sides after the fold gives
+    # the float product to within the int8 quantization error, and SmoothQuant's
+    # own scale (s = 1 / sigma, sigma_k = sqrt(max|x_k| / max|w_k|), alpha 0.5)
+    # moves the outlier columns' range into the weights: a smaller error than
+    # quantizing x and w as they are
+    m, n, k = 64, 96, 1024
+    x = G.activations(23, m, k)
+    w = G.normal(23, G.TID_B, (n, k))
+    exact = x.astype(np.float64) @ w.astype(np.float64).T
+
+    def rel_err(s):
+        qx, r = O.smoothquant(x, s)
+        qw, sb = O.quantize_weights(w, s, divide=True)
+        c = O.dequant_f16(O.gemm_i32(qx, qw), r, sb).astype(np.float64)
+        return np.linalg.norm(c - exact) / np.linalg.norm(exact)
+
+    sigma = np.sqrt(np.abs(x.astype(np.float32)).max(0) / np.abs(w.astype(np.float32)).max(0))
+    plain, smoothed = rel_err(np.ones(k, np.float32)), rel_err((1 / sigma).astype(np.float32))
+    assert smoothed < 0.02 and smoothed < 0.5 * plain
