@@ -455,7 +455,7 @@ def main(argv=None) -> int:
                 "traffic_source": (f"{TRAFFIC_PROFILE.relative_to(ROOT)} (rocprofv3 FETCH_SIZE x2.0 "
                                    "+ WRITE_SIZE x1.0, calibrated on a 2^30-byte copy; "
                                    "FETCH_SIZE includes MALL hits)") if traffic else None,
-                "kernel": "gemm_i8_tile_kernel<Cfg<256,256,128,2,2,4>, F16>",
+                "kernel": "gemm_i8_tile_kernel<Cfg<256,256,128,2,2,4,4>, F16>",
                 "avg_launch_us": gemm_avg_us,
                 "note": "int8 ops (2*M*N*K) per launch / average launch duration over the four "
                         "projection GEMMs; peak = 5.0 POP/s dense int8"}

@@ -19,7 +19,7 @@ namespace {
 using gemm::KArgs;
 
 // Production tile configuration.
-using GemmMain = gemm::Cfg<256, 256, 128, 2, 2, 4>;
+using GemmMain = gemm::Cfg<256, 256, 128, 2, 2, 4, 4>;
 // Packed-weight tile configuration (m > kDecodeMaxM).
 using GemmPacked = gemm::PbCfg<256, 4, 2, 4>;
 // Decode configurations: <32-row m tiles, 32-row weight tiles, waves, ring>.

@@ -384,7 +384,7 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-using GemmGrouped = gemm::Cfg<256, 256, 128, 2, 2, 4>;
+using GemmGrouped = gemm::Cfg<256, 256, 128, 2, 2, 4, 4>;
 
 } // namespace
 
