@@ -253,14 +253,18 @@ def bench_decode(torch, w8a8, dev, gen, iters=20):
         for (n, k) in shapes:
             x, s, q, r, out = bufs[(n, k)]
             copies, sb = weights[(n, k)]
+            # split-K workspace (M = 64 takes one), allocated once
+            wsz = w8a8.gemm_packed_workspace_size(m, n, k)
+            ws = torch.empty(wsz, dtype=torch.uint8, device=dev) if wsz else None
             # the two copies alternate: each launch streams its weights from HBM
             calls = [(lambda c=copies[i % 2]: w8a8.fused_sq_gemm_packed(
-                x, s, c, sb, out=out, q=q, row_scale=r)) for i in range(iters)]
+                x, s, c, sb, out=out, q=q, row_scale=r, workspace=ws)) for i in range(iters)]
             us = graph_us(torch, calls)
             # algorithmic HBM bytes of the layer: weights once, activations
             # fp16 in, int8 + row scale round trip, scales, fp16 out
             nbytes = n * k + 4 * n + 2 * m * k + 4 * k + 2 * (m * k + 4 * m) + 2 * m * n
             results.append({"M": m, "N": n, "K": k, "us_per_layer": us,
+                            "workspace_bytes": wsz,
                             "GBps": nbytes / (us * 1e-6) / 1e9,
                             "frac_hbm": nbytes / (us * 1e-6) / PEAK_HBM_BPS,
                             "TOPS": 2.0 * m * n * k / (us * 1e-6) / 1e12})

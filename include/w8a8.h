@@ -207,15 +207,27 @@ int w8a8_quantize_weights(const void* w, uint32_t n, uint32_t k, uint32_t ldw,
                           hipStream_t stream);
 
 /*
+ * Bytes of device workspace w8a8_gemm_packed / w8a8_fused_sq_gemm_packed can
+ * use for an m x n x k problem: the int32 split-K partials of decode shapes
+ * with 32 < m <= 64 (the caller-allocated workspace of the reference's
+ * split-K, rocwmma_gemm_splitk.cpp:214); 0 when the shape takes no workspace.
+ */
+size_t w8a8_gemm_packed_workspace_size(uint32_t m, uint32_t n, uint32_t k);
+
+/*
  * w8a8_gemm over packed weights (layout W8A8_LAYOUT_A_ROW_B_NK, B = the packed
  * buffer of w [n, k]); same outputs bit for bit.  Requires a 16-byte aligned
  * A with lda % 16 == 0 and k % 16 == 0 (W8A8_ERROR_NOT_SUPPORTED otherwise).
  * Decode shapes (m <= 64) stream the packed weights at close to HBM rate.
+ * workspace (16-byte aligned, ws_bytes >= w8a8_gemm_packed_workspace_size)
+ * lets 32 < m <= 64 split K across blocks; NULL runs the unsplit kernel
+ * (same results).
  */
 int w8a8_gemm_packed(uint32_t m, uint32_t n, uint32_t k, const int8_t* a,
                      const int8_t* w_packed, void* c, uint32_t lda, uint32_t ldc,
                      const float* scale_a, const float* scale_b, float tensor_scale_a,
-                     float tensor_scale_b, int out_type, hipStream_t stream);
+                     float tensor_scale_b, int out_type, void* workspace, size_t ws_bytes,
+                     hipStream_t stream);
 
 /*
  * w8a8_fused_sq_gemm with packed weights: the decode-time linear layer
@@ -224,6 +236,7 @@ int w8a8_gemm_packed(uint32_t m, uint32_t n, uint32_t k, const int8_t* a,
 int w8a8_fused_sq_gemm_packed(const void* x, const float* smooth_scale, const int8_t* w_packed,
                               const float* scale_w, void* c, uint32_t m, uint32_t n, uint32_t k,
                               uint32_t ldx, uint32_t ldc, int8_t* q, float* row_scale,
+                              void* workspace, size_t ws_bytes,
                               hipStream_t stream);
 
 /* ------------------------------------------------------------------------- */

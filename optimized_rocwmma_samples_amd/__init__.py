@@ -36,7 +36,7 @@ from ._lib import (  # noqa: F401
 __all__ = [
     "library", "version", "smoothquant", "moe_smoothquant", "gemm", "gemm_workspace_size",
     "fused_sq_gemm", "W8A8Error", "PackedWeights", "pack_weights", "pack_weights_size",
-    "gemm_packed", "fused_sq_gemm_packed", "grouped_gemm", "topk_softmax", "moe_sort",
+    "gemm_packed", "gemm_packed_workspace_size", "fused_sq_gemm_packed", "grouped_gemm", "topk_softmax", "moe_sort",
     "moe_gemm", "moe_silu_mul_quant", "moe_combine", "moe_ffn", "add_rmsnorm_smoothquant",
     "rmsnorm", "add_rmsnorm", "quantize_weights",
 ]
@@ -306,9 +306,31 @@ def quantize_weights(w, smooth_scale=None, fold: int = FOLD_DIVIDE, packed: bool
     return (PackedWeights(buf, n, k) if packed else buf), sb
 
 
+def gemm_packed_workspace_size(m: int, n: int, k: int) -> int:
+    """Bytes of split-K workspace the packed path can use for m x n x k (0: none)."""
+    return int(library().w8a8_gemm_packed_workspace_size(m, n, k))
+
+
+def _packed_workspace(workspace, m, n, k, device):
+    # "auto": allocate what the library asks for; None: run without (unsplit)
+    if isinstance(workspace, str):
+        if workspace != "auto":
+            raise ValueError("workspace must be 'auto', None or a device tensor")
+        size = gemm_packed_workspace_size(m, n, k)
+        if size == 0:
+            return None, 0
+        workspace = _torch().empty(size, dtype=_torch().uint8, device=device)
+    if workspace is None:
+        return None, 0
+    _require_cuda(workspace)
+    return workspace, workspace.numel() * workspace.element_size()
+
+
 def gemm_packed(a, pw: PackedWeights, scale_a=None, scale_b=None, tensor_scale_a: float = 1.0,
-                tensor_scale_b: float = 1.0, out_dtype=None, out=None):
-    """gemm(a, w, ...) with w given as PackedWeights; a int8 [M, K] row-major."""
+                tensor_scale_b: float = 1.0, out_dtype=None, out=None, workspace="auto"):
+    """gemm(a, w, ...) with w given as PackedWeights; a int8 [M, K] row-major.
+    workspace: 'auto' (allocated here when the shape uses one), None (no
+    split-K), or a preallocated device tensor (see gemm_packed_workspace_size)."""
     torch = _torch()
     _require_cuda(a, pw.data, scale_a, scale_b)
     out_dtype = out_dtype or torch.float16
@@ -317,15 +339,17 @@ def gemm_packed(a, pw: PackedWeights, scale_a=None, scale_b=None, tensor_scale_a
         raise ValueError(f"a has K={k}, packed weights K={pw.k}")
     c = out if out is not None else torch.empty((m, pw.n), dtype=out_dtype, device=a.device)
     otype = OUT_I32 if c.dtype == torch.int32 else OUT_F16
+    ws, ws_bytes = _packed_workspace(workspace, m, pw.n, k, a.device)
     _lib.call("w8a8_gemm_packed", m, pw.n, k, _ptr(a), _ptr(pw.data), _ptr(c), a.stride(0),
               c.stride(0), _ptr(scale_a), _ptr(scale_b), float(tensor_scale_a),
-              float(tensor_scale_b), otype, _stream(a.device))
+              float(tensor_scale_b), otype, _ptr(ws), ws_bytes, _stream(a.device))
     return c
 
 
 def fused_sq_gemm_packed(x, smooth_scale, pw: PackedWeights, scale_w, out=None, q=None,
-                         row_scale=None):
-    """fused_sq_gemm with PackedWeights: returns (c fp16 [M, N], q, row_scale)."""
+                         row_scale=None, workspace="auto"):
+    """fused_sq_gemm with PackedWeights: returns (c fp16 [M, N], q, row_scale).
+    workspace as for gemm_packed."""
     torch = _torch()
     _require_cuda(x, smooth_scale, pw.data, scale_w)
     m, k = x.shape
@@ -335,9 +359,10 @@ def fused_sq_gemm_packed(x, smooth_scale, pw: PackedWeights, scale_w, out=None, 
     q = q if q is not None else torch.empty((m, k), dtype=torch.int8, device=x.device)
     r = row_scale if row_scale is not None else torch.empty(m, dtype=torch.float32,
                                                             device=x.device)
+    ws, ws_bytes = _packed_workspace(workspace, m, pw.n, k, x.device)
     _lib.call("w8a8_fused_sq_gemm_packed", _ptr(x), _ptr(smooth_scale), _ptr(pw.data),
               _ptr(scale_w), _ptr(c), m, pw.n, k, x.stride(0), c.stride(0), _ptr(q), _ptr(r),
-              _stream(x.device))
+              _ptr(ws), ws_bytes, _stream(x.device))
     return c, q, r
 
 

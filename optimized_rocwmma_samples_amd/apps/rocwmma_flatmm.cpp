@@ -21,9 +21,13 @@ static void test_flatmm(uint32_t m, uint32_t n, uint32_t k, bool verify)
     const size_t       pbytes = w8a8_pack_weights_size(n, k);
     app::Dev<int8_t>   dp(pbytes);
     CHECK_W8A8(w8a8_pack_weights(dw.p, n, k, k, dp.p, pbytes, nullptr));
+    // split-K workspace for 32 < M <= 64 (caller-allocated, as the reference's
+    // split-K sample allocates its own, rocwmma_gemm_splitk.cpp:214)
+    const size_t     wsb = w8a8_gemm_packed_workspace_size(m, n, k);
+    app::Dev<int8_t> dws(wsb > 0 ? wsb : 16);
     auto fn = [&](void* c, int out) {
         CHECK_W8A8(w8a8_gemm_packed(m, n, k, da.p, dp.p, c, k, n, dsa.p, dsb.p, 1.f, 1.f, out,
-                                    nullptr));
+                                    wsb > 0 ? dws.p : nullptr, wsb, nullptr));
     };
     const double ms    = app::bench_ms([&] { fn(dc.p, W8A8_OUT_F16); });
     const double bytes = (double)n * k + (double)m * k + 4.0 * (m + n) + 2.0 * m * n;

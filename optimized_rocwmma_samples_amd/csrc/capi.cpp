@@ -337,29 +337,41 @@ int w8a8_pack_weights(const int8_t* w, uint32_t n, uint32_t k, uint32_t ldw, int
     return hip_status(w8a8::launch_pack_weights(w, n, k, ldw, packed, stream), "w8a8_pack_weights");
 }
 
+size_t w8a8_gemm_packed_workspace_size(uint32_t m, uint32_t n, uint32_t k)
+{
+    if(m == 0 || n == 0 || k == 0) return 0;
+    w8a8::GemmArgs g{m, n, k, nullptr, nullptr, nullptr, k, k, n, nullptr, nullptr, 1.f, 1.f,
+                     W8A8_OUT_F16};
+    return w8a8::packed_workspace_bytes(g);
+}
+
 int w8a8_gemm_packed(uint32_t m, uint32_t n, uint32_t k, const int8_t* a,
                      const int8_t* w_packed, void* c, uint32_t lda, uint32_t ldc,
                      const float* scale_a, const float* scale_b, float tensor_scale_a,
-                     float tensor_scale_b, int out_type, hipStream_t stream)
+                     float tensor_scale_b, int out_type, void* workspace, size_t ws_bytes,
+                     hipStream_t stream)
 {
     int rc = validate_gemm("w8a8_gemm_packed", m, n, k, a, w_packed, c, lda, k, ldc, out_type,
                            W8A8_LAYOUT_A_ROW_B_NK);
     if(rc != W8A8_SUCCESS) return rc;
     if(reinterpret_cast<uintptr_t>(w_packed) % 16 != 0)
         return fail(W8A8_ERROR_INVALID_VALUE, "w8a8_gemm_packed: w_packed must be 16-byte aligned");
+    if(workspace && reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+        return fail(W8A8_ERROR_INVALID_VALUE, "w8a8_gemm_packed: workspace must be 16-byte aligned");
     w8a8::GemmArgs g{m, n, k, a, w_packed, c, lda, k, ldc, scale_a, scale_b,
                      tensor_scale_a, tensor_scale_b, out_type};
     if(!w8a8::gemm_packed_ok(g))
         return fail(W8A8_ERROR_NOT_SUPPORTED,
                     "w8a8_gemm_packed: needs 16-byte aligned A, lda %% 16 == 0, k %% 16 == 0 "
                     "and A row panels under 2 GiB (m=%u lda=%u k=%u)", m, lda, k);
-    return hip_status(w8a8::launch_gemm_packed(g, stream), "w8a8_gemm_packed");
+    return hip_status(w8a8::launch_gemm_packed(g, workspace, workspace ? ws_bytes : 0, stream),
+                      "w8a8_gemm_packed");
 }
 
 int w8a8_fused_sq_gemm_packed(const void* x, const float* smooth_scale, const int8_t* w_packed,
                               const float* scale_w, void* c, uint32_t m, uint32_t n, uint32_t k,
                               uint32_t ldx, uint32_t ldc, int8_t* q, float* row_scale,
-                              hipStream_t stream)
+                              void* workspace, size_t ws_bytes, hipStream_t stream)
 {
     if(!x || !smooth_scale || !w_packed || !scale_w || !c || !q || !row_scale)
         return fail(W8A8_ERROR_INVALID_VALUE, "w8a8_fused_sq_gemm_packed: null pointer argument");
@@ -377,7 +389,7 @@ int w8a8_fused_sq_gemm_packed(const void* x, const float* smooth_scale, const in
     int rc = w8a8_smoothquant(x, smooth_scale, q, row_scale, m, k, 127.f, ldx, k, stream);
     if(rc != W8A8_SUCCESS) return rc;
     return w8a8_gemm_packed(m, n, k, q, w_packed, c, k, ldc, row_scale, scale_w, 1.f, 1.f,
-                            W8A8_OUT_F16, stream);
+                            W8A8_OUT_F16, workspace, ws_bytes, stream);
 }
 
 // ---------------------------------------------------------------------------

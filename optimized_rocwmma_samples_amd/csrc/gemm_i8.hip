@@ -5,6 +5,7 @@
 // operands) and the repack used for the reference sample's A col-major /
 // B [K,N] layout.
 #include "gemm_i8_decode_kernel.hpp"
+#include "gemm_i8_decode_wide_kernel.hpp"
 #include "gemm_i8_kernel.hpp"
 #include "gemm_i8_pb_kernel.hpp"
 #include "w8a8_internal.hpp"
@@ -27,6 +28,9 @@ using DecSmall   = gemm::DecCfg<1, 1, 4, 3>; // m <= 32, or <= 16 packed
 using DecSmallW  = gemm::DecCfg<1, 2, 8, 3>; // packed, 16 < m <= 32, many slabs
 using DecMid     = gemm::DecCfg<2, 1, 8, 3>; // 32 < m <= 64
 using DecMidW    = gemm::DecCfg<2, 2, 8, 2>; // packed, 32 < m <= 64, many slabs
+// packed, 32 < m <= 64 with a split-K workspace: 8 half slabs per block share
+// the A k-tile through LDS
+using DecWide    = gemm::DecWideCfg<8, 3>;
 // A packed GEMM with at least this many 64-row slabs has enough blocks at
 // 64 rows per block to fill the chip; fewer slabs run 32 rows per block.
 constexpr uint32_t kWideSlabs = 384;
@@ -115,14 +119,46 @@ uint32_t weight_panel_rows(const GemmArgs& g, bool packed)
     return (uint32_t)std::min<size_t>(g.n, rows);
 }
 
+// K splits of the wide decode kernel for one weight panel: enough blocks for
+// every CU, at least 8 k-tiles per split; 1 = no split.
+uint32_t decode_wide_splits(const GemmArgs& g, uint32_t n)
+{
+    static const uint32_t cus = [] {
+        int dev = 0, c = 256;
+        if(hipGetDevice(&dev) == hipSuccess)
+            (void)hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev);
+        return (uint32_t)c;
+    }();
+    const uint32_t nblk  = (n + DecWide::kRows - 1) / DecWide::kRows;
+    const uint32_t nkt   = gemm::packed_ktiles(g.k);
+    const uint32_t want  = (cus + nblk - 1) / nblk;
+    const uint32_t most  = std::max<uint32_t>(1, nkt / 8);
+    return std::max<uint32_t>(1, std::min(want, most));
+}
+
+bool decode_wide_shape(const GemmArgs& g) { return g.m > 32 && g.m <= kDecodeMaxM; }
+
 } // namespace
+
+size_t packed_workspace_bytes(const GemmArgs& g)
+{
+    if(!decode_wide_shape(g) || !gemm_decode_ok(g)) return 0;
+    const uint32_t step = weight_panel_rows(g, true);
+    size_t         most = 0;
+    for(uint32_t n0 = 0; n0 < g.n; n0 += step) {
+        const uint32_t nn = std::min(step, g.n - n0);
+        most = std::max(most, gemm::decode_ws_bytes(g.m, nn, decode_wide_splits(g, nn)));
+    }
+    return most;
+}
 
 bool gemm_decode_ok(const GemmArgs& g)
 {
     return g.m <= kDecodeMaxM && (uint64_t)(g.m - 1) * g.lda + g.k < 0x7FFFFFFFull;
 }
 
-hipError_t launch_gemm_decode(const GemmArgs& g, bool packed, hipStream_t stream)
+hipError_t launch_gemm_decode(const GemmArgs& g, bool packed, void* ws, size_t ws_bytes,
+                              hipStream_t stream)
 {
     if(g.m == 0 || g.n == 0) return hipSuccess;
     const int      vec_ok = out_vec_ok(g);
@@ -131,6 +167,16 @@ hipError_t launch_gemm_decode(const GemmArgs& g, bool packed, hipStream_t stream
     for(uint32_t n0 = 0; n0 < g.n; n0 += step) {
         const KArgs p = n_panel(g, n0, std::min(step, g.n - n0), packed);
         hipError_t  e;
+        if(packed && decode_wide_shape(g) && ws != nullptr) {
+            // the workspace holds every panel's partials (panels run in stream order)
+            const uint32_t splits = decode_wide_splits(g, p.n);
+            if(gemm::decode_ws_bytes(g.m, p.n, splits) <= ws_bytes) {
+                e = gemm::launch_decode_wide<DecWide>(p, g.out_type, vec_ok,
+                                                      static_cast<int32_t*>(ws), splits, stream);
+                if(e != hipSuccess) return e;
+                continue;
+            }
+        }
         if(packed) {
             if(g.m <= 16 || (g.m <= 32 && !wide))
                 e = gemm::launch_decode<DecSmall, true>(p, g.out_type, vec_ok, stream);
@@ -151,10 +197,10 @@ hipError_t launch_gemm_decode(const GemmArgs& g, bool packed, hipStream_t stream
     return hipSuccess;
 }
 
-hipError_t launch_gemm_packed(const GemmArgs& g, hipStream_t stream)
+hipError_t launch_gemm_packed(const GemmArgs& g, void* ws, size_t ws_bytes, hipStream_t stream)
 {
     if(g.m == 0 || g.n == 0) return hipSuccess;
-    if(gemm_decode_ok(g)) return launch_gemm_decode(g, true, stream);
+    if(gemm_decode_ok(g)) return launch_gemm_decode(g, true, ws, ws_bytes, stream);
     const size_t   esz    = g.out_type == W8A8_OUT_I32 ? 4 : 2;
     const int      vec_ok = out_vec_ok(g);
     constexpr size_t kLimit = 0x7FFFFFFFull;
@@ -208,7 +254,7 @@ bool gemm_packed_ok(const GemmArgs& g)
 hipError_t launch_gemm_nk(const GemmArgs& g, hipStream_t stream)
 {
     if(g.m == 0 || g.n == 0) return hipSuccess;
-    if(gemm_decode_ok(g)) return launch_gemm_decode(g, false, stream);
+    if(gemm_decode_ok(g)) return launch_gemm_decode(g, false, nullptr, 0, stream);
     const size_t esz    = g.out_type == W8A8_OUT_I32 ? 4 : 2;
     const int    vec_ok = out_vec_ok(g);
     // The tile kernel addresses each operand through a buffer resource whose

@@ -70,7 +70,8 @@ hipError_t launch_gemm_nk(const GemmArgs& g, hipStream_t stream);
 // waves of a block.  `packed`: g.b holds packed weights (g.ldb unused).
 constexpr uint32_t kDecodeMaxM = 64;
 bool       gemm_decode_ok(const GemmArgs& g);
-hipError_t launch_gemm_decode(const GemmArgs& g, bool packed, hipStream_t stream);
+hipError_t launch_gemm_decode(const GemmArgs& g, bool packed, void* ws, size_t ws_bytes,
+                              hipStream_t stream);
 
 // Packed weights: [n, k] int8 rearranged into MFMA register order, 64-row
 // slabs x 128-deep k-tiles of 8 KiB, zero padded (n to 64, k to 128).
@@ -93,7 +94,11 @@ hipError_t launch_quantize_weights(const WeightQuant& p, bool divide, bool packe
 // GEMM over packed weights (g.ldb unused).  gemm_packed_ok: 16-byte aligned
 // A, lda % 16 == 0, k % 16 == 0 and every A panel addressable (< 2 GiB).
 bool       gemm_packed_ok(const GemmArgs& g);
-hipError_t launch_gemm_packed(const GemmArgs& g, hipStream_t stream);
+hipError_t launch_gemm_packed(const GemmArgs& g, void* ws, size_t ws_bytes, hipStream_t stream);
+// Split-K workspace the packed path can use for this problem (decode shapes
+// 32 < m <= 64); 0 when none is used.  A smaller (or no) workspace falls back
+// to the unsplit decode kernel.
+size_t     packed_workspace_bytes(const GemmArgs& g);
 
 // Generic strided GEMM (any layout/alignment): A(m,k) = a[m*sam + k*sak],
 // B(n,k) = b[n*sbn + k*sbk].  Slow; used for odd shapes.

@@ -145,7 +145,7 @@ def test_pack_weights_validation(w8a8):
 
 def _packed_args(**kw):
     base = dict(m=1, n=64, k=64, a=FAKE, w=FAKE, c=FAKE, lda=64, ldc=64, sa=None, sb=None,
-                tsa=1.0, tsb=1.0, out=W.OUT_F16, stream=None)
+                tsa=1.0, tsb=1.0, out=W.OUT_F16, ws=None, ws_bytes=0, stream=None)
     base.update(kw)
     return list(base.values())
 
@@ -160,6 +160,7 @@ def _packed_args(**kw):
     (dict(k=40, lda=48), W.ERROR_NOT_SUPPORTED, "k % 16"),
     (dict(lda=72), W.ERROR_NOT_SUPPORTED, "lda % 16"),
     (dict(a=ctypes.c_void_p(0x1001)), W.ERROR_NOT_SUPPORTED, "aligned A"),
+    (dict(ws=ctypes.c_void_p(0x2004), ws_bytes=1 << 20), W.ERROR_INVALID_VALUE, "workspace"),
     (dict(m=1000, lda=(1 << 23) + 16), W.ERROR_NOT_SUPPORTED, "2 GiB"),
     (dict(m=64, lda=(1 << 26) + 16), W.ERROR_NOT_SUPPORTED, "2 GiB"),
 ])
@@ -169,7 +170,7 @@ def test_gemm_packed_validation(w8a8, kw, code, needle):
 
 
 def test_fused_packed_validation(w8a8):
-    args = [FAKE, FAKE, FAKE, FAKE, FAKE, 4, 64, 64, 0, 0, FAKE, FAKE, None]
+    args = [FAKE, FAKE, FAKE, FAKE, FAKE, 4, 64, 64, 0, 0, FAKE, FAKE, None, 0, None]
     bad = list(args)
     bad[3] = None
     assert _status("w8a8_fused_sq_gemm_packed", *bad)[0] == W.ERROR_INVALID_VALUE
@@ -343,3 +344,16 @@ def _wq_args(**kw):
 def test_quantize_weights_validation(w8a8, kw, needle):
     rc, msg = _status("w8a8_quantize_weights", *_wq_args(**kw))
     assert rc == W.ERROR_INVALID_VALUE and needle in msg, msg
+
+
+def test_packed_workspace_size(w8a8):
+    lib = W.library()
+    # decode shapes 32 < m <= 64 take int32 split-K partials: splits * m * ceil4(n) * 4
+    for m, n, k in ((64, 28672, 8192), (48, 8192, 28672), (33, 1000, 4096)):
+        size = lib.w8a8_gemm_packed_workspace_size(m, n, k)
+        ld = -(-n // 4) * 4
+        assert size % (m * ld * 4) == 0 and size > 0, (m, n, k, size)
+    # other shapes take none
+    for m, n, k in ((1, 28672, 8192), (16, 4096, 4096), (32, 4096, 4096), (65, 4096, 4096),
+                    (0, 64, 64)):
+        assert lib.w8a8_gemm_packed_workspace_size(m, n, k) == 0

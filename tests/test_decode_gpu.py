@@ -170,3 +170,59 @@ def test_config4_fused_decode(w8a8, gpu, config4_weights, m):
         assert_f16_bitexact(host(c_pk), exp)
         assert np.array_equal(host(c_pl).view(np.uint16), host(c_pk).view(np.uint16))
         del pw
+
+
+# 32 < m <= 64 over packed weights with a workspace: the wide decode kernel
+# (A k-tile shared through LDS, K split across blocks, int32 partials summed by
+# a second kernel).  Every result must equal the unsplit kernel's bit for bit.
+WIDE_SHAPES = [(64, 4096, 4096), (33, 1000, 4112), (48, 300, 2048), (64, 70, 8192),
+               (40, 28672, 1024), (64, 8192, 14336), (57, 513, 256)]
+
+
+@pytest.mark.parametrize("m,n,k", WIDE_SHAPES)
+def test_wide_decode_matches_unsplit(w8a8, gpu, m, n, k):
+    import torch
+    a, b, sa, sb = inputs(m, n, k, 3000 + m + n + k)
+    ad, sad, sbd = dev(a, gpu), dev(sa, gpu), dev(sb, gpu)
+    pw = w8a8.pack_weights(dev(b, gpu))
+    assert w8a8.gemm_packed_workspace_size(m, n, k) > 0 or k // 128 < 16
+    i_ws = w8a8.gemm_packed(ad, pw, out_dtype=torch.int32)
+    i_no = w8a8.gemm_packed(ad, pw, out_dtype=torch.int32, workspace=None)
+    assert_i32_equal(host(i_ws), O.gemm_i32(a, b))
+    assert_i32_equal(host(i_no), host(i_ws))
+    f_ws = w8a8.gemm_packed(ad, pw, sad, sbd)
+    f_no = w8a8.gemm_packed(ad, pw, sad, sbd, workspace=None)
+    assert_f16_bitexact(host(f_ws), O.dequant_f16(O.gemm_i32(a, b), sa, sb))
+    assert np.array_equal(host(f_ws).view(np.uint16), host(f_no).view(np.uint16))
+
+
+def test_wide_decode_single_split_and_ldc(w8a8, gpu):
+    # a workspace of any size with a shape that takes one split: the wide
+    # kernel runs its own epilogue; output rows with a padded stride
+    import torch
+    m, n, k = 64, 2048, 1024  # 8 k-tiles: one split
+    assert w8a8.gemm_packed_workspace_size(m, n, k) == 0
+    a, b, sa, sb = inputs(m, n, k, 77)
+    pw = w8a8.pack_weights(dev(b, gpu))
+    ws = torch.empty(16, dtype=torch.uint8, device=gpu)
+    big = torch.full((m, n + 8), 3, dtype=torch.int32, device=gpu)
+    w8a8.gemm_packed(dev(a, gpu), pw, out=big[:, :n], workspace=ws)
+    got = host(big)
+    assert_i32_equal(got[:, :n], O.gemm_i32(a, b))
+    assert (got[:, n:] == 3).all()
+    c = w8a8.gemm_packed(dev(a, gpu), pw, dev(sa, gpu), dev(sb, gpu), workspace=ws)
+    assert_f16_bitexact(host(c), O.dequant_f16(O.gemm_i32(a, b), sa, sb))
+
+
+def test_wide_decode_workspace_reuse(w8a8, gpu):
+    # consecutive calls share one workspace (stream order): a larger then a
+    # smaller problem
+    import torch
+    n, k = 4096, 8192
+    a, b, _, _ = inputs(64, n, k, 91)
+    ad = dev(a, gpu)
+    pw = w8a8.pack_weights(dev(b, gpu))
+    ws = torch.empty(w8a8.gemm_packed_workspace_size(64, n, k), dtype=torch.uint8, device=gpu)
+    for m in (64, 40):
+        c = w8a8.gemm_packed(ad[:m], pw, out_dtype=torch.int32, workspace=ws)
+        assert_i32_equal(host(c), O.gemm_i32(a[:m], b))
