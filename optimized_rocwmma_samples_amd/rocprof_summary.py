@@ -36,6 +36,20 @@ def _rows(pattern: str):
             yield from csv.DictReader(f)
 
 
+def _grid(r: dict) -> str:
+    """Total work-items of a dispatch: the kernel trace gives X, Y, Z apart
+    (a 2-D launch such as a split-K grid would otherwise show only X)."""
+    if r.get("Grid_Size"):
+        return r["Grid_Size"]
+    dims = [r.get(f"Grid_Size_{a}") for a in "XYZ"]
+    if not dims[0]:
+        return "?"
+    total = 1
+    for d in dims:
+        total *= int(d) if d else 1
+    return str(total)
+
+
 def trace(directory: str, match: str = "w8a8|gemm|sq_|neg") -> str:
     groups = defaultdict(list)
     for r in _rows(os.path.join(directory, "**", "*kernel_trace.csv")):
@@ -43,8 +57,7 @@ def trace(directory: str, match: str = "w8a8|gemm|sq_|neg") -> str:
         if not re.search(match, name):
             continue
         dur = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
-        grid = r.get("Grid_Size") or r.get("Grid_Size_X") or "?"
-        groups[(short_name(name), grid)].append(dur)
+        groups[(short_name(name), _grid(r))].append(dur)
     out = [f"{'kernel':60s} {'grid':>9s} {'calls':>5s} {'avg_us':>10s} {'min_us':>10s}"]
     for (name, grid), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
         out.append(f"{name[:60]:60s} {grid:>9s} {len(d):5d} {sum(d) / len(d) / 1e3:10.2f} "
