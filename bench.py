@@ -321,6 +321,7 @@ def bench_moe(torch, w8a8, dev, gen, iters=10):
     r2 = torch.empty(cap, dtype=torch.float32, device=dev)
     y = torch.empty((cap, h), dtype=torch.float16, device=dev)
     out = torch.empty((t, h), dtype=torch.float16, device=dev)
+    ws = torch.empty(w8a8.moe_gemm_workspace_size(e, cap, h, inter), dtype=torch.uint8, device=dev)
     stages = ["route", "sort", "quant", "gate_up", "silu_quant", "down", "combine"]
 
     def chain(ev=None):
@@ -332,11 +333,11 @@ def bench_moe(torch, w8a8, dev, gen, iters=10):
         mark(2)
         w8a8.moe_smoothquant(x, s, ids, dst_row=srt["dst_row"], rows=cap, out=qa, row_scale=ra)
         mark(3)
-        w8a8.moe_gemm(qa, wgu, srt["start"], srt["count"], ra, sgu, out=gu)
+        w8a8.moe_gemm(qa, wgu, srt["start"], srt["count"], ra, sgu, out=gu, workspace=ws)
         mark(4)
         w8a8.moe_silu_mul_quant(gu, srt["start"], srt["count"], q=q2, row_scale=r2)
         mark(5)
-        w8a8.moe_gemm(q2, wd, srt["start"], srt["count"], r2, sd, out=y)
+        w8a8.moe_gemm(q2, wd, srt["start"], srt["count"], r2, sd, out=y, workspace=ws)
         mark(6)
         w8a8.moe_combine(y, w, srt["dst_row"], out=out)
         mark(7)

@@ -320,12 +320,23 @@ int w8a8_moe_sort(const int32_t* topk_ids, uint32_t tokens, uint32_t topk, uint3
  * per-expert arrays are read on the device (the output of w8a8_moe_sort), so
  * nothing is synchronized with the host; rows outside [0, rows) are never
  * touched, whatever the arrays hold.
+ * workspace (optional, 16-byte aligned, w8a8_moe_gemm_workspace_size bytes;
+ * NULL or smaller: not used): when the tiles' last round would leave at
+ * least half the CUs idle, its tiles are split along K over those CUs, the
+ * int32 partials go to the workspace and a second launch sums them (exact:
+ * results are bit-identical with and without a workspace).  The rocWMMA
+ * split-K sample likewise takes a caller-allocated workspace
+ * (rocwmma_gemm_splitk.cpp:214).  Calls that share a workspace must be
+ * ordered on one stream.
  */
+size_t w8a8_moe_gemm_workspace_size(uint32_t experts, uint32_t rows, uint32_t n, uint32_t k);
+
 int w8a8_moe_gemm(uint32_t experts, uint32_t rows, uint32_t n, uint32_t k, const int8_t* a,
                   uint32_t lda, const int8_t* w, uint32_t ldw, uint64_t w_expert_stride, void* c,
                   uint32_t ldc, const float* scale_a, const float* scale_w,
                   float tensor_scale_a, float tensor_scale_b, const int32_t* expert_start,
-                  const int32_t* expert_count, int out_type, hipStream_t stream);
+                  const int32_t* expert_count, int out_type, void* workspace, size_t ws_bytes,
+                  hipStream_t stream);
 
 /*
  * SiLU(gate) * up requantization between the expert GEMMs: row r of

@@ -36,9 +36,10 @@ from ._lib import (  # noqa: F401
 __all__ = [
     "library", "version", "smoothquant", "moe_smoothquant", "gemm", "gemm_workspace_size",
     "fused_sq_gemm", "W8A8Error", "PackedWeights", "pack_weights", "pack_weights_size",
-    "gemm_packed", "gemm_packed_workspace_size", "fused_sq_gemm_packed", "grouped_gemm", "topk_softmax", "moe_sort",
-    "moe_gemm", "moe_silu_mul_quant", "moe_combine", "moe_ffn", "add_rmsnorm_smoothquant",
-    "rmsnorm", "add_rmsnorm", "quantize_weights",
+    "gemm_packed", "gemm_packed_workspace_size", "fused_sq_gemm_packed", "grouped_gemm",
+    "topk_softmax", "moe_sort", "moe_gemm", "moe_gemm_workspace_size", "moe_silu_mul_quant",
+    "moe_combine", "moe_ffn", "add_rmsnorm_smoothquant", "rmsnorm", "add_rmsnorm",
+    "quantize_weights",
 ]
 
 
@@ -312,11 +313,15 @@ def gemm_packed_workspace_size(m: int, n: int, k: int) -> int:
 
 
 def _packed_workspace(workspace, m, n, k, device):
+    return _workspace(workspace, lambda: gemm_packed_workspace_size(m, n, k), device)
+
+
+def _workspace(workspace, size_fn, device):
     # "auto": allocate what the library asks for; None: run without (unsplit)
     if isinstance(workspace, str):
         if workspace != "auto":
             raise ValueError("workspace must be 'auto', None or a device tensor")
-        size = gemm_packed_workspace_size(m, n, k)
+        size = size_fn()
         if size == 0:
             return None, 0
         workspace = _torch().empty(size, dtype=_torch().uint8, device=device)
@@ -426,9 +431,18 @@ def moe_sort(topk_ids, experts: int, unit_size: int = 32):
     return out
 
 
+def moe_gemm_workspace_size(experts: int, rows: int, n: int, k: int) -> int:
+    """Bytes of the optional moe_gemm workspace (tail split along K)."""
+    return int(library().w8a8_moe_gemm_workspace_size(experts, rows, n, k))
+
+
 def moe_gemm(a, w, expert_start, expert_count, scale_a=None, scale_w=None, out_dtype=None,
-             out=None, tensor_scale_a: float = 1.0, tensor_scale_b: float = 1.0):
-    """Expert GEMM over expert-sorted rows: a int8 [rows, K], w int8 [E, N, K]."""
+             out=None, tensor_scale_a: float = 1.0, tensor_scale_b: float = 1.0,
+             workspace="auto"):
+    """Expert GEMM over expert-sorted rows: a int8 [rows, K], w int8 [E, N, K].
+    workspace: 'auto' (allocated here), None (no tail split), or a
+    preallocated device tensor of moe_gemm_workspace_size bytes; the result
+    is bit-identical either way."""
     torch = _torch()
     _require_cuda(a, w, expert_start, expert_count, scale_a, scale_w)
     out_dtype = out_dtype or torch.float16
@@ -438,10 +452,11 @@ def moe_gemm(a, w, expert_start, expert_count, scale_a=None, scale_w=None, out_d
         raise ValueError(f"a has K={k}, weights K={kw}")
     c = out if out is not None else torch.empty((rows, n), dtype=out_dtype, device=a.device)
     otype = OUT_I32 if c.dtype == torch.int32 else OUT_F16
+    ws, ws_bytes = _workspace(workspace, lambda: moe_gemm_workspace_size(e, rows, n, k), a.device)
     _lib.call("w8a8_moe_gemm", e, rows, n, k, _ptr(a), a.stride(0), _ptr(w), w.stride(1),
               w.stride(0), _ptr(c), c.stride(0), _ptr(scale_a), _ptr(scale_w),
               float(tensor_scale_a), float(tensor_scale_b), _ptr(expert_start),
-              _ptr(expert_count), otype, _stream(a.device))
+              _ptr(expert_count), otype, _ptr(ws), ws_bytes, _stream(a.device))
     return c
 
 
@@ -489,8 +504,10 @@ def moe_ffn(x, logits, smooth_scale, w_gate_up, sb_gate_up, w_down, sb_down, top
     qa = torch.empty((rows, h), dtype=torch.int8, device=x.device)
     ra = torch.empty(rows, dtype=torch.float32, device=x.device)
     moe_smoothquant(x, smooth_scale, ids, dst_row=srt["dst_row"], rows=rows, out=qa, row_scale=ra)
-    gu = moe_gemm(qa, w_gate_up, srt["start"], srt["count"], ra, sb_gate_up)
+    ws = torch.empty(moe_gemm_workspace_size(e, rows, h, w_down.shape[2]), dtype=torch.uint8,
+                     device=x.device)
+    gu = moe_gemm(qa, w_gate_up, srt["start"], srt["count"], ra, sb_gate_up, workspace=ws)
     q2, r2 = moe_silu_mul_quant(gu, srt["start"], srt["count"], smooth_scale_down)
-    y = moe_gemm(q2, w_down, srt["start"], srt["count"], r2, sb_down)
+    y = moe_gemm(q2, w_down, srt["start"], srt["count"], r2, sb_down, workspace=ws)
     out = moe_combine(y, w, srt["dst_row"])
     return out, dict(weights=w, ids=ids, sort=srt, qa=qa, ra=ra, gate_up=gu, q2=q2, r2=r2, y=y)

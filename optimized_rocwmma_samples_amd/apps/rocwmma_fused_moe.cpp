@@ -25,6 +25,8 @@ static void test_fused_moe(uint32_t t, uint32_t h, uint32_t inter, uint32_t e, u
     app::Dev<float>    dl(hl), ds(hs), dsgu(hsgu), dsd(hsd), w((size_t)t * k), ra(cap), r2(cap);
     app::Dev<int8_t>   dwgu(hwgu), dwd(hwd), qa((size_t)cap * h), q2((size_t)cap * inter);
     app::Dev<int32_t>  ids((size_t)t * k), cnt(e), st(e + 1), pad(e), srt(cap), dst((size_t)t * k);
+    const size_t       wsb = w8a8_moe_gemm_workspace_size(e, cap, h, inter);
+    app::Dev<int8_t>   ws(wsb);
     auto fn = [&] {
         CHECK_W8A8(w8a8_topk_softmax(dl.p, 0, w.p, ids.p, t, e, k, nullptr));
         CHECK_W8A8(w8a8_moe_sort(ids.p, t, k, e, 32, cnt.p, st.p, pad.p, srt.p, cap, dst.p, nullptr));
@@ -32,12 +34,12 @@ static void test_fused_moe(uint32_t t, uint32_t h, uint32_t inter, uint32_t e, u
                                         cap, nullptr));
         CHECK_W8A8(w8a8_moe_gemm(e, cap, 2 * inter, h, qa.p, h, dwgu.p, h, (uint64_t)2 * inter * h,
                                  gu.p, 2 * inter, ra.p, dsgu.p, 1.f, 1.f, st.p, cnt.p,
-                                 W8A8_OUT_F16, nullptr));
+                                 W8A8_OUT_F16, ws.p, wsb, nullptr));
         CHECK_W8A8(w8a8_moe_silu_mul_quant(gu.p, 2 * inter, nullptr, st.p, cnt.p, e, cap, inter,
                                            q2.p, inter, r2.p, 127.f, nullptr));
         CHECK_W8A8(w8a8_moe_gemm(e, cap, h, inter, q2.p, inter, dwd.p, inter, (uint64_t)h * inter,
                                  y.p, h, r2.p, dsd.p, 1.f, 1.f, st.p, cnt.p, W8A8_OUT_F16,
-                                 nullptr));
+                                 ws.p, wsb, nullptr));
         CHECK_W8A8(w8a8_moe_combine(y.p, h, cap, w.p, dst.p, t, k, h, out.p, h, nullptr));
     };
     const double ms    = app::bench_ms(fn, 3, 10);

@@ -496,11 +496,18 @@ int w8a8_moe_sort(const int32_t* topk_ids, uint32_t tokens, uint32_t topk, uint3
                       fn);
 }
 
+size_t w8a8_moe_gemm_workspace_size(uint32_t experts, uint32_t rows, uint32_t n, uint32_t k)
+{
+    if(experts == 0 || rows == 0 || n == 0 || k == 0) return 0;
+    return w8a8::moe_gemm_workspace_bytes();
+}
+
 int w8a8_moe_gemm(uint32_t experts, uint32_t rows, uint32_t n, uint32_t k, const int8_t* a,
                   uint32_t lda, const int8_t* w, uint32_t ldw, uint64_t w_expert_stride, void* c,
                   uint32_t ldc, const float* scale_a, const float* scale_w,
                   float tensor_scale_a, float tensor_scale_b, const int32_t* expert_start,
-                  const int32_t* expert_count, int out_type, hipStream_t stream)
+                  const int32_t* expert_count, int out_type, void* workspace, size_t ws_bytes,
+                  hipStream_t stream)
 {
     const char* fn = "w8a8_moe_gemm";
     if(!a || !w || !c || !expert_start || !expert_count)
@@ -520,10 +527,12 @@ int w8a8_moe_gemm(uint32_t experts, uint32_t rows, uint32_t n, uint32_t k, const
                     "%s: needs 16-byte aligned a/w, lda, ldw, k, w_expert_stride %% 16 == 0", fn);
     if((uint64_t)rows * lda > 0x7FFFFFFFull || (uint64_t)n * ldw > 0x7FFFFFFFull)
         return fail(W8A8_ERROR_NOT_SUPPORTED, "%s: a or one expert's weights over 2 GiB", fn);
+    if(workspace && reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: workspace must be 16-byte aligned", fn);
     if(rows == 0) return hip_status(hipSuccess, fn);
     w8a8::MoeGemmArgs g{a,    w,   c,   scale_a, scale_w, expert_start, expert_count,
                         rows, experts, n, k, lda, ldw, ldc, w_expert_stride, tensor_scale_a,
-                        tensor_scale_b, out_type};
+                        tensor_scale_b, out_type, workspace, workspace ? ws_bytes : 0};
     return hip_status(w8a8::launch_moe_gemm(g, stream), fn);
 }
 

@@ -107,34 +107,70 @@ struct MoeArgs {
     uint32_t       experts, n, k, lda, ldw, ldc;
     uint64_t       w_stride;     // elements between consecutive experts' weights
     float          tsa, tsb;
+    int32_t*       ws;           // tail-split partials (cus slots of Partial<C>) or null
+    uint32_t       cus;          // compute units the split fills (0: no split)
 };
 
-template <class C, int OUT>
-__global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_moe_kernel(MoeArgs q, int vec_ok)
+// Tail split.  With T equal tiles on `cus` CUs the last round holds
+// L = T % cus tiles and leaves the other CUs idle for a whole tile time.
+// When L <= cus / 2 each of those L tiles is cut along K into `parts` pieces
+// (L * parts <= cus) whose int32 partials go to the workspace; the fixup
+// kernel sums them (exact) and runs the usual epilogue.  Tiles [0, base) run
+// whole, as without a split.
+constexpr uint32_t kMaxParts     = 8;
+constexpr uint32_t kMinKtPerPart = 16; // shorter pieces do not repay the partial traffic
+
+struct TailSplit {
+    uint32_t base, left, parts;
+};
+
+__device__ __forceinline__ TailSplit tail_split(uint32_t total, uint32_t cus, uint32_t nk,
+                                                bool enabled)
 {
-    extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
+    TailSplit s{total, 0u, 1u};
+    if(!enabled || cus < 2) return s;
+    const uint32_t left = total % cus;
+    if(left == 0 || left > cus / 2) return s;
+    const uint32_t parts = min(min(cus / left, nk / kMinKtPerPart), kMaxParts);
+    if(parts < 2) return s;
+    return TailSplit{total - left, left, parts};
+}
+
+// Rows of expert e, clamped to the buffers: a corrupt count can never make a
+// block read or write outside a, c or sa.
+__device__ __forceinline__ uint32_t moe_rows_of(const MoeArgs& q, uint32_t e)
+{
+    const int32_t st = q.expert_start[e], cnt = q.expert_count[e];
+    if(st < 0 || cnt <= 0 || (uint32_t)st >= q.rows) return 0u;
+    return min((uint32_t)cnt, q.rows - (uint32_t)st);
+}
+
+template <class C>
+__device__ __forceinline__ uint32_t moe_total_tiles(const MoeArgs& q)
+{
     const uint32_t tiles_n = (q.n + C::kBN - 1) / C::kBN;
-    // rows of expert e, clamped to the buffers: a corrupt count can never
-    // make a block read or write outside a, c or sa
-    auto rows_of = [&](uint32_t e) -> uint32_t {
-        const int32_t st = q.expert_start[e], cnt = q.expert_count[e];
-        if(st < 0 || cnt <= 0 || (uint32_t)st >= q.rows) return 0u;
-        return min((uint32_t)cnt, q.rows - (uint32_t)st);
-    };
-    auto tiles = [&](uint32_t e) { return (rows_of(e) + C::kBM - 1) / C::kBM * tiles_n; };
+    auto tiles = [&](uint32_t e) { return (moe_rows_of(q, e) + C::kBM - 1) / C::kBM * tiles_n; };
     uint32_t e, first, total;
     find_slot(q.experts, 0xFFFFFFFFu, tiles, e, first, total);
-    if(blockIdx.x >= total) return;
-    const uint32_t lid = xcd_remap(blockIdx.x, total);
+    return total;
+}
+
+// Problem and tile origin of logical MoE tile `lid` (< total).
+template <class C, int OUT>
+__device__ __forceinline__ void moe_tile(const MoeArgs& q, uint32_t lid, KArgs& p, uint32_t& m0,
+                                         uint32_t& n0)
+{
+    const uint32_t tiles_n = (q.n + C::kBN - 1) / C::kBN;
+    auto tiles = [&](uint32_t e) { return (moe_rows_of(q, e) + C::kBM - 1) / C::kBM * tiles_n; };
+    uint32_t e, first, total;
     find_slot(q.experts, lid, tiles, e, first, total);
     const uint32_t row0 = (uint32_t)q.expert_start[e];
-    KArgs          p;
     p.a   = q.a + (size_t)row0 * q.lda;
     p.b   = q.w + (size_t)e * q.w_stride;
     p.c   = static_cast<int8_t*>(q.c) + (size_t)row0 * q.ldc * (OUT == W8A8_OUT_I32 ? 4 : 2);
     p.sa  = q.sa ? q.sa + row0 : nullptr;
     p.sb  = q.sw ? q.sw + (size_t)e * q.n : nullptr;
-    p.m   = rows_of(e);
+    p.m   = moe_rows_of(q, e);
     p.n   = q.n;
     p.k   = q.k;
     p.lda = q.lda;
@@ -142,9 +178,60 @@ __global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_moe_kernel(MoeArgs q, 
     p.ldc = q.ldc;
     p.tsa = q.tsa;
     p.tsb = q.tsb;
-    uint32_t m0, n0;
     local_tile<C>(lid - first, p.m, p.n, m0, n0);
-    gemm_tile<C, OUT>(p, m0, n0, vec_ok, lds);
+}
+
+template <class C, int OUT>
+__global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_moe_kernel(MoeArgs q, int vec_ok)
+{
+    extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
+    const uint32_t  total = moe_total_tiles<C>(q);
+    const uint32_t  nk    = (q.k + C::kBK - 1) / C::kBK;
+    const TailSplit sp    = tail_split(total, q.cus, nk, q.ws != nullptr);
+    if(blockIdx.x < sp.base) {
+        KArgs    p;
+        uint32_t m0, n0;
+        moe_tile<C, OUT>(q, xcd_remap(blockIdx.x, sp.base), p, m0, n0);
+        gemm_tile<C, OUT>(p, m0, n0, vec_ok, lds);
+        return;
+    }
+    const uint32_t x = blockIdx.x - sp.base;
+    if(x >= sp.left * sp.parts) return;
+    const uint32_t slot = x / sp.parts, part = x % sp.parts;
+    KArgs          p;
+    uint32_t       m0, n0;
+    moe_tile<C, OUT>(q, sp.base + slot, p, m0, n0);
+    const uint32_t kt0 = part * nk / sp.parts, kt1 = (part + 1) * nk / sp.parts;
+    gemm_tile<C, OUT, true>(p, m0, n0, vec_ok, lds, kt0, kt1 - kt0,
+                            q.ws + (size_t)x * Partial<C>::kInts);
+}
+
+// Split tiles, kPieces blocks each: a block holds kFixupWaves of the tile's
+// waves, sums their accumulators over the parts in order and runs their part
+// of the tile epilogue.
+template <class C, int OUT>
+__global__ void __launch_bounds__(Partial<C>::kFixupWaves * kWave, 1)
+    gemm_i8_moe_fixup_kernel(MoeArgs q, int vec_ok)
+{
+    extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
+    const uint32_t  total = moe_total_tiles<C>(q);
+    const uint32_t  nk    = (q.k + C::kBK - 1) / C::kBK;
+    const TailSplit sp    = tail_split(total, q.cus, nk, q.ws != nullptr);
+    const uint32_t  slot  = blockIdx.x / Partial<C>::kPieces;
+    const int       wave_base = (int)(blockIdx.x % Partial<C>::kPieces) * Partial<C>::kFixupWaves;
+    if(slot >= sp.left) return;
+    KArgs    p;
+    uint32_t m0, n0;
+    moe_tile<C, OUT>(q, sp.base + slot, p, m0, n0);
+    v16i acc[C::kTilesM][C::kTilesN];
+#pragma unroll
+    for(int i = 0; i < C::kTilesM; ++i)
+#pragma unroll
+        for(int j = 0; j < C::kTilesN; ++j) acc[i][j] = v16i{0};
+    const uint32_t tid = wave_base * kWave + threadIdx.x;
+    for(uint32_t part = 0; part < sp.parts; ++part)
+        add_partial<C>(q.ws + (size_t)(slot * sp.parts + part) * Partial<C>::kInts, tid, acc);
+    tile_epilogue<C, OUT>(p, m0, n0, vec_ok, lds, acc, wave_base);
 }
 
 // One flag per (config, output type, kernel kind): the two output types of a
@@ -178,22 +265,43 @@ hipError_t launch_grouped(const KArgs* groups_dev, uint32_t ngroups, uint32_t to
 }
 
 // Grid bound: every expert's last m tile may be partial, so at most
-// ceil(rows / BM) + experts m tiles in total.
+// ceil(rows / BM) + experts m tiles in total; a tail split adds at most
+// cus - 1 blocks.  The fixup launch has kPieces blocks per split tile (at
+// most cus / 2 split tiles).
+template <class C>
+size_t moe_workspace_bytes(uint32_t cus)
+{
+    return (size_t)cus * Partial<C>::kBytes;
+}
+
 template <class C>
 hipError_t launch_moe(const MoeArgs& q, int out_type, int vec_ok, hipStream_t stream)
 {
     const uint32_t tiles_n = (q.n + C::kBN - 1) / C::kBN;
     const uint64_t bound   = ((uint64_t)(q.rows + C::kBM - 1) / C::kBM + q.experts) * tiles_n;
     if(bound == 0) return hipSuccess;
-    if(bound > 0x7FFFFFFFull) return hipErrorInvalidValue;
+    const bool     split = q.ws != nullptr && q.cus >= 2;
+    const uint64_t grid  = bound + (split ? q.cus : 0);
+    const uint32_t fixup_blocks = q.cus / 2 * Partial<C>::kPieces;
+    if(grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
     if(out_type == W8A8_OUT_I32) {
         raise_lds_once<C, W8A8_OUT_I32, 1>(reinterpret_cast<const void*>(gemm_i8_moe_kernel<C, W8A8_OUT_I32>));
-        hipLaunchKernelGGL((gemm_i8_moe_kernel<C, W8A8_OUT_I32>), dim3((uint32_t)bound),
+        hipLaunchKernelGGL((gemm_i8_moe_kernel<C, W8A8_OUT_I32>), dim3((uint32_t)grid),
                            dim3(C::kThreads), C::kLdsBytes, stream, q, vec_ok);
+        if(split) {
+            hipLaunchKernelGGL((gemm_i8_moe_fixup_kernel<C, W8A8_OUT_I32>), dim3(fixup_blocks),
+                               dim3(Partial<C>::kFixupWaves * kWave), Partial<C>::kFixupLds,
+                               stream, q, vec_ok);
+        }
     } else {
         raise_lds_once<C, W8A8_OUT_F16, 1>(reinterpret_cast<const void*>(gemm_i8_moe_kernel<C, W8A8_OUT_F16>));
-        hipLaunchKernelGGL((gemm_i8_moe_kernel<C, W8A8_OUT_F16>), dim3((uint32_t)bound),
+        hipLaunchKernelGGL((gemm_i8_moe_kernel<C, W8A8_OUT_F16>), dim3((uint32_t)grid),
                            dim3(C::kThreads), C::kLdsBytes, stream, q, vec_ok);
+        if(split) {
+            hipLaunchKernelGGL((gemm_i8_moe_fixup_kernel<C, W8A8_OUT_F16>), dim3(fixup_blocks),
+                               dim3(Partial<C>::kFixupWaves * kWave), Partial<C>::kFixupLds,
+                               stream, q, vec_ok);
+        }
     }
     return hipGetLastError();
 }

@@ -230,7 +230,7 @@ __device__ __forceinline__ void store4(const KArgs& p, uint32_t m, uint32_t n, c
 // a wave store covers whole 128-byte lines of 64 // (kWaveN / 8) rows.
 template <class C>
 __device__ __forceinline__ void epilogue_f16_lds(const KArgs& p, uint32_t m0, uint32_t n0,
-                                                 int vec_ok, int8_t* lds, int wave, int lane,
+                                                 int vec_ok, int8_t* lds, int slot, int lane,
                                                  int wm, int wn,
                                                  const v16i (&acc)[C::kTilesM][C::kTilesN],
                                                  bool mode1, float ab)
@@ -244,7 +244,7 @@ __device__ __forceinline__ void epilogue_f16_lds(const KArgs& p, uint32_t m0, ui
 
     // every wave's fragment reads and LDS loads are done: the ring is free
     block_barrier();
-    int8_t* stage = lds + wave * (C::kWaveM * kRowBytes);
+    int8_t* stage = lds + slot * (C::kWaveM * kRowBytes);
 #pragma unroll
     for(int i = 0; i < C::kTilesM; ++i) {
         const int      row = i * 32 + (lane & 31);
@@ -307,12 +307,81 @@ __device__ __forceinline__ void epilogue_f16_lds(const KArgs& p, uint32_t m0, ui
     }
 }
 
+// int32 accumulators of one tile as a K-split partial: register block
+// q = (i * kTilesN + j) * 4 + g (4 ints) of thread t at ints
+// (q * kThreads + t) * 4, so every store and load of a block is contiguous.
+template <class C>
+struct Partial {
+    static constexpr int    kBlocks = C::kTilesM * C::kTilesN * 4;
+    static constexpr size_t kInts   = (size_t)kBlocks * C::kThreads * 4;
+    static constexpr size_t kBytes  = kInts * 4;
+    // fixup blocks of kFixupWaves waves: the tile's epilogue in kPieces blocks
+    static constexpr int    kFixupWaves = 2;
+    static constexpr int    kPieces     = C::kWaves / kFixupWaves;
+    static constexpr int    kFixupLds   = kFixupWaves * C::kWaveM * C::kWaveN * 2;
+    static_assert(C::kWaves % kFixupWaves == 0, "whole fixup blocks");
+};
+
+template <class C>
+__device__ __forceinline__ void store_partial(int32_t* part,
+                                              const v16i (&acc)[C::kTilesM][C::kTilesN])
+{
+#pragma unroll
+    for(int i = 0; i < C::kTilesM; ++i)
+#pragma unroll
+        for(int j = 0; j < C::kTilesN; ++j)
+#pragma unroll
+            for(int g = 0; g < 4; ++g) {
+                const int q = (i * C::kTilesN + j) * 4 + g;
+                v4i       v = {acc[i][j][g * 4 + 0], acc[i][j][g * 4 + 1], acc[i][j][g * 4 + 2],
+                               acc[i][j][g * 4 + 3]};
+                *reinterpret_cast<v4i*>(part + ((size_t)q * C::kThreads + threadIdx.x) * 4) = v;
+            }
+}
+
+// acc += one partial, for thread `tid` of the tile's layout.  The loads go out
+// in batches of kBatch into a register array before any add, so a thread
+// keeps kBatch loads in flight.
+template <class C>
+__device__ __forceinline__ void add_partial(const int32_t* part, uint32_t tid,
+                                            v16i (&acc)[C::kTilesM][C::kTilesN])
+{
+    constexpr int kBatch = 16;
+    static_assert(Partial<C>::kBlocks % kBatch == 0, "whole batches");
+#pragma unroll
+    for(int b = 0; b < Partial<C>::kBlocks; b += kBatch) {
+        v4i v[kBatch];
+#pragma unroll
+        for(int x = 0; x < kBatch; ++x)
+            v[x] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(
+                part + ((size_t)(b + x) * C::kThreads + tid) * 4));
+        __builtin_amdgcn_sched_barrier(0); // every load of the batch issued before the adds
+#pragma unroll
+        for(int x = 0; x < kBatch; ++x) {
+            const int q = b + x, i = q / (4 * C::kTilesN), j = (q / 4) % C::kTilesN, g = q % 4;
+            acc[i][j][g * 4 + 0] += v[x].x;
+            acc[i][j][g * 4 + 1] += v[x].y;
+            acc[i][j][g * 4 + 2] += v[x].z;
+            acc[i][j][g * 4 + 3] += v[x].w;
+        }
+    }
+}
+
+template <class C, int OUT>
+__device__ __forceinline__ void tile_epilogue(const KArgs& p, uint32_t m0, uint32_t n0,
+                                              int vec_ok, int8_t* lds,
+                                              const v16i (&acc)[C::kTilesM][C::kTilesN],
+                                              int wave_base = 0);
+
 // One BM x BN output tile at (m0, n0) of problem p, computed by the whole
 // block; `lds` is the block's kLdsBytes ring.  Shared by the plain, grouped
 // and MoE kernels, which differ only in how a block finds its tile.
-template <class C, int OUT>
+// PART: only k-tiles [kt0, kt0 + nkt) are summed and the int32 accumulators
+// go to `part` (store_partial layout) instead of through the epilogue.
+template <class C, int OUT, bool PART = false>
 __device__ __forceinline__ void gemm_tile(const KArgs& p, uint32_t m0, uint32_t n0, int vec_ok,
-                                          int8_t* lds)
+                                          int8_t* lds, uint32_t kt0 = 0, uint32_t nkt = 0,
+                                          int32_t* part = nullptr)
 {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); // wave-uniform
     const int lane = threadIdx.x % kWave;
@@ -349,7 +418,7 @@ __device__ __forceinline__ void gemm_tile(const KArgs& p, uint32_t m0, uint32_t 
     const uint32_t lds0 = (uint32_t)(uintptr_t)lds; // LDS byte address of the ring
 
     auto issue_stage = [&](int stage, uint32_t kt) {
-        const uint32_t k0     = kt * C::kBK;
+        const uint32_t k0     = (kt0 + kt) * C::kBK;
         const bool     full_k = k0 + C::kBK <= p.k; // uniform: only a K tail is partial
         const uint32_t sbase  = lds0 + stage * C::kStageBytes + wave * (C::kLoadsA * 1024);
         const uint32_t sbaseb = lds0 + stage * C::kStageBytes + C::kABytes
@@ -411,7 +480,7 @@ __device__ __forceinline__ void gemm_tile(const KArgs& p, uint32_t m0, uint32_t 
     constexpr int kMfma = C::kTilesM * C::kTilesN;
     constexpr int kDs   = C::kTilesM + C::kTilesN;
 
-    const uint32_t nk = (p.k + C::kBK - 1) / C::kBK;
+    const uint32_t nk = PART ? nkt : (p.k + C::kBK - 1) / C::kBK;
 
     // ---- prologue: fill every stage of the ring ----------------------------
     // Tiles past K are still issued (every lane then reads kOob: zeros, no
@@ -460,13 +529,32 @@ __device__ __forceinline__ void gemm_tile(const KArgs& p, uint32_t m0, uint32_t 
     }
     wait_vmcnt<0>(); // no global->LDS write may outlive the workgroup's LDS
 
-    // ---- epilogue ----------------------------------------------------------
-    // acc[i][j][r]: m = m0 + wm*kWaveM + i*32 + lane%32,
-    //               n = n0 + wn*kWaveN + j*32 + (r/4)*8 + (lane/32)*4 + r%4.
+    if constexpr(PART) {
+        store_partial<C>(part, acc);
+        return;
+    }
+    tile_epilogue<C, OUT>(p, m0, n0, vec_ok, lds, acc);
+}
+
+// acc[i][j][r]: m = m0 + wm*kWaveM + i*32 + lane%32,
+//               n = n0 + wn*kWaveN + j*32 + (r/4)*8 + (lane/32)*4 + r%4.
+// A block may hold only waves wave_base, wave_base + 1, ... of the tile (the
+// split-tile fixup); each wave stages through LDS slice threadIdx.x / 64.
+template <class C, int OUT>
+__device__ __forceinline__ void tile_epilogue(const KArgs& p, uint32_t m0, uint32_t n0,
+                                              int vec_ok, int8_t* lds,
+                                              const v16i (&acc)[C::kTilesM][C::kTilesN],
+                                              int wave_base)
+{
+    const int   slot  = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int   wave  = wave_base + slot;
+    const int   lane  = threadIdx.x % kWave;
+    const int   wm    = wave / C::kWavesN;
+    const int   wn    = wave % C::kWavesN;
     const bool  mode1 = (p.sa == nullptr && p.sb == nullptr);
     const float ab    = p.tsa * p.tsb;
     if constexpr(OUT == W8A8_OUT_F16) {
-        epilogue_f16_lds<C>(p, m0, n0, vec_ok, lds, wave, lane, wm, wn, acc, mode1, ab);
+        epilogue_f16_lds<C>(p, m0, n0, vec_ok, lds, slot, lane, wm, wn, acc, mode1, ab);
         return;
     }
 #pragma unroll

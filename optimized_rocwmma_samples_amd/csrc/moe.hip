@@ -205,6 +205,7 @@ struct SiluRows {
     uint32_t        ldq;
     float*          r;
     float           qmax;
+    uint32_t        gu_bytes, q_bytes, s2_bytes; // buffer extents of the vector kernel
 };
 
 // Expert holding sorted row `row`, or -1 for padding / out-of-range rows.
@@ -224,9 +225,35 @@ __device__ __forceinline__ int row_expert(const SiluRows& p, uint32_t row)
     return e;
 }
 
-__device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.f + expf(-g))) * u; }
+// (g / (1 + exp(-g))) * u in about a third of the instructions of expf and
+// the IEEE division (the requantization is VALU-bound with those):
+//   exp(-g) = 2^(ph + pl), ph + pl = -g * log2(e) with log2(e) in two parts
+//   and the product's rounding error recovered by an fma, so v_exp_f32 of ph
+//   times (1 + pl ln 2) is within about an ulp of exp(-g);
+//   g / d from v_rcp_f32 and one residual correction (the quotient is then
+//   the correctly rounded one except in rare near-halfway cases).
+// Where exp(-g) overflows (ph >= 128) the division gives -0, for g = +inf it
+// gives +inf; both are selected explicitly.
+__device__ __forceinline__ float silu_mul(float g, float u)
+{
+    constexpr float kLog2eHi = 1.44269502162933349609375f;   // float(log2 e)
+    constexpr float kLog2eLo = 1.925963033500011079e-8f;     // log2 e - kLog2eHi
+    constexpr float kLn2     = 0.693147180559945309f;
+    const float ph = -g * kLog2eHi;
+    const float pl = __builtin_fmaf(-g, kLog2eLo, __builtin_fmaf(-g, kLog2eHi, -ph));
+    float       e  = __builtin_amdgcn_exp2f(ph);
+    e              = __builtin_fmaf(e, pl * kLn2, e);
+    const float d  = 1.f + e;
+    const float r  = __builtin_amdgcn_rcpf(d);
+    const float q0 = g * r;
+    float       q  = __builtin_fmaf(__builtin_fmaf(-d, q0, g), r, q0);
+    q              = ph >= 128.f ? -0.f : q;
+    q              = g == __builtin_inff() ? g : q;
+    return q * u;
+}
 
-template <int CPL, int WPR, bool VEC>
+// Generic form (any inter, alignment and size): element loads and stores.
+template <int CPL, int WPR>
 __global__ void __launch_bounds__(kSqThreads) silu_quant_kernel(SiluRows p)
 {
     constexpr int kRowsPerBlock = kSqWaves / WPR;
@@ -250,43 +277,16 @@ __global__ void __launch_bounds__(kSqThreads) silu_quant_kernel(SiluRows p)
 #pragma unroll
         for(int j = 0; j < CPL; ++j) {
             const uint32_t c = base + j * (8 * kWave);
-            if(VEC && c + 8 <= n) {
-                const uint4 gr = *reinterpret_cast<const uint4*>(g + c);
-                const uint4 ur = *reinterpret_cast<const uint4*>(u + c);
-                const uint32_t gw[4] = {gr.x, gr.y, gr.z, gr.w};
-                const uint32_t uw[4] = {ur.x, ur.y, ur.z, ur.w};
 #pragma unroll
-                for(int h = 0; h < 4; ++h) {
-                    pv[j * 8 + 2 * h]     = silu_mul(half_bits_to_float(gw[h] & 0xFFFFu),
-                                                     half_bits_to_float(uw[h] & 0xFFFFu));
-                    pv[j * 8 + 2 * h + 1] = silu_mul(half_bits_to_float(gw[h] >> 16),
-                                                     half_bits_to_float(uw[h] >> 16));
+            for(int x = 0; x < 8; ++x) {
+                float a = 0.f;
+                if(c + x < n) {
+                    a = silu_mul(half_bits_to_float(g[c + x]), half_bits_to_float(u[c + x]));
+                    if(s2) a *= s2[c + x];
                 }
-                if(s2) {
-                    const float4 s0 = *reinterpret_cast<const float4*>(s2 + c);
-                    const float4 s1 = *reinterpret_cast<const float4*>(s2 + c + 4);
-                    pv[j * 8 + 0] *= s0.x;
-                    pv[j * 8 + 1] *= s0.y;
-                    pv[j * 8 + 2] *= s0.z;
-                    pv[j * 8 + 3] *= s0.w;
-                    pv[j * 8 + 4] *= s1.x;
-                    pv[j * 8 + 5] *= s1.y;
-                    pv[j * 8 + 6] *= s1.z;
-                    pv[j * 8 + 7] *= s1.w;
-                }
-            } else {
-#pragma unroll
-                for(int x = 0; x < 8; ++x) {
-                    float a = 0.f;
-                    if(c + x < n) {
-                        a = silu_mul(half_bits_to_float(g[c + x]), half_bits_to_float(u[c + x]));
-                        if(s2) a *= s2[c + x];
-                    }
-                    pv[j * 8 + x] = a;
-                }
+                pv[j * 8 + x] = a;
+                amax          = fmaxf(amax, fabsf(a));
             }
-#pragma unroll
-            for(int x = 0; x < 8; ++x) amax = fmaxf(amax, fabsf(pv[j * 8 + x]));
         }
     }
     amax = wave_max(amax);
@@ -306,19 +306,100 @@ __global__ void __launch_bounds__(kSqThreads) silu_quant_kernel(SiluRows p)
 #pragma unroll
     for(int j = 0; j < CPL; ++j) {
         const uint32_t c = base + j * (8 * kWave);
-        int            qi[8];
 #pragma unroll
-        for(int x = 0; x < 8; ++x) qi[x] = quant_i8(pv[j * 8 + x], inv, qmax);
-        if(VEC && c + 8 <= n) {
-            uint2 pk;
-            pk.x = pack4_i8(qi[0], qi[1], qi[2], qi[3]);
-            pk.y = pack4_i8(qi[4], qi[5], qi[6], qi[7]);
-            *reinterpret_cast<uint2*>(qrow + c) = pk;
-        } else {
+        for(int x = 0; x < 8; ++x)
+            if(c + x < n) qrow[c + x] = (int8_t)quant_i8(pv[j * 8 + x], inv, qmax);
+    }
+}
+
+// Vector form (inter % 8 == 0, 16-byte aligned rows, every operand under
+// 2 GiB): no per-lane branch anywhere.  All of a row's gate and up chunks go
+// out at once as raw buffer loads (a chunk past the row or a row past `rows`
+// gets offset kOob and reads zeros, which leave the absmax alone), the
+// expert lookup runs while they are in flight, and the int8 chunks go out as
+// buffer stores that kOob drops (padding rows and columns past inter).
+template <int CPL, int WPR, bool S2>
+__global__ void __launch_bounds__(kSqThreads) silu_quant_vec_kernel(SiluRows p)
+{
+    constexpr int      kRowsPerBlock = kSqWaves / WPR;
+    constexpr int      kSpan         = CPL * 8 * kWave;
+    constexpr uint32_t kOob          = gemm::kOob;
+    const int          wave = threadIdx.x / kWave;
+    const int          lane = threadIdx.x % kWave;
+    const int          rib  = wave / WPR;
+    const int          part = wave % WPR;
+    const uint32_t     row  = blockIdx.x * kRowsPerBlock + rib;
+    const uint32_t     n    = p.inter;
+    const bool         in_rows = row < p.rows;
+
+    const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(p.gu), 0, (int)p.gu_bytes, gemm::kBufferFlags);
+    uint32_t col[CPL]; // column of each 8-element chunk, or kOob
+    v4i      gr[CPL], ur[CPL];
 #pragma unroll
-            for(int x = 0; x < 8; ++x)
-                if(c + x < n) qrow[c + x] = (int8_t)qi[x];
+    for(int j = 0; j < CPL; ++j) {
+        const uint32_t c  = part * kSpan + j * (8 * kWave) + lane * 8;
+        col[j]            = (in_rows && c < n) ? c : kOob;
+        const uint32_t vo = col[j] != kOob ? (row * p.ld_gu + c) * 2 : kOob;
+        gr[j]             = __builtin_amdgcn_raw_buffer_load_b128(rg, vo, 0, 0);
+        ur[j]             = __builtin_amdgcn_raw_buffer_load_b128(rg, vo, n * 2, 0);
+    }
+    const int  e     = in_rows ? row_expert(p, row) : -1;
+    const bool valid = e >= 0;
+
+    float pv[CPL * 8];
+    float amax = 0.f;
+#pragma unroll
+    for(int j = 0; j < CPL; ++j) {
+        const uint32_t gw[4] = {(uint32_t)gr[j].x, (uint32_t)gr[j].y, (uint32_t)gr[j].z,
+                                (uint32_t)gr[j].w};
+        const uint32_t uw[4] = {(uint32_t)ur[j].x, (uint32_t)ur[j].y, (uint32_t)ur[j].z,
+                                (uint32_t)ur[j].w};
+#pragma unroll
+        for(int h = 0; h < 4; ++h) {
+            pv[j * 8 + 2 * h]     = silu_mul(half_bits_to_float(gw[h] & 0xFFFFu),
+                                             half_bits_to_float(uw[h] & 0xFFFFu));
+            pv[j * 8 + 2 * h + 1] = silu_mul(half_bits_to_float(gw[h] >> 16),
+                                             half_bits_to_float(uw[h] >> 16));
         }
+        if constexpr(S2) {
+            // s2[e, col]; a padding row (no expert) reads zeros
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(p.s2), 0, (int)p.s2_bytes, gemm::kBufferFlags);
+            const uint32_t so = (valid && col[j] != kOob) ? (uint32_t)e * n * 4 + col[j] * 4 : kOob;
+            const v4i      s0 = __builtin_amdgcn_raw_buffer_load_b128(rs, so, 0, 0);
+            const v4i      s1 = __builtin_amdgcn_raw_buffer_load_b128(rs, so, 16, 0);
+            const int      sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+            for(int x = 0; x < 8; ++x) pv[j * 8 + x] *= __int_as_float(sv[x]);
+        }
+#pragma unroll
+        for(int x = 0; x < 8; ++x) amax = fmaxf(amax, fabsf(pv[j * 8 + x]));
+    }
+    amax = wave_max(amax);
+    if constexpr(WPR > 1) {
+        __shared__ float red[kSqWaves];
+        if(lane == 0) red[wave] = amax;
+        __syncthreads();
+#pragma unroll
+        for(int w = 0; w < WPR; ++w) amax = fmaxf(amax, red[rib * WPR + w]);
+    }
+    const float qmax = p.qmax;
+    const float rs   = amax / qmax;
+    if(valid && part == 0 && lane == 0) p.r[row] = rs;
+    const float inv = rs > 0.f ? 1.f / rs : 0.f;
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(p.q, 0, (int)p.q_bytes,
+                                                                        gemm::kBufferFlags);
+#pragma unroll
+    for(int j = 0; j < CPL; ++j) {
+        const float* v = pv + j * 8;
+        v2i          pk;
+        pk.x = (int)pack4_i8(quant_i8(v[0], inv, qmax), quant_i8(v[1], inv, qmax),
+                             quant_i8(v[2], inv, qmax), quant_i8(v[3], inv, qmax));
+        pk.y = (int)pack4_i8(quant_i8(v[4], inv, qmax), quant_i8(v[5], inv, qmax),
+                             quant_i8(v[6], inv, qmax), quant_i8(v[7], inv, qmax));
+        __builtin_amdgcn_raw_buffer_store_b64(
+            pk, rq, (valid && col[j] != kOob) ? row * p.ldq + col[j] : kOob, 0, 0);
     }
 }
 
@@ -327,11 +408,14 @@ hipError_t launch_silu_rows(const SiluRows& p, bool vec, hipStream_t stream)
 {
     constexpr int kRowsPerBlock = kSqWaves / WPR;
     const dim3    grid((p.rows + kRowsPerBlock - 1) / kRowsPerBlock);
-    if(vec)
-        hipLaunchKernelGGL((silu_quant_kernel<CPL, WPR, true>), grid, dim3(kSqThreads), 0, stream, p);
+    if(vec && p.s2 != nullptr)
+        hipLaunchKernelGGL((silu_quant_vec_kernel<CPL, WPR, true>), grid, dim3(kSqThreads), 0,
+                           stream, p);
+    else if(vec)
+        hipLaunchKernelGGL((silu_quant_vec_kernel<CPL, WPR, false>), grid, dim3(kSqThreads), 0,
+                           stream, p);
     else
-        hipLaunchKernelGGL((silu_quant_kernel<CPL, WPR, false>), grid, dim3(kSqThreads), 0, stream,
-                           p);
+        hipLaunchKernelGGL((silu_quant_kernel<CPL, WPR>), grid, dim3(kSqThreads), 0, stream, p);
     return hipGetLastError();
 }
 
@@ -438,10 +522,18 @@ hipError_t launch_silu_mul_quant(const uint16_t* gu, uint32_t ld_gu, const float
                                  uint32_t ldq, float* r, float qmax, hipStream_t stream)
 {
     if(rows == 0) return hipSuccess;
-    SiluRows p{gu, ld_gu, s2, expert_start, expert_count, experts, rows, inter, q, ldq, r, qmax};
+    const uint64_t gu_bytes = ((uint64_t)(rows - 1) * ld_gu + 2ull * inter) * 2;
+    const uint64_t q_bytes  = (uint64_t)(rows - 1) * ldq + inter;
+    const uint64_t s2_bytes = (uint64_t)experts * inter * 4;
+    SiluRows p{gu, ld_gu, s2, expert_start, expert_count, experts, rows, inter, q, ldq, r, qmax,
+               (uint32_t)std::min<uint64_t>(gu_bytes, 0xFFFFFFFFull),
+               (uint32_t)std::min<uint64_t>(q_bytes, 0xFFFFFFFFull),
+               (uint32_t)std::min<uint64_t>(s2_bytes, 0xFFFFFFFFull)};
+    constexpr uint64_t kBufLimit = 0x7FFFFFFFull; // offsets stay below kOob
     const bool vec = reinterpret_cast<uintptr_t>(gu) % 16 == 0 && ld_gu % 8 == 0
                      && inter % 8 == 0 && (s2 == nullptr || reinterpret_cast<uintptr_t>(s2) % 16 == 0)
-                     && reinterpret_cast<uintptr_t>(q) % 8 == 0 && ldq % 8 == 0;
+                     && reinterpret_cast<uintptr_t>(q) % 8 == 0 && ldq % 8 == 0
+                     && gu_bytes <= kBufLimit && q_bytes <= kBufLimit && s2_bytes <= kBufLimit;
     const uint32_t n = inter;
     if(n <= 512) return launch_silu_rows<1, 1>(p, vec, stream);
     if(n <= 1024) return launch_silu_rows<2, 1>(p, vec, stream);
@@ -478,6 +570,21 @@ uint32_t grouped_gemm_tiles(uint32_t m, uint32_t n)
            * ((n + GemmGrouped::kBN - 1) / GemmGrouped::kBN);
 }
 
+namespace {
+uint32_t device_cus()
+{
+    static const uint32_t cus = [] {
+        int dev = 0, c = 256;
+        if(hipGetDevice(&dev) == hipSuccess)
+            (void)hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev);
+        return (uint32_t)c;
+    }();
+    return cus;
+}
+} // namespace
+
+size_t moe_gemm_workspace_bytes() { return gemm::moe_workspace_bytes<GemmGrouped>(device_cus()); }
+
 hipError_t launch_moe_gemm(const MoeGemmArgs& a, hipStream_t stream)
 {
     gemm::MoeArgs q;
@@ -498,6 +605,9 @@ hipError_t launch_moe_gemm(const MoeGemmArgs& a, hipStream_t stream)
     q.w_stride     = a.w_stride;
     q.tsa          = a.tsa;
     q.tsb          = a.tsb;
+    const bool split = a.ws != nullptr && a.ws_bytes >= moe_gemm_workspace_bytes();
+    q.ws           = split ? static_cast<int32_t*>(a.ws) : nullptr;
+    q.cus          = split ? device_cus() : 0;
     const size_t esz    = a.out_type == W8A8_OUT_I32 ? 4 : 2;
     const int    vec_ok = reinterpret_cast<uintptr_t>(a.c) % (4 * esz) == 0 && a.ldc % 4 == 0
                        && (a.scale_w == nullptr

@@ -148,7 +148,12 @@ struct MoeGemmArgs {
     uint64_t       w_stride;
     float          tsa, tsb;
     int            out_type;
+    void*          ws;       // tail-split partials, or null (no split)
+    size_t         ws_bytes;
 };
 hipError_t launch_moe_gemm(const MoeGemmArgs& a, hipStream_t stream);
+// Workspace that lets launch_moe_gemm split its last partial round of tiles
+// along K (one int32 tile partial per CU of the current device).
+size_t moe_gemm_workspace_bytes();
 
 } // namespace w8a8

@@ -247,7 +247,7 @@ def test_moe_sort_validation(w8a8):
 def _moe_gemm_args(**kw):
     base = dict(e=8, rows=512, n=256, k=128, a=FAKE, lda=128, w=FAKE, ldw=128, ws=256 * 128,
                 c=FAKE, ldc=256, sa=None, sw=None, tsa=1.0, tsb=1.0, st=FAKE, cnt=FAKE,
-                out=W.OUT_F16, stream=None)
+                out=W.OUT_F16, wsp=None, wsb=0, stream=None)
     base.update(kw)
     return list(base.values())
 
@@ -260,6 +260,7 @@ def _moe_gemm_args(**kw):
     (dict(k=40, lda=48, ldw=48, ws=256 * 48), W.ERROR_NOT_SUPPORTED, "% 16"),
     (dict(rows=1 << 24, lda=256, k=256, ldw=256, ws=256 * 256), W.ERROR_NOT_SUPPORTED, "2 GiB"),
     (dict(out=5), W.ERROR_INVALID_VALUE, "out_type"),
+    (dict(wsp=ctypes.c_void_p(0x1008), wsb=1 << 26), W.ERROR_INVALID_VALUE, "16-byte"),
 ])
 def test_moe_gemm_validation(w8a8, kw, code, needle):
     rc, msg = _status("w8a8_moe_gemm", *_moe_gemm_args(**kw))
@@ -344,6 +345,16 @@ def _wq_args(**kw):
 def test_quantize_weights_validation(w8a8, kw, needle):
     rc, msg = _status("w8a8_quantize_weights", *_wq_args(**kw))
     assert rc == W.ERROR_INVALID_VALUE and needle in msg, msg
+
+
+def test_moe_gemm_workspace_size(w8a8):
+    lib = W.library()
+    # one int32 partial of a 256 x 256 tile (256 KiB) per CU
+    size = lib.w8a8_moe_gemm_workspace_size(8, 8192, 4096, 14336)
+    assert size > 0 and size % (256 * 256 * 4) == 0
+    assert size == W.moe_gemm_workspace_size(8, 64, 128, 128)
+    for dims in ((0, 64, 64, 64), (8, 0, 64, 64), (8, 64, 0, 64), (8, 64, 64, 0)):
+        assert lib.w8a8_moe_gemm_workspace_size(*dims) == 0
 
 
 def test_packed_workspace_size(w8a8):

@@ -163,6 +163,66 @@ def test_moe_gemm_exact(w8a8, gpu, t, k, e, h, n, unit):
         assert_f16_bitexact(cf[r0:r1], O.dequant_f16(acc, sa[r0:r1], sw[x]))
 
 
+def _tail_split_parts(total, cus, nk):
+    # host restatement of the kernel's tail split rule (which tiles run in
+    # K pieces), used only to check that a test shape takes that path
+    left = total % cus
+    if left == 0 or left > cus // 2:
+        return 0, 1
+    parts = min(cus // left, nk // 16, 8)
+    return (left, parts) if parts >= 2 else (0, 1)
+
+
+# (expert row counts, K, N) on 256 CUs: 18 tile rows x 16 = 288 tiles leave
+# 32 tail tiles (expert 2, whose second tile row holds 44 rows) cut in 2;
+# 3 tile rows x 2 = 6 tiles (fewer than the CUs) each cut in 8; one expert
+# of 17 tile rows (16 tail tiles cut in 2); an empty expert between two
+# others (96 tiles, all cut in 2)
+SPLIT_CASES = [([1000, 3000, 300], 4096, 4096), ([200, 300], 16384, 512),
+               ([4352], 4096, 4096), ([700, 0, 520], 4096, 4096)]
+
+
+@pytest.mark.parametrize("counts,k,n", SPLIT_CASES)
+def test_moe_gemm_tail_split_exact(w8a8, gpu, counts, k, n):
+    import torch
+    unit = 32
+    count = np.array(counts, np.int32)
+    padded = -(-count // unit) * unit
+    start = np.concatenate([[0], np.cumsum(padded)]).astype(np.int32)
+    rows, e = int(start[-1]), len(counts)
+    seed = sum(counts) + k
+    a = G.int8(seed, G.TID_A, (rows, k))
+    w = G.int8(seed, G.TID_B, (e, n, k))
+    sa = G.uniform(seed, G.TID_SA, (rows,), 1e-3, 1e-2)
+    sw = G.uniform(seed, G.TID_SB, (e, n), 1e-3, 1e-2)
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
+    total = sum(-(-c // 256) for c in counts) * (-(-n // 256))
+    left, parts = _tail_split_parts(total, cus, -(-k // 128))
+    assert left > 0 and parts >= 2, (total, cus, "shape does not exercise the tail split")
+    args = (dev(a, gpu), dev(w, gpu), dev(start, gpu), dev(count, gpu))
+    kw = dict(scale_a=dev(sa, gpu), scale_w=dev(sw, gpu))
+    ws = torch.empty(w8a8.moe_gemm_workspace_size(e, rows, n, k), dtype=torch.uint8, device=gpu)
+    # two calls sharing the workspace, then the unsplit path
+    ci = host(w8a8.moe_gemm(*args, out_dtype=torch.int32, workspace=ws))
+    cf = host(w8a8.moe_gemm(*args, workspace=ws, **kw))
+    ci0 = host(w8a8.moe_gemm(*args, out_dtype=torch.int32, workspace=None))
+    cf0 = host(w8a8.moe_gemm(*args, workspace=None, **kw))
+    for x in range(e):
+        r0, r1 = start[x], start[x] + count[x]
+        if r1 == r0:
+            continue
+        assert_i32_equal(ci[r0:r1], ci0[r0:r1])
+        assert_f16_bitexact(cf[r0:r1], cf0[r0:r1])
+        # against the oracle on the expert's first and last rows (the last
+        # tile row is the one a tail split cuts) and a random sample
+        pick = np.unique(np.concatenate([np.arange(r0, min(r1, r0 + 8)),
+                                         np.arange(max(r0, r1 - 40), r1),
+                                         np.random.default_rng(x).integers(r0, r1, 24)]))
+        acc = O.gemm_i32(a[pick], w[x])
+        assert_i32_equal(ci[pick], acc)
+        assert_f16_bitexact(cf[pick], O.dequant_f16(acc, sa[pick], sw[x]))
+
+
 def test_moe_gemm_leaves_padding_rows(w8a8, gpu):
     import torch
     t, k, e, h, n, unit = 100, 2, 4, 128, 64, 32
@@ -204,6 +264,38 @@ def test_silu_mul_quant(w8a8, gpu, inter, with_s2):
         if r1 < start[x + 1]:  # padding rows untouched
             assert (qg[r1:start[x + 1]] == 99).all() and (rg[r1:start[x + 1]] == -1).all()
     assert mism <= max(2, int(1e-3 * count.sum() * inter)), f"{mism} off-by-one values"
+
+
+def test_silu_mul_quant_special_values(w8a8, gpu):
+    import torch
+    # one expert, rows of chosen gate values (up = 1 unless stated):
+    #   0: every gate <= -89: exp(-g) overflows, silu = -0, so r = 0, q = 0
+    #   1: a dense sweep of [-20, 20]
+    #   2: the fp16 extremes +-65504 and neighbours of the overflow point
+    #   3: a sweep of [-88.5, -60] next to a gate of 1 (tiny silu values)
+    #   4: up of both signs and zero
+    inter = 4096
+    gu = np.zeros((5, 2 * inter), np.float16)
+    gu[:, inter:] = 1.0
+    gu[0, :inter] = np.linspace(-89.0, -60000.0, inter)
+    gu[1, :inter] = np.linspace(-20.0, 20.0, inter)
+    gu[2, :inter] = np.resize(np.array([65504, -65504, -88.6, -88.75, -87.0, 11.1, -11.1, 0.0],
+                                       np.float16), inter)
+    gu[3, :inter] = np.linspace(-88.5, -60.0, inter)
+    gu[3, 7] = 1.0
+    gu[4, :inter] = np.linspace(-6.0, 6.0, inter)
+    gu[4, inter:] = np.resize(np.array([1.5, -2.0, 0.0, -0.25], np.float16), inter)
+    start = np.array([0], np.int32)
+    count = np.array([5], np.int32)
+    q = torch.full((5, inter), 99, dtype=torch.int8, device=gpu)
+    r = torch.full((5,), -1.0, dtype=torch.float32, device=gpu)
+    w8a8.moe_silu_mul_quant(dev(gu, gpu), dev(start, gpu), dev(count, gpu), None, q=q, row_scale=r)
+    qg, rg = host(q), host(r)
+    qo, ro = O.silu_mul_quant(gu)
+    assert rg[0] == 0 and (qg[0] == 0).all()
+    assert ulp_diff(rg, ro).max() <= 4
+    assert np.abs(qg.astype(np.int32) - qo).max() <= 1
+    assert int((qg != qo).sum()) <= 4
 
 
 def test_moe_combine_exact(w8a8, gpu):
