@@ -406,6 +406,10 @@ hipError_t dispatch(const QuantRows& p, hipStream_t stream)
         if(vec && n % 8 == 0) {
             // (configurations chosen by a sweep on MI355X over CPL, WPR,
             // block size and blocks per CU, cache-warm and cache-cold)
+            // A few rows (decode): the launch is latency-bound, so each row
+            // is spread over all 16 waves of a 1024-thread block.
+            if(p.rows <= 64 && n > 4096 && n <= 8192) return launch_stream<1, 16, 1024>(p, stream);
+            if(p.rows <= 64 && n > 8192 && n <= 16384) return launch_stream<2, 16, 1024>(p, stream);
             if(n <= 512) return launch_stream<1, 1, 512>(p, stream);
             if(n <= 1024) return launch_stream<2, 1, 512>(p, stream);
             if(n <= 2048) return launch_stream<4, 1, 512>(p, stream);

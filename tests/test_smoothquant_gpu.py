@@ -58,6 +58,17 @@ def test_row_lengths(w8a8, gpu, n):
     check_exact(qg, rg, *O.smoothquant(x, s))
 
 
+@pytest.mark.parametrize("m", [1, 64, 65])
+@pytest.mark.parametrize("n", [8192, 12288, 16384, 28672])
+def test_decode_row_counts(w8a8, gpu, m, n):
+    # decode row counts take the one-block-per-row launch (rows <= 64)
+    seed = 300 + m + n
+    x = G.activations(seed, m, n)
+    s = G.uniform(seed, G.TID_S, (n,), 0.5, 2.0)
+    qg, rg = run_sq(w8a8, x, s, gpu)
+    check_exact(qg, rg, *O.smoothquant(x, s))
+
+
 def test_zero_rows_ties_and_qmax(w8a8, gpu):
     n = 1024
     x = np.zeros((4, n), np.float16)
