@@ -119,8 +119,11 @@ uint32_t weight_panel_rows(const GemmArgs& g, bool packed)
     return (uint32_t)std::min<size_t>(g.n, rows);
 }
 
-// K splits of the wide decode kernel for one weight panel: enough blocks for
-// every CU, at least 8 k-tiles per split; 1 = no split.
+// K splits of the wide decode kernel for one weight panel: the count that
+// minimises the weight bytes of the busiest CU, ceil(blocks / CUs) / splits
+// (the fewest splits among equals), at least 8 k-tiles per split; 1 = no
+// split.  E.g. 112 panels of W1 on 256 CUs: 2 splits (224 blocks, one per
+// CU) rather than 3 (336 blocks: 80 CUs would stream two).
 uint32_t decode_wide_splits(const GemmArgs& g, uint32_t n)
 {
     static const uint32_t cus = [] {
@@ -129,11 +132,19 @@ uint32_t decode_wide_splits(const GemmArgs& g, uint32_t n)
             (void)hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev);
         return (uint32_t)c;
     }();
-    const uint32_t nblk  = (n + DecWide::kRows - 1) / DecWide::kRows;
-    const uint32_t nkt   = gemm::packed_ktiles(g.k);
-    const uint32_t want  = (cus + nblk - 1) / nblk;
-    const uint32_t most  = std::max<uint32_t>(1, nkt / 8);
-    return std::max<uint32_t>(1, std::min(want, most));
+    const uint32_t nblk = (n + DecWide::kRows - 1) / DecWide::kRows;
+    const uint32_t nkt  = gemm::packed_ktiles(g.k);
+    const uint32_t most = std::max<uint32_t>(1, std::min<uint32_t>(nkt / 8, 8));
+    uint32_t       best = 1;
+    double         cost = 1e30;
+    for(uint32_t s = 1; s <= most; ++s) {
+        const double c = (double)((nblk * s + cus - 1) / cus) / s;
+        if(c < cost * (1 - 1e-9)) {
+            cost = c;
+            best = s;
+        }
+    }
+    return best;
 }
 
 bool decode_wide_shape(const GemmArgs& g) { return g.m > 32 && g.m <= kDecodeMaxM; }
