@@ -19,8 +19,11 @@ namespace {
 
 using gemm::KArgs;
 
-// Production tile configuration.
-using GemmMain = gemm::Cfg<256, 256, 128, 2, 2, 4, 4>;
+// Production tile configuration, and the smaller tiles of launches that
+// would leave most CUs idle with it (pick_tile_cfg).
+using GemmMain  = gemm::Cfg<256, 256, 128, 2, 2, 4, 4>;
+using GemmMidM  = gemm::Cfg<128, 256, 128, 2, 2, 4, 4>; // 8 waves of 64 x 64
+using GemmSmall = gemm::Cfg<128, 128, 128, 2, 2, 4, 4>; // 8 waves of 64 x 32
 // Packed-weight tile configuration (m > kDecodeMaxM).
 using GemmPacked = gemm::PbCfg<256, 4, 2, 4>;
 // Decode configurations: <32-row m tiles, 32-row weight tiles, waves, ring>.
@@ -119,12 +122,7 @@ uint32_t weight_panel_rows(const GemmArgs& g, bool packed)
     return (uint32_t)std::min<size_t>(g.n, rows);
 }
 
-// K splits of the wide decode kernel for one weight panel: the count that
-// minimises the weight bytes of the busiest CU, ceil(blocks / CUs) / splits
-// (the fewest splits among equals), at least 8 k-tiles per split; 1 = no
-// split.  E.g. 112 panels of W1 on 256 CUs: 2 splits (224 blocks, one per
-// CU) rather than 3 (336 blocks: 80 CUs would stream two).
-uint32_t decode_wide_splits(const GemmArgs& g, uint32_t n)
+uint32_t device_cus()
 {
     static const uint32_t cus = [] {
         int dev = 0, c = 256;
@@ -132,6 +130,37 @@ uint32_t decode_wide_splits(const GemmArgs& g, uint32_t n)
             (void)hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev);
         return (uint32_t)c;
     }();
+    return cus;
+}
+
+// Tile configuration of one launch.  256 x 256 tiles have the best per-op
+// rate once they fill the chip; a launch with fewer than 3/4 of a round of
+// them leaves most CUs idle, and smaller tiles finish it sooner (measured
+// on MI355X, cfg3 shapes: M = 512 qkv 46 -> 25 µs, o_proj 45 -> 22 µs,
+// down 140 -> 71 µs with 128 x 128; M = 2048 o_proj 59 -> 42 µs, down
+// 164 -> 119 µs with 128 x 256; the shapes with enough 256 x 256 tiles, e.g.
+// M = 2048 qkv or gate_up, are slower with smaller ones).
+enum class TileCfg { kMain, kMidM, kSmall };
+
+TileCfg pick_tile_cfg(uint32_t m, uint32_t n)
+{
+    auto tiles = [&](uint32_t bm, uint32_t bn) {
+        return (uint64_t)((m + bm - 1) / bm) * ((n + bn - 1) / bn);
+    };
+    const uint64_t enough = (uint64_t)device_cus() * 3 / 4;
+    if(tiles(GemmMain::kBM, GemmMain::kBN) >= enough) return TileCfg::kMain;
+    if(tiles(GemmMidM::kBM, GemmMidM::kBN) >= enough) return TileCfg::kMidM;
+    return TileCfg::kSmall;
+}
+
+// K splits of the wide decode kernel for one weight panel: the count that
+// minimises the weight bytes of the busiest CU, ceil(blocks / CUs) / splits
+// (the fewest splits among equals), at least 8 k-tiles per split; 1 = no
+// split.  E.g. 112 panels of W1 on 256 CUs: 2 splits (224 blocks, one per
+// CU) rather than 3 (336 blocks: 80 CUs would stream two).
+uint32_t decode_wide_splits(const GemmArgs& g, uint32_t n)
+{
+    const uint32_t cus  = device_cus();
     const uint32_t nblk = (n + DecWide::kRows - 1) / DecWide::kRows;
     const uint32_t nkt  = gemm::packed_ktiles(g.k);
     const uint32_t most = std::max<uint32_t>(1, std::min<uint32_t>(nkt / 8, 8));
@@ -286,7 +315,12 @@ hipError_t launch_gemm_nk(const GemmArgs& g, hipStream_t stream)
             p.c     = static_cast<int8_t*>(g.c) + ((size_t)m0 * g.ldc + n0) * esz;
             p.sa    = g.scale_a ? g.scale_a + m0 : nullptr;
             p.sb    = g.scale_b ? g.scale_b + n0 : nullptr;
-            hipError_t e = gemm::launch_cfg<GemmMain>(p, g.out_type, vec_ok, stream);
+            hipError_t e;
+            switch(pick_tile_cfg(p.m, p.n)) {
+            case TileCfg::kMain: e = gemm::launch_cfg<GemmMain>(p, g.out_type, vec_ok, stream); break;
+            case TileCfg::kMidM: e = gemm::launch_cfg<GemmMidM>(p, g.out_type, vec_ok, stream); break;
+            default: e = gemm::launch_cfg<GemmSmall>(p, g.out_type, vec_ok, stream); break;
+            }
             if(e != hipSuccess) return e;
         }
     }

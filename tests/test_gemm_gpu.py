@@ -45,6 +45,28 @@ def test_f16_dequant_mode2(w8a8, gpu, m, n, k):
     assert_f16_bitexact(host(c), O.dequant_f16(O.gemm_i32(a, b), sa, sb))
 
 
+# The launch picks its tile by how many 256 x 256 tiles there are (256 CUs):
+#   >= 192 of them: 256 x 256; else >= 192 tiles of 128 x 256: 128 x 256;
+#   else 128 x 128.  Each with partial tiles on both edges.
+TILE_CFG_SHAPES = [
+    (4100, 3000, 160),   # 17 x 12 = 204 tiles of 256 x 256
+    (2048, 4096, 512),   # 128 of 256 x 256 -> 256 of 128 x 256
+    (1500, 4000, 272),   # 96 of 256 x 256 -> 192 of 128 x 256, ragged edges
+    (700, 1100, 400),    # 15 of 256 x 256 -> 128 x 128, ragged edges
+]
+
+
+@pytest.mark.parametrize("m,n,k", TILE_CFG_SHAPES)
+def test_tile_configs_exact(w8a8, gpu, m, n, k):
+    import torch
+    a, b, sa, sb = inputs(m, n, k, m + 3 * n + 5 * k)
+    ad, bd = dev(a, gpu), dev(b, gpu)
+    acc = O.gemm_i32(a, b)
+    assert_i32_equal(host(w8a8.gemm(ad, bd, out_dtype=torch.int32)), acc)
+    c = w8a8.gemm(ad, bd, dev(sa, gpu), dev(sb, gpu))
+    assert_f16_bitexact(host(c), O.dequant_f16(acc, sa, sb))
+
+
 def test_f16_dequant_mode1_tensor_scales(w8a8, gpu):
     m, n, k = 256, 512, 256
     a, b, _, _ = inputs(m, n, k, 5)
