@@ -121,8 +121,11 @@ int w8a8_add_rmsnorm_smoothquant(const void* x, const void* residual, const floa
 /* ------------------------------------------------------------------------- */
 
 /*
- * Bytes of device workspace w8a8_gemm needs for this problem (0 for the
- * primary layout; the sample layout is repacked K-contiguous into it).
+ * Bytes of device workspace w8a8_gemm can use for this problem.  Sample
+ * layout: A and B are repacked K-contiguous into it.  Primary layout: int32
+ * K-split partials when the problem's tiles would fill at most half of the
+ * CUs (0 otherwise); the rocWMMA split-K sample likewise takes a
+ * caller-allocated workspace (rocwmma_gemm_splitk.cpp:214).
  */
 size_t w8a8_gemm_workspace_size(uint32_t m, uint32_t n, uint32_t k, int layout);
 
@@ -144,6 +147,12 @@ size_t w8a8_gemm_workspace_size(uint32_t m, uint32_t n, uint32_t k, int layout);
  * gemm_splitk_stage1/gemm_splitk_reduce (rocwmma_gemm_splitk.cpp:104-201) and
  * streamk_gemm_kernel (rocwmma_streamk_gemm.cpp:86-211), in one launch with no
  * workspace, bit-identical to the full GEMM.
+ * Primary layout with a workspace (16-byte aligned, at least
+ * w8a8_gemm_workspace_size bytes; NULL or smaller: not used): a problem
+ * whose tiles fill at most half of the CUs runs each tile as K pieces on the
+ * idle CUs, the pieces' int32 partials go to the workspace and a second
+ * launch sums them, again bit-identical.  Calls sharing a workspace must be
+ * ordered on one stream.
  */
 int w8a8_gemm(uint32_t m, uint32_t n, uint32_t k, const int8_t* a, const int8_t* b, void* c,
               uint32_t lda, uint32_t ldb, uint32_t ldc, const float* scale_a,
@@ -157,11 +166,12 @@ int w8a8_gemm(uint32_t m, uint32_t n, uint32_t k, const int8_t* a, const int8_t*
  *   x fp16 [m, ldx]; w int8 [n, ldw] (K-contiguous weights); c fp16 [m, ldc].
  * q and row_scale are caller-provided buffers (m*k bytes, m floats): they are
  * written, so the caller can reuse the quantized activations for several GEMMs.
+ * workspace / ws_bytes: as for w8a8_gemm (primary layout; NULL, 0 allowed).
  */
 int w8a8_fused_sq_gemm(const void* x, const float* smooth_scale, const int8_t* w,
                        const float* scale_w, void* c, uint32_t m, uint32_t n, uint32_t k,
                        uint32_t ldx, uint32_t ldw, uint32_t ldc, int8_t* q, float* row_scale,
-                       hipStream_t stream);
+                       void* workspace, size_t ws_bytes, hipStream_t stream);
 
 /* ------------------------------------------------------------------------- */
 /* Packed ("pre-shuffled") weights                                            */

@@ -226,8 +226,11 @@ def gemm(a, b, scale_a=None, scale_b=None, tensor_scale_a: float = 1.0,
     return c
 
 
-def fused_sq_gemm(x, smooth_scale, w, scale_w, out=None, q=None, row_scale=None):
-    """SmoothQuant x [M, K] then C = dequant(q . w^T): returns (c fp16 [M, N], q, row_scale)."""
+def fused_sq_gemm(x, smooth_scale, w, scale_w, out=None, q=None, row_scale=None,
+                  workspace=None):
+    """SmoothQuant x [M, K] then C = dequant(q . w^T): returns (c fp16 [M, N], q, row_scale).
+    workspace: None (allocated here when the shape can use a K split, see
+    gemm_workspace_size) or a device tensor; an empty tensor runs unsplit."""
     torch = _torch()
     _require_cuda(x, smooth_scale, w, scale_w)
     m, k = x.shape
@@ -236,9 +239,13 @@ def fused_sq_gemm(x, smooth_scale, w, scale_w, out=None, q=None, row_scale=None)
     q = q if q is not None else torch.empty((m, k), dtype=torch.int8, device=x.device)
     r = row_scale if row_scale is not None else torch.empty(m, dtype=torch.float32,
                                                             device=x.device)
+    if workspace is None:
+        ws_bytes = gemm_workspace_size(m, n, k)
+        if ws_bytes:
+            workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
     _lib.call("w8a8_fused_sq_gemm", _ptr(x), _ptr(smooth_scale), _ptr(w), _ptr(scale_w), _ptr(c),
-              m, n, k, x.stride(0), w.stride(0), c.stride(0), _ptr(q), _ptr(r),
-              _stream(x.device))
+              m, n, k, x.stride(0), w.stride(0), c.stride(0), _ptr(q), _ptr(r), _ptr(workspace),
+              workspace.numel() if workspace is not None else 0, _stream(x.device))
     return c, q, r
 
 

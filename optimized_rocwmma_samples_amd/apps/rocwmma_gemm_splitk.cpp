@@ -2,11 +2,14 @@
 // Stands in for the reference's split-K and stream-K samples
 // (rocwmma_gemm_splitk.cpp:251-263, rocwmma_streamk_gemm.cpp:286-297): m <= 64
 // runs the weight-streaming kernel that splits K across the waves of each
-// block (int32 partials summed in LDS, one launch, no workspace).
+// block (int32 partials summed in LDS, one launch, no workspace); larger m
+// whose tiles fill at most half of the CUs splits each tile along K across
+// blocks into the caller's workspace (int32 partials, a fixup launch sums
+// them), like the reference's workspace-based split-K (:214).
 // `rocwmma_gemm_splitk [M N K]`; default: BASELINE config 4, the Llama-70B MLP
 // weights [28672, 8192] and [8192, 28672] at M in {1, 16, 64}, then the
 // reference's shapes.  Result line
-//   [SplitK-GEMM] M=<M> N=<N> K=<K> split_k=<in-block|none>  <ms> ms  <TF> TFlops/s  <GB/s> GB/s
+//   [SplitK-GEMM] M=<M> N=<N> K=<K> split_k=<in-block|workspace|none>  <ms> ms  <TF> TFlops/s  <GB/s> GB/s
 // (GB/s = weights + activations + scales + output once).
 #include "common.hpp"
 
@@ -20,14 +23,17 @@ static void test_decode(uint32_t m, uint32_t n, uint32_t k, bool verify)
     app::Dev<int8_t>   da(ha), dw(hw);
     app::Dev<float>    dsa(hsa), dsb(hsb);
     app::Dev<uint16_t> dc((size_t)m * n);
+    const size_t       wsb = w8a8_gemm_workspace_size(m, n, k, W8A8_LAYOUT_A_ROW_B_NK);
+    app::Dev<int8_t>   ws(wsb);
     auto fn = [&](void* c, int out) {
         CHECK_W8A8(w8a8_gemm(m, n, k, da.p, dw.p, c, k, k, n, dsa.p, dsb.p, 1.f, 1.f, out,
-                             W8A8_LAYOUT_A_ROW_B_NK, nullptr, 0, nullptr));
+                             W8A8_LAYOUT_A_ROW_B_NK, wsb ? ws.p : nullptr, wsb, nullptr));
     };
     const double ms    = app::bench_ms([&] { fn(dc.p, W8A8_OUT_F16); });
     const double bytes = (double)n * k + (double)m * k + 4.0 * (m + n) + 2.0 * m * n;
     std::cout << "[SplitK-GEMM] M=" << m << " N=" << n << " K=" << k
-              << " split_k=" << (m <= 64 ? "in-block" : "none") << "  " << ms << " ms  "
+              << " split_k=" << (m <= 64 ? "in-block" : wsb ? "workspace" : "none") << "  " << ms
+              << " ms  "
               << 2.0 * m * n * k / (ms * 1e-3) / 1e12 << " TFlops/s  "
               << bytes / (ms * 1e-3) / 1e9 << " GB/s\n";
     if(verify) {

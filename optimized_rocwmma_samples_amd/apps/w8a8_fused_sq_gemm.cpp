@@ -15,9 +15,11 @@ static void test_fused(uint32_t m, uint32_t n, uint32_t k, bool verify)
     app::Dev<uint16_t> dx(hx), dc((size_t)m * n);
     app::Dev<float>    ds(hs), dsb(hsb), dr(m);
     app::Dev<int8_t>   dw(hw), dq((size_t)m * k);
+    const size_t       wsb = w8a8_gemm_workspace_size(m, n, k, W8A8_LAYOUT_A_ROW_B_NK);
+    app::Dev<int8_t>   ws(wsb);
     auto fn = [&] {
         CHECK_W8A8(w8a8_fused_sq_gemm(dx.p, ds.p, dw.p, dsb.p, dc.p, m, n, k, 0, 0, 0, dq.p, dr.p,
-                                      nullptr));
+                                      ws.p, wsb, nullptr));
     };
     const double ms = app::bench_ms(fn);
     std::cout << "[FusedSQ-GEMM] M=" << m << " N=" << n << " K=" << k << "  " << ms << " ms  "

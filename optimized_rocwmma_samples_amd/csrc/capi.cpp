@@ -219,6 +219,12 @@ static uint32_t round_up16(uint32_t v) { return (v + 15u) & ~15u; }
 
 size_t w8a8_gemm_workspace_size(uint32_t m, uint32_t n, uint32_t k, int layout)
 {
+    if(layout == W8A8_LAYOUT_A_ROW_B_NK) {
+        // K-split partials for launches that fill at most half the CUs
+        w8a8::GemmArgs g{m, n, k, nullptr, nullptr, nullptr, k, k, n, nullptr, nullptr, 1.f, 1.f,
+                         W8A8_OUT_F16};
+        return w8a8::gemm_nk_workspace_bytes(g);
+    }
     if(layout != W8A8_LAYOUT_A_COL_B_KN) return 0;
     const size_t kp = round_up16(k);
     // repacked A [m, kp] and B [n, kp], each 256-byte aligned
@@ -282,19 +288,22 @@ int w8a8_gemm(uint32_t m, uint32_t n, uint32_t k, const int8_t* a, const int8_t*
         g.lda = kp;
         g.ldb = kp;
         g.k   = kp; // zero padding contributes nothing
-        return hip_status(w8a8::launch_gemm_nk(g, stream), "w8a8_gemm");
+        return hip_status(w8a8::launch_gemm_nk(g, nullptr, 0, stream), "w8a8_gemm");
     }
 
+    if(workspace && reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+        return fail(W8A8_ERROR_INVALID_VALUE, "w8a8_gemm: workspace must be 16-byte aligned");
     if(!w8a8::gemm_fast_path_ok(g))
         return hip_status(w8a8::launch_gemm_generic(g, lda, 1, ldb, 1, stream),
                           "w8a8_gemm(generic)");
-    return hip_status(w8a8::launch_gemm_nk(g, stream), "w8a8_gemm");
+    return hip_status(w8a8::launch_gemm_nk(g, workspace, workspace ? workspace_bytes : 0, stream),
+                      "w8a8_gemm");
 }
 
 int w8a8_fused_sq_gemm(const void* x, const float* smooth_scale, const int8_t* w,
                        const float* scale_w, void* c, uint32_t m, uint32_t n, uint32_t k,
                        uint32_t ldx, uint32_t ldw, uint32_t ldc, int8_t* q, float* row_scale,
-                       hipStream_t stream)
+                       void* workspace, size_t ws_bytes, hipStream_t stream)
 {
     if(!x || !smooth_scale || !w || !scale_w || !c || !q || !row_scale)
         return fail(W8A8_ERROR_INVALID_VALUE, "w8a8_fused_sq_gemm: null pointer argument");
@@ -310,7 +319,7 @@ int w8a8_fused_sq_gemm(const void* x, const float* smooth_scale, const int8_t* w
     int rc = w8a8_smoothquant(x, smooth_scale, q, row_scale, m, k, 127.f, ldx, k, stream);
     if(rc != W8A8_SUCCESS) return rc;
     return w8a8_gemm(m, n, k, q, w, c, k, ldw, ldc, row_scale, scale_w, 1.f, 1.f, W8A8_OUT_F16,
-                     W8A8_LAYOUT_A_ROW_B_NK, nullptr, 0, stream);
+                     W8A8_LAYOUT_A_ROW_B_NK, workspace, ws_bytes, stream);
 }
 
 size_t w8a8_pack_weights_size(uint32_t n, uint32_t k)

@@ -153,6 +153,36 @@ TileCfg pick_tile_cfg(uint32_t m, uint32_t n)
     return TileCfg::kSmall;
 }
 
+// K split of a dense launch (one panel): when the chosen tiles fill at most
+// half of the CUs, each tile runs as `parts` K pieces on otherwise idle CUs
+// (gemm_i8_split_kernel + fixup).  parts = 1: no split.
+struct DenseSplit {
+    TileCfg  cfg;
+    uint32_t tiles, parts;
+    size_t   bytes; // workspace the split needs
+};
+
+DenseSplit dense_split(uint32_t m, uint32_t n, uint32_t k)
+{
+    DenseSplit d{pick_tile_cfg(m, n), 0, 1, 0};
+    uint32_t   bm = GemmMain::kBM, bn = GemmMain::kBN;
+    size_t     part_bytes = gemm::Partial<GemmMain>::kBytes;
+    if(d.cfg == TileCfg::kMidM) {
+        bm = GemmMidM::kBM, bn = GemmMidM::kBN, part_bytes = gemm::Partial<GemmMidM>::kBytes;
+    } else if(d.cfg == TileCfg::kSmall) {
+        bm = GemmSmall::kBM, bn = GemmSmall::kBN, part_bytes = gemm::Partial<GemmSmall>::kBytes;
+    }
+    d.tiles             = ((m + bm - 1) / bm) * ((n + bn - 1) / bn);
+    const uint32_t cus  = device_cus();
+    const uint32_t nk   = (k + 127) / 128;
+    if((uint64_t)d.tiles * 2 > cus) return d;
+    const uint32_t parts = std::min({cus / d.tiles, nk / gemm::kMinKtPerPart, gemm::kMaxParts});
+    if(parts < 2) return d;
+    d.parts = parts;
+    d.bytes = (size_t)d.tiles * parts * part_bytes;
+    return d;
+}
+
 // K splits of the wide decode kernel for one weight panel: the count that
 // minimises the weight bytes of the busiest CU, ceil(blocks / CUs) / splits
 // (the fewest splits among equals), at least 8 k-tiles per split; 1 = no
@@ -291,7 +321,13 @@ bool gemm_packed_ok(const GemmArgs& g)
     return g.m <= kDecodeMaxM ? gemm_decode_ok(g) : (uint64_t)g.lda * GemmPacked::kBM <= kLimit;
 }
 
-hipError_t launch_gemm_nk(const GemmArgs& g, hipStream_t stream)
+size_t gemm_nk_workspace_bytes(const GemmArgs& g)
+{
+    if(g.m == 0 || g.n == 0 || g.k == 0 || gemm_decode_ok(g)) return 0;
+    return dense_split(g.m, g.n, g.k).bytes;
+}
+
+hipError_t launch_gemm_nk(const GemmArgs& g, void* ws, size_t ws_bytes, hipStream_t stream)
 {
     if(g.m == 0 || g.n == 0) return hipSuccess;
     if(gemm_decode_ok(g)) return launch_gemm_decode(g, false, nullptr, 0, stream);
@@ -305,6 +341,21 @@ hipError_t launch_gemm_nk(const GemmArgs& g, hipStream_t stream)
         g.m, std::max<size_t>(GemmMain::kBM, kLimit / g.lda / GemmMain::kBM * GemmMain::kBM));
     const uint32_t nstep = (uint32_t)std::min<size_t>(
         g.n, std::max<size_t>(GemmMain::kBN, kLimit / g.ldb / GemmMain::kBN * GemmMain::kBN));
+    if(ws != nullptr && mstep == g.m && nstep == g.n) {
+        const DenseSplit d = dense_split(g.m, g.n, g.k);
+        if(d.parts > 1 && ws_bytes >= d.bytes) {
+            const KArgs p  = make_kargs(g);
+            int32_t*    pw = static_cast<int32_t*>(ws);
+            switch(d.cfg) {
+            case TileCfg::kMain:
+                return gemm::launch_cfg_split<GemmMain>(p, g.out_type, vec_ok, pw, d.parts, stream);
+            case TileCfg::kMidM:
+                return gemm::launch_cfg_split<GemmMidM>(p, g.out_type, vec_ok, pw, d.parts, stream);
+            default:
+                return gemm::launch_cfg_split<GemmSmall>(p, g.out_type, vec_ok, pw, d.parts, stream);
+            }
+        }
+    }
     for(uint32_t m0 = 0; m0 < g.m; m0 += mstep) {
         for(uint32_t n0 = 0; n0 < g.n; n0 += nstep) {
             KArgs p = make_kargs(g);

@@ -117,9 +117,6 @@ struct MoeArgs {
 // (L * parts <= cus) whose int32 partials go to the workspace; the fixup
 // kernel sums them (exact) and runs the usual epilogue.  Tiles [0, base) run
 // whole, as without a split.
-constexpr uint32_t kMaxParts     = 8;
-constexpr uint32_t kMinKtPerPart = 16; // shorter pieces do not repay the partial traffic
-
 struct TailSplit {
     uint32_t base, left, parts;
 };

@@ -322,6 +322,11 @@ struct Partial {
     static_assert(C::kWaves % kFixupWaves == 0, "whole fixup blocks");
 };
 
+// K pieces of a split tile: at most kMaxParts, each at least kMinKtPerPart
+// k-tiles (shorter pieces do not repay the partial traffic).
+constexpr uint32_t kMaxParts     = 8;
+constexpr uint32_t kMinKtPerPart = 16;
+
 template <class C>
 __device__ __forceinline__ void store_partial(int32_t* part,
                                               const v16i (&acc)[C::kTilesM][C::kTilesN])
@@ -346,7 +351,7 @@ template <class C>
 __device__ __forceinline__ void add_partial(const int32_t* part, uint32_t tid,
                                             v16i (&acc)[C::kTilesM][C::kTilesN])
 {
-    constexpr int kBatch = 16;
+    constexpr int kBatch = Partial<C>::kBlocks < 16 ? Partial<C>::kBlocks : 16;
     static_assert(Partial<C>::kBlocks % kBatch == 0, "whole batches");
 #pragma unroll
     for(int b = 0; b < Partial<C>::kBlocks; b += kBatch) {
@@ -597,8 +602,50 @@ __global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_tile_kernel(KArgs p, i
     gemm_tile<C, OUT>(p, tm * C::kBM, tn * C::kBN, vec_ok, lds);
 }
 
-// Launch one configuration; the caller has validated the fast-path
-// preconditions (16-byte aligned a/b, lda/ldb/k multiples of 16).
+// K split of a launch whose tiles fill at most half of the CUs: block b runs
+// piece b % parts of tile b / parts (k-tiles [part * nk / parts,
+// (part + 1) * nk / parts)) and stores its int32 accumulators to
+// ws + b * Partial<C>::kInts; gemm_i8_split_fixup_kernel then sums each
+// tile's pieces in order (exact) and runs the tile epilogue, in kPieces
+// blocks of kFixupWaves waves per tile.
+template <class C, int OUT>
+__global__ void __launch_bounds__(C::kThreads, 1)
+    gemm_i8_split_kernel(KArgs p, int vec_ok, int32_t* ws, uint32_t parts)
+{
+    extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
+    const uint32_t tiles_m = (p.m + C::kBM - 1) / C::kBM;
+    const uint32_t tiles_n = (p.n + C::kBN - 1) / C::kBN;
+    const uint32_t slot = blockIdx.x / parts, part = blockIdx.x % parts;
+    uint32_t       tm, tn;
+    tile_coords<C::kGroupM>(slot, tiles_m, tiles_n, tm, tn);
+    const uint32_t nk  = (p.k + C::kBK - 1) / C::kBK;
+    const uint32_t kt0 = part * nk / parts, kt1 = (part + 1) * nk / parts;
+    gemm_tile<C, OUT, true>(p, tm * C::kBM, tn * C::kBN, vec_ok, lds, kt0, kt1 - kt0,
+                            ws + (size_t)blockIdx.x * Partial<C>::kInts);
+}
+
+template <class C, int OUT>
+__global__ void __launch_bounds__(Partial<C>::kFixupWaves * kWave, 1)
+    gemm_i8_split_fixup_kernel(KArgs p, int vec_ok, const int32_t* ws, uint32_t parts)
+{
+    extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
+    const uint32_t tiles_m   = (p.m + C::kBM - 1) / C::kBM;
+    const uint32_t tiles_n   = (p.n + C::kBN - 1) / C::kBN;
+    const uint32_t slot      = blockIdx.x / Partial<C>::kPieces;
+    const int      wave_base = (int)(blockIdx.x % Partial<C>::kPieces) * Partial<C>::kFixupWaves;
+    uint32_t       tm, tn;
+    tile_coords<C::kGroupM>(slot, tiles_m, tiles_n, tm, tn);
+    v16i acc[C::kTilesM][C::kTilesN];
+#pragma unroll
+    for(int i = 0; i < C::kTilesM; ++i)
+#pragma unroll
+        for(int j = 0; j < C::kTilesN; ++j) acc[i][j] = v16i{0};
+    const uint32_t tid = wave_base * kWave + threadIdx.x;
+    for(uint32_t part = 0; part < parts; ++part)
+        add_partial<C>(ws + (size_t)(slot * parts + part) * Partial<C>::kInts, tid, acc);
+    tile_epilogue<C, OUT>(p, tm * C::kBM, tn * C::kBN, vec_ok, lds, acc, wave_base);
+}
+
 template <class C, int OUT>
 void raise_lds_limit_once()
 {
@@ -607,6 +654,17 @@ void raise_lds_limit_once()
     static std::once_flag once;
     std::call_once(once, [] {
         (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_i8_tile_kernel<C, OUT>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
+        (void)hipGetLastError();
+    });
+}
+
+template <class C, int OUT>
+void raise_split_lds_once()
+{
+    static std::once_flag once;
+    std::call_once(once, [] {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_i8_split_kernel<C, OUT>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
         (void)hipGetLastError();
     });
@@ -626,6 +684,30 @@ hipError_t launch_cfg(const KArgs& p, int out_type, int vec_ok, hipStream_t stre
         raise_lds_limit_once<C, W8A8_OUT_F16>();
         hipLaunchKernelGGL((gemm_i8_tile_kernel<C, W8A8_OUT_F16>), dim3(tiles), dim3(C::kThreads),
                            C::kLdsBytes, stream, p, vec_ok);
+    }
+    return hipGetLastError();
+}
+
+// Split launch (see gemm_i8_split_kernel): ws holds tiles * parts partials.
+template <class C>
+hipError_t launch_cfg_split(const KArgs& p, int out_type, int vec_ok, int32_t* ws,
+                            uint32_t parts, hipStream_t stream)
+{
+    const uint32_t tiles  = ((p.m + C::kBM - 1) / C::kBM) * ((p.n + C::kBN - 1) / C::kBN);
+    const dim3     grid(tiles * parts), fgrid(tiles * Partial<C>::kPieces);
+    const dim3     fblock(Partial<C>::kFixupWaves * kWave);
+    if(out_type == W8A8_OUT_I32) {
+        raise_split_lds_once<C, W8A8_OUT_I32>();
+        hipLaunchKernelGGL((gemm_i8_split_kernel<C, W8A8_OUT_I32>), grid, dim3(C::kThreads),
+                           C::kLdsBytes, stream, p, vec_ok, ws, parts);
+        hipLaunchKernelGGL((gemm_i8_split_fixup_kernel<C, W8A8_OUT_I32>), fgrid, fblock,
+                           Partial<C>::kFixupLds, stream, p, vec_ok, ws, parts);
+    } else {
+        raise_split_lds_once<C, W8A8_OUT_F16>();
+        hipLaunchKernelGGL((gemm_i8_split_kernel<C, W8A8_OUT_F16>), grid, dim3(C::kThreads),
+                           C::kLdsBytes, stream, p, vec_ok, ws, parts);
+        hipLaunchKernelGGL((gemm_i8_split_fixup_kernel<C, W8A8_OUT_F16>), fgrid, fblock,
+                           Partial<C>::kFixupLds, stream, p, vec_ok, ws, parts);
     }
     return hipGetLastError();
 }

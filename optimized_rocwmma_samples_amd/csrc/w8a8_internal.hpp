@@ -64,7 +64,10 @@ struct GemmArgs {
 // k % 16 == 0.
 // Small m (decode) is routed to the decode kernel inside launch_gemm_nk.
 bool       gemm_fast_path_ok(const GemmArgs& g);
-hipError_t launch_gemm_nk(const GemmArgs& g, hipStream_t stream);
+// ws (optional): int32 partials of a K split, used when the launch's tiles
+// fill at most half the CUs and ws_bytes >= gemm_nk_workspace_bytes(g).
+hipError_t launch_gemm_nk(const GemmArgs& g, void* ws, size_t ws_bytes, hipStream_t stream);
+size_t     gemm_nk_workspace_bytes(const GemmArgs& g);
 
 // Decode kernel (m <= kDecodeMaxM): weights streamed once, split-K across the
 // waves of a block.  `packed`: g.b holds packed weights (g.ldb unused).

@@ -110,17 +110,24 @@ def test_gemm_validation(w8a8, kw, needle):
 
 
 def test_gemm_workspace_size(w8a8):
-    assert W.gemm_workspace_size(100, 200, 300) == 0
     ws = W.gemm_workspace_size(100, 200, 300, W.LAYOUT_A_COL_B_KN)
     assert ws >= (100 + 200) * 304 and ws % 256 == 0
+    # primary layout: K-split partials (64 KiB per 128 x 128 tile piece) only
+    # when the tiles fill at most half of the 256 CUs and K allows 2 pieces
+    # of 16 k-tiles
+    assert W.gemm_workspace_size(100, 200, 300) == 0          # K too short
+    assert W.gemm_workspace_size(512, 4096, 4096) == 128 * 2 * 65536
+    assert W.gemm_workspace_size(512, 512, 16384) == 16 * 8 * 65536
+    assert W.gemm_workspace_size(8192, 4096, 4096) == 0       # fills the chip
+    assert W.gemm_workspace_size(64, 4096, 16384) == 0        # decode kernel
 
 
 def test_fused_validation(w8a8):
     rc, msg = _status("w8a8_fused_sq_gemm", FAKE, FAKE, FAKE, None, FAKE, 4, 4, 4, 0, 0, 0, FAKE,
-                      FAKE, None)
+                      FAKE, None, 0, None)
     assert rc == W.ERROR_INVALID_VALUE
     rc, msg = _status("w8a8_fused_sq_gemm", FAKE, FAKE, FAKE, FAKE, FAKE, 4, 4, 8, 4, 0, 0, FAKE,
-                      FAKE, None)
+                      FAKE, None, 0, None)
     assert rc == W.ERROR_INVALID_VALUE and "ldx" in msg
 
 

@@ -67,6 +67,34 @@ def test_tile_configs_exact(w8a8, gpu, m, n, k):
     assert_f16_bitexact(host(c), O.dequant_f16(acc, sa, sb))
 
 
+# K split (workspace given) of launches whose 128 x 128 tiles fill at most
+# half of the 256 CUs: tiles x pieces
+SPLIT_SHAPES = [
+    (512, 4096, 4096),   # 128 tiles x 2
+    (512, 512, 16384),   # 16 tiles x 8
+    (1000, 1500, 4112),  # 96 tiles x 2, ragged edges, the K tail in the last piece
+    (300, 600, 8192),    # 15 tiles x 4, ragged edges
+]
+
+
+@pytest.mark.parametrize("m,n,k", SPLIT_SHAPES)
+def test_k_split_exact(w8a8, gpu, m, n, k):
+    import torch
+    assert w8a8.gemm_workspace_size(m, n, k) > 0
+    a, b, sa, sb = inputs(m, n, k, 2 * m + n + k)
+    ad, bd, sad, sbd = dev(a, gpu), dev(b, gpu), dev(sa, gpu), dev(sb, gpu)
+    none = torch.empty(0, dtype=torch.uint8, device=gpu)
+    ci = host(w8a8.gemm(ad, bd, out_dtype=torch.int32))           # split (workspace allocated)
+    cf = host(w8a8.gemm(ad, bd, sad, sbd))
+    assert_i32_equal(ci, host(w8a8.gemm(ad, bd, out_dtype=torch.int32, workspace=none)))
+    assert_f16_bitexact(cf, host(w8a8.gemm(ad, bd, sad, sbd, workspace=none)))
+    rows = np.unique(np.concatenate([np.arange(16), np.arange(m - 16, m),
+                                     np.random.default_rng(m).integers(0, m, 64)]))
+    acc = O.gemm_i32(a[rows], b)
+    assert_i32_equal(ci[rows], acc)
+    assert_f16_bitexact(cf[rows], O.dequant_f16(acc, sa[rows], sb))
+
+
 def test_f16_dequant_mode1_tensor_scales(w8a8, gpu):
     m, n, k = 256, 512, 256
     a, b, _, _ = inputs(m, n, k, 5)
