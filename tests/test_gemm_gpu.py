@@ -95,6 +95,26 @@ def test_k_split_exact(w8a8, gpu, m, n, k):
     assert_f16_bitexact(cf[rows], O.dequant_f16(acc, sa[rows], sb))
 
 
+def test_k_split_strided(w8a8, gpu):
+    # split path with row strides on A, B and C (16 tiles x 2 pieces)
+    import torch
+    m, n, k = 256, 1024, 4096
+    a, b, sa, sb = inputs(m, n, k + 32, 77)
+    ad = dev(a, gpu)[:, :k]
+    bd = dev(b, gpu)[:, :k]
+    acc = O.gemm_i32(a[:, :k], b[:, :k])
+    for dt in (torch.int32, torch.float16):
+        big = torch.full((m, n + 8), -3, dtype=dt, device=gpu)
+        w8a8.gemm(ad, bd, dev(sa, gpu) if dt == torch.float16 else None,
+                  dev(sb, gpu) if dt == torch.float16 else None, out=big[:, :n])
+        got = host(big)
+        if dt == torch.int32:
+            assert_i32_equal(got[:, :n], acc)
+        else:
+            assert_f16_bitexact(np.ascontiguousarray(got[:, :n]), O.dequant_f16(acc, sa, sb))
+        assert (got[:, n:] == -3).all()
+
+
 def test_f16_dequant_mode1_tensor_scales(w8a8, gpu):
     m, n, k = 256, 512, 256
     a, b, _, _ = inputs(m, n, k, 5)
