@@ -28,8 +28,12 @@ using GemmMain  = gemm::Cfg<256, 256, 128, 2, 2, 4, 4>;
 // 128 x 256: o_proj 47 -> 40 µs, down 146 -> 116 µs).
 using GemmMidM  = gemm::Cfg<128, 256, 128, 3, 2, 4, 4>; // 8 waves of 64 x 64, 144 KiB LDS
 using GemmSmall = gemm::Cfg<128, 128, 128, 3, 2, 4, 4>; // 8 waves of 64 x 32, 96 KiB LDS
-// Packed-weight tile configuration (m > kDecodeMaxM).
-using GemmPacked = gemm::PbCfg<256, 4, 2, 4>;
+// Packed-weight tile configurations (m > kDecodeMaxM): 256 x 256 blocks, and
+// 128 / 64-row blocks for launches that would leave most CUs idle with them
+// (pick_packed_cfg).
+using GemmPacked    = gemm::PbCfg<256, 4, 2, 4>;
+using GemmPacked128 = gemm::PbCfg<128, 4, 2, 4>;
+using GemmPacked64  = gemm::PbCfg<64, 4, 2, 4>;
 // Decode configurations: <32-row m tiles, 32-row weight tiles, waves, ring>.
 using DecSmall   = gemm::DecCfg<1, 1, 4, 3>; // m <= 32, or <= 16 packed
 using DecSmallW  = gemm::DecCfg<1, 2, 8, 3>; // packed, 16 < m <= 32, many slabs
@@ -155,6 +159,18 @@ TileCfg pick_tile_cfg(uint32_t m, uint32_t n)
     if(tiles(GemmMain::kBM, GemmMain::kBN) >= enough) return TileCfg::kMain;
     if(tiles(GemmMidM::kBM, GemmMidM::kBN) >= enough) return TileCfg::kMidM;
     return TileCfg::kSmall;
+}
+
+// Block height of a packed-weight launch (blocks are always 256 weight
+// columns): the tallest of 256 / 128 / 64 rows that gives at least 3/4 of a
+// round of blocks, else 64.
+int pick_packed_cfg(uint32_t m, uint32_t n)
+{
+    const uint64_t cols   = (n + GemmPacked::kBN - 1) / GemmPacked::kBN;
+    const uint64_t enough = (uint64_t)device_cus() * 3 / 4;
+    if((m + 255) / 256 * cols >= enough) return 256;
+    if((m + 127) / 128 * cols >= enough) return 128;
+    return 64;
 }
 
 // K split of a dense launch (one panel): when the chosen tiles fill at most
@@ -290,7 +306,12 @@ hipError_t launch_gemm_packed(const GemmArgs& g, void* ws, size_t ws_bytes, hipS
             p.a     = g.a + (size_t)m0 * g.lda;
             p.c     = static_cast<int8_t*>(p.c) + (size_t)m0 * g.ldc * esz;
             p.sa    = g.scale_a ? g.scale_a + m0 : nullptr;
-            hipError_t e = gemm::launch_pb<GemmPacked>(p, g.out_type, vec_ok, stream);
+            hipError_t e;
+            switch(pick_packed_cfg(p.m, p.n)) {
+            case 256: e = gemm::launch_pb<GemmPacked>(p, g.out_type, vec_ok, stream); break;
+            case 128: e = gemm::launch_pb<GemmPacked128>(p, g.out_type, vec_ok, stream); break;
+            default: e = gemm::launch_pb<GemmPacked64>(p, g.out_type, vec_ok, stream); break;
+            }
             if(e != hipSuccess) return e;
         }
     }

@@ -87,6 +87,21 @@ def test_packed_int32_exact(w8a8, gpu, m, n, k):
     assert_i32_equal(host(c), O.gemm_i32(a, b))
 
 
+# Packed weights above the decode sizes: the block height follows the block
+# count (256 CUs): 12 x 16 = 192 blocks of 256 rows; 6 x 16 of 256 rows ->
+# 192 of 128 rows; few blocks -> 64 rows.  Ragged M and N edges.
+@pytest.mark.parametrize("m,n,k", [(3072, 4096, 256), (1500, 4000, 272), (700, 1100, 400)])
+def test_packed_block_heights_exact(w8a8, gpu, m, n, k):
+    import torch
+    a, b, sa, sb = inputs(m, n, k, 3000 + m + n + k)
+    ad = dev(a, gpu)
+    pw = w8a8.pack_weights(dev(b, gpu))
+    acc = O.gemm_i32(a, b)
+    assert_i32_equal(host(w8a8.gemm_packed(ad, pw, out_dtype=torch.int32)), acc)
+    c = w8a8.gemm_packed(ad, pw, dev(sa, gpu), dev(sb, gpu))
+    assert_f16_bitexact(host(c), O.dequant_f16(acc, sa, sb))
+
+
 @pytest.mark.parametrize("packed", [False, True])
 @pytest.mark.parametrize("m", [1, 24, 64])
 def test_decode_f16_modes(w8a8, gpu, packed, m):
