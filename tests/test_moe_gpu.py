@@ -173,13 +173,23 @@ def _tail_split_parts(total, cus, nk):
     return (left, parts) if parts >= 2 else (0, 1)
 
 
-# (expert row counts, K, N) on 256 CUs: 18 tile rows x 16 = 288 tiles leave
-# 32 tail tiles (expert 2, whose second tile row holds 44 rows) cut in 2;
-# 3 tile rows x 2 = 6 tiles (fewer than the CUs) each cut in 8; one expert
-# of 17 tile rows (16 tail tiles cut in 2); an empty expert between two
-# others (96 tiles, all cut in 2)
+# (expert row counts, K, N) on 256 CUs (tile rows of 256 or 128, _tile_rows):
+# 18 tile rows x 16 = 288 tiles leave 32 tail tiles (expert 2, whose second
+# tile row holds 44 rows) cut in 2; 5 tile rows of 128 x 2 = 10 tiles (fewer
+# than the CUs) each cut in 8; one expert of 17 tile rows (16 tail tiles cut
+# in 2); an empty expert between two others (4 tile rows x 16 = 64 tiles,
+# all cut in 2)
 SPLIT_CASES = [([1000, 3000, 300], 4096, 4096), ([200, 300], 16384, 512),
-               ([4352], 4096, 4096), ([700, 0, 520], 4096, 4096)]
+               ([4352], 4096, 4096), ([300, 0, 260], 4096, 4096)]
+
+
+def _tile_rows(counts, rows):
+    # 128-row tiles when u128 * 0.8 > u256 for the average padded rows per
+    # expert (the library's choice), else 256
+    avg = rows / len(counts)
+    u = {bm: avg / (np.ceil(avg / bm) * bm) for bm in (128, 256)}
+    bm = 128 if u[128] * 0.8 > u[256] else 256
+    return sum(-(-c // bm) for c in counts), bm
 
 
 @pytest.mark.parametrize("counts,k,n", SPLIT_CASES)
@@ -196,7 +206,7 @@ def test_moe_gemm_tail_split_exact(w8a8, gpu, counts, k, n):
     sa = G.uniform(seed, G.TID_SA, (rows,), 1e-3, 1e-2)
     sw = G.uniform(seed, G.TID_SB, (e, n), 1e-3, 1e-2)
     cus = torch.cuda.get_device_properties(gpu).multi_processor_count
-    total = sum(-(-c // 256) for c in counts) * (-(-n // 256))
+    total = _tile_rows(counts, rows)[0] * (-(-n // 256))
     left, parts = _tail_split_parts(total, cus, -(-k // 128))
     assert left > 0 and parts >= 2, (total, cus, "shape does not exercise the tail split")
     args = (dev(a, gpu), dev(w, gpu), dev(start, gpu), dev(count, gpu))
