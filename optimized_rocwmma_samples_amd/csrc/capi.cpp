@@ -422,8 +422,8 @@ int w8a8_grouped_gemm(const w8a8_group_desc* groups, uint32_t num_groups, int ou
                     workspace_bytes, w8a8_grouped_gemm_workspace_size(num_groups));
     if(reinterpret_cast<uintptr_t>(workspace) % 64 != 0)
         return fail(W8A8_ERROR_INVALID_VALUE, "%s: workspace must be 64-byte aligned", fn);
-    uint64_t   tiles  = 0;
-    int        vec_ok = 1;
+    uint64_t   tiles[3] = {0, 0, 0}; // per tile configuration
+    int        vec_ok   = 1;
     const size_t esz  = out_type == W8A8_OUT_I32 ? 4 : 2;
     for(uint32_t i = 0; i < num_groups; ++i) {
         const w8a8_group_desc& d = groups[i];
@@ -444,15 +444,16 @@ int w8a8_grouped_gemm(const w8a8_group_desc* groups, uint32_t num_groups, int ou
             return fail(W8A8_ERROR_NOT_SUPPORTED, "%s: group %u: operand over 2 GiB", fn, i);
         vec_ok = vec_ok && reinterpret_cast<uintptr_t>(d.c) % (4 * esz) == 0 && d.ldc % 4 == 0
                  && (d.scale_b == nullptr || reinterpret_cast<uintptr_t>(d.scale_b) % 16 == 0);
-        tiles += w8a8::grouped_gemm_tiles(d.m, d.n);
+        for(int c = 0; c < 3; ++c) tiles[c] += w8a8::grouped_gemm_tiles(d.m, d.n, c);
     }
-    if(tiles > 0x7FFFFFFFull) return fail(W8A8_ERROR_NOT_SUPPORTED, "%s: too many tiles", fn);
-    if(tiles == 0) return hip_status(hipSuccess, fn);
+    if(tiles[2] > 0x7FFFFFFFull) return fail(W8A8_ERROR_NOT_SUPPORTED, "%s: too many tiles", fn);
+    if(tiles[0] == 0) return hip_status(hipSuccess, fn);
+    const int cfg = w8a8::grouped_gemm_cfg(tiles);
     hipError_t e = hipMemcpyAsync(workspace, groups, (size_t)num_groups * sizeof(w8a8_group_desc),
                                   hipMemcpyHostToDevice, stream);
     if(e == hipSuccess)
         e = w8a8::launch_grouped_gemm(static_cast<const w8a8_group_desc*>(workspace), num_groups,
-                                      (uint32_t)tiles, out_type, vec_ok, stream);
+                                      (uint32_t)tiles[cfg], cfg, out_type, vec_ok, stream);
     return hip_status(e, fn);
 }
 

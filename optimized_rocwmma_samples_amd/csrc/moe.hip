@@ -574,18 +574,7 @@ hipError_t launch_moe_combine(const uint16_t* y, uint32_t ldy, uint32_t rows_y, 
     return hipGetLastError();
 }
 
-hipError_t launch_grouped_gemm(const w8a8_group_desc* groups_dev, uint32_t ngroups,
-                               uint32_t total_tiles, int out_type, int vec_ok, hipStream_t stream)
-{
-    return gemm::launch_grouped<GemmGrouped>(reinterpret_cast<const gemm::KArgs*>(groups_dev),
-                                             ngroups, total_tiles, out_type, vec_ok, stream);
-}
-
-uint32_t grouped_gemm_tiles(uint32_t m, uint32_t n)
-{
-    return ((m + GemmGrouped::kBM - 1) / GemmGrouped::kBM)
-           * ((n + GemmGrouped::kBN - 1) / GemmGrouped::kBN);
-}
+using GemmGroupedSmall = gemm::Cfg<128, 128, 128, 3, 2, 4, 4>;
 
 namespace {
 uint32_t device_cus()
@@ -599,6 +588,35 @@ uint32_t device_cus()
     return cus;
 }
 } // namespace
+
+hipError_t launch_grouped_gemm(const w8a8_group_desc* groups_dev, uint32_t ngroups,
+                               uint32_t total_tiles, int cfg, int out_type, int vec_ok,
+                               hipStream_t stream)
+{
+    const auto* g = reinterpret_cast<const gemm::KArgs*>(groups_dev);
+    if(cfg == 1)
+        return gemm::launch_grouped<GemmGroupedMid>(g, ngroups, total_tiles, out_type, vec_ok,
+                                                    stream);
+    if(cfg == 2)
+        return gemm::launch_grouped<GemmGroupedSmall>(g, ngroups, total_tiles, out_type, vec_ok,
+                                                      stream);
+    return gemm::launch_grouped<GemmGrouped>(g, ngroups, total_tiles, out_type, vec_ok, stream);
+}
+
+uint32_t grouped_gemm_tiles(uint32_t m, uint32_t n, int cfg)
+{
+    const uint32_t bm = cfg == 0 ? 256 : 128, bn = cfg == 2 ? 128 : 256;
+    return ((m + bm - 1) / bm) * ((n + bn - 1) / bn);
+}
+
+int grouped_gemm_cfg(const uint64_t tiles[3])
+{
+    const uint64_t enough = (uint64_t)device_cus() * 3 / 4;
+    if(tiles[0] >= enough) return 0;
+    if(tiles[1] >= enough) return 1;
+    return 2;
+}
+
 
 size_t moe_gemm_workspace_bytes()
 {

@@ -135,9 +135,14 @@ hipError_t launch_moe_combine(const uint16_t* y, uint32_t ldy, uint32_t rows_y, 
 
 // Grouped GEMM over device descriptors (validated by the caller: fast-path
 // alignment, every operand under 2 GiB).
-uint32_t   grouped_gemm_tiles(uint32_t m, uint32_t n);
+// Grouped GEMM tile configurations: 0 = 256 x 256, 1 = 128 x 256, 2 = 128 x 128.
+uint32_t   grouped_gemm_tiles(uint32_t m, uint32_t n, int cfg);
+// The tallest configuration whose tile total is at least 3/4 of a round of
+// the CUs (tiles[c] = total tiles of configuration c), else 128 x 128.
+int        grouped_gemm_cfg(const uint64_t tiles[3]);
 hipError_t launch_grouped_gemm(const w8a8_group_desc* groups_dev, uint32_t ngroups,
-                               uint32_t total_tiles, int out_type, int vec_ok, hipStream_t stream);
+                               uint32_t total_tiles, int cfg, int out_type, int vec_ok,
+                               hipStream_t stream);
 
 struct MoeGemmArgs {
     const int8_t*  a;

@@ -114,6 +114,28 @@ def test_moe_sort_vs_reference_kernels(w8a8, gpu):
 
 
 # -------------------------------------------------------------------- GEMMs
+# The grouped launch picks one tile for all groups by the total tile count
+# (256 CUs): 207 tiles of 256 x 256; 111 of 256 x 256 -> 222 of 128 x 256.
+@pytest.mark.parametrize("shapes", [[(2048, 4096, 256), (2048, 2048, 128), (700, 1100, 64)],
+                                    [(1500, 4096, 256), (700, 1100, 128)]])
+def test_grouped_gemm_tile_configs(w8a8, gpu, shapes):
+    import torch
+    probs, host_in = [], []
+    for i, (m, n, k) in enumerate(shapes):
+        a = G.int8(90 + i, G.TID_A, (m, k))
+        b = G.int8(90 + i, G.TID_B, (n, k))
+        sa = G.uniform(90 + i, G.TID_SA, (m,), 1e-3, 1e-2)
+        sb = G.uniform(90 + i, G.TID_SB, (n,), 1e-3, 1e-2)
+        probs.append((dev(a, gpu), dev(b, gpu), dev(sa, gpu), dev(sb, gpu)))
+        host_in.append((a, b, sa, sb))
+    outs_i = w8a8.grouped_gemm([(a, b, None, None) for a, b, _, _ in probs], out_dtype=torch.int32)
+    outs_f = w8a8.grouped_gemm(probs)
+    for (a, b, sa, sb), oi, of in zip(host_in, outs_i, outs_f):
+        acc = O.gemm_i32(a, b)
+        assert_i32_equal(host(oi), acc)
+        assert_f16_bitexact(host(of), O.dequant_f16(acc, sa, sb))
+
+
 def test_grouped_gemm_int32_and_f16(w8a8, gpu):
     import torch
     shapes = [(256, 512, 256), (0, 64, 64), (300, 200, 80), (1, 4096, 1024), (512, 256, 4112)]
