@@ -73,19 +73,56 @@ __global__ void __launch_bounds__(256) gemm_i8_generic_kernel(KArgs p, size_t sa
 
 __global__ void __launch_bounds__(256) transpose_i8_kernel(const int8_t* src, uint32_t lds_src,
                                                            int8_t* dst, uint32_t ldd,
-                                                           uint32_t rows, uint32_t cols)
+                                                           uint32_t rows, uint32_t cols, int vec)
 {
-    // dst[r, c] = src[c * lds_src + r]; tile 64x64 through LDS
-    __shared__ int8_t tile[64][65];
+    // dst[r, c] = src[c * lds_src + r] (0 for c >= cols: the K padding), one
+    // 64 x 64 tile per block through LDS.  Each thread moves 16 bytes each
+    // way: a 16-byte run of one source row in, a 16-byte run of one
+    // destination row out (vec: src and lds_src 16-byte aligned; dst and ldd
+    // are, by construction).  Rows of the LDS tile are padded to 68 bytes.
+    constexpr int kPitch = 68;
+    __shared__ __attribute__((aligned(16))) int8_t tile[64 * kPitch];
     const uint32_t r0 = blockIdx.x * 64, c0 = blockIdx.y * 64;
-    for(int i = threadIdx.x; i < 64 * 64; i += 256) {
-        const uint32_t cc = c0 + i / 64, rr = r0 + i % 64;
-        tile[i / 64][i % 64] = (cc < cols && rr < rows) ? src[(size_t)cc * lds_src + rr] : 0;
+    const int      t  = threadIdx.x;
+    {
+        const int      cl = t / 4, rc = (t % 4) * 16; // source row c0 + cl, bytes r0 + rc ..
+        const uint32_t cc = c0 + cl, rr = r0 + rc;
+        int4           v  = make_int4(0, 0, 0, 0);
+        if(cc < cols) {
+            const int8_t* p = src + (size_t)cc * lds_src + rr;
+            if(vec && rr + 16 <= rows) {
+                v = *reinterpret_cast<const int4*>(p);
+            } else {
+                int8_t b[16];
+                for(int e = 0; e < 16; ++e) b[e] = rr + e < rows ? p[e] : 0;
+                v = *reinterpret_cast<const int4*>(b);
+            }
+        }
+        int* row = reinterpret_cast<int*>(tile + cl * kPitch + rc);
+        row[0] = v.x;
+        row[1] = v.y;
+        row[2] = v.z;
+        row[3] = v.w;
     }
     __syncthreads();
-    for(int i = threadIdx.x; i < 64 * 64; i += 256) {
-        const uint32_t rr = r0 + i / 64, cc = c0 + i % 64;
-        if(rr < rows && cc < ldd) dst[(size_t)rr * ldd + cc] = tile[i % 64][i / 64];
+    const int      rl = t / 4, cc0 = (t % 4) * 16; // destination row r0 + rl, columns c0 + cc0 ..
+    const uint32_t rr = r0 + rl;
+    if(rr >= rows) return;
+    uint32_t w[4];
+#pragma unroll
+    for(int q = 0; q < 4; ++q) {
+        uint32_t x = 0;
+#pragma unroll
+        for(int e = 0; e < 4; ++e)
+            x |= (uint32_t)(uint8_t)tile[(cc0 + q * 4 + e) * kPitch + rl] << (8 * e);
+        w[q] = x;
+    }
+    const uint32_t cbase = c0 + cc0;
+    int8_t*        d     = dst + (size_t)rr * ldd + cbase;
+    if(cbase + 16 <= ldd) {
+        *reinterpret_cast<int4*>(d) = make_int4((int)w[0], (int)w[1], (int)w[2], (int)w[3]);
+    } else {
+        for(int e = 0; cbase + e < ldd; ++e) d[e] = (int8_t)(w[e / 4] >> (8 * (e % 4)));
     }
 }
 
@@ -421,9 +458,10 @@ hipError_t launch_gemm_generic(const GemmArgs& g, size_t sam, size_t sak, size_t
 hipError_t launch_transpose_i8(const int8_t* src, uint32_t lds_src, int8_t* dst, uint32_t ldd,
                                uint32_t rows, uint32_t cols, hipStream_t stream)
 {
-    dim3 grid((rows + 63) / 64, (ldd + 63) / 64);
+    dim3      grid((rows + 63) / 64, (ldd + 63) / 64);
+    const int vec = reinterpret_cast<uintptr_t>(src) % 16 == 0 && lds_src % 16 == 0;
     hipLaunchKernelGGL(transpose_i8_kernel, grid, dim3(256), 0, stream, src, lds_src, dst, ldd,
-                       rows, cols);
+                       rows, cols, vec);
     return hipGetLastError();
 }
 

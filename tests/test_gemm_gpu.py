@@ -183,6 +183,17 @@ def test_sample_layout(w8a8, gpu):
     assert_i32_equal(host(c2), exp)
 
 
+@pytest.mark.parametrize("m,n,k", [(300, 200, 100), (1000, 520, 784)])
+def test_sample_layout_ragged(w8a8, gpu, m, n, k):
+    # the sample layout's repack: lda = m, ldb = n not multiples of 16 (byte
+    # path) or ragged tile edges, K padded with zeros
+    import torch
+    at = G.int8(41 + m, G.TID_A, (k, m))
+    b = G.int8(41 + m, G.TID_B, (k, n))
+    c = w8a8.gemm(dev(at, gpu), dev(b, gpu), layout=w8a8.LAYOUT_A_COL_B_KN, out_dtype=torch.int32)
+    assert_i32_equal(host(c), O.gemm_i32(at, b, layout=1))
+
+
 def test_output_leading_dimension(w8a8, gpu):
     import torch
     m, n, k = 200, 300, 128
