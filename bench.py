@@ -369,6 +369,8 @@ def bench_moe(torch, w8a8, dev, gen, iters=10):
     y = torch.empty((cap, h), dtype=torch.float16, device=dev)
     out = torch.empty((t, h), dtype=torch.float16, device=dev)
     ws = torch.empty(w8a8.moe_gemm_workspace_size(e, cap, h, inter), dtype=torch.uint8, device=dev)
+    sort_ws = torch.empty(max(1, w8a8.moe_sort_workspace_size(t, k, e)), dtype=torch.uint8,
+                          device=dev)
     stages = ["route", "sort", "quant", "gate_up", "silu_quant", "down", "combine"]
 
     def chain(ev=None):
@@ -376,7 +378,7 @@ def bench_moe(torch, w8a8, dev, gen, iters=10):
         mark(0)
         w, ids = w8a8.topk_softmax(logits, k)
         mark(1)
-        srt = w8a8.moe_sort(ids, e, 32)
+        srt = w8a8.moe_sort(ids, e, 32, workspace=sort_ws)
         mark(2)
         w8a8.moe_smoothquant(x, s, ids, dst_row=srt["dst_row"], rows=cap, out=qa, row_scale=ra)
         mark(3)

@@ -312,12 +312,19 @@ size_t w8a8_moe_sort_capacity(uint32_t tokens, uint32_t topk, uint32_t experts,
  *   padded_count [E] (count rounded up to unit_size), sorted_token_ids
  *   [sorted_capacity] (token of each sorted row, -1 in padding), dst_row
  *   [tokens*topk] (sorted row of each pair, -1 for an id outside [0, E)).
- * experts <= 1024.  One launch; no memset needed before it.
+ * experts <= 1024.  No memset needed before it.  Without a workspace: one
+ * launch of one workgroup.  With one (4-byte aligned, at least
+ * w8a8_moe_sort_workspace_size bytes: 4 * E per 1024 pairs; 0 when
+ * tokens * topk <= 1024): three launches spread over 1024-pair blocks
+ * (block counts, offsets, stable scatter), as the reference splits it into
+ * histogram / prefix / scatter; the outputs are identical either way.
  */
+size_t w8a8_moe_sort_workspace_size(uint32_t tokens, uint32_t topk, uint32_t experts);
+
 int w8a8_moe_sort(const int32_t* topk_ids, uint32_t tokens, uint32_t topk, uint32_t experts,
                   uint32_t unit_size, int32_t* expert_count, int32_t* expert_start,
                   int32_t* padded_count, int32_t* sorted_token_ids, uint32_t sorted_capacity,
-                  int32_t* dst_row, hipStream_t stream);
+                  int32_t* dst_row, void* workspace, size_t ws_bytes, hipStream_t stream);
 
 /*
  * Expert GEMM over expert-sorted rows (the per-expert GEMMs of

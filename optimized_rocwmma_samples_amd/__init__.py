@@ -37,7 +37,7 @@ __all__ = [
     "library", "version", "smoothquant", "moe_smoothquant", "gemm", "gemm_workspace_size",
     "fused_sq_gemm", "W8A8Error", "PackedWeights", "pack_weights", "pack_weights_size",
     "gemm_packed", "gemm_packed_workspace_size", "fused_sq_gemm_packed", "grouped_gemm",
-    "topk_softmax", "moe_sort", "moe_gemm", "moe_gemm_workspace_size", "moe_silu_mul_quant",
+    "topk_softmax", "moe_sort", "moe_sort_workspace_size", "moe_gemm", "moe_gemm_workspace_size", "moe_silu_mul_quant",
     "moe_combine", "moe_ffn", "add_rmsnorm_smoothquant", "rmsnorm", "add_rmsnorm",
     "quantize_weights",
 ]
@@ -418,9 +418,17 @@ def topk_softmax(logits, topk: int):
     return w, ids
 
 
-def moe_sort(topk_ids, experts: int, unit_size: int = 32):
+def moe_sort_workspace_size(tokens: int, topk: int, experts: int) -> int:
+    """Bytes of the optional moe_sort workspace (0: one workgroup suffices)."""
+    return int(library().w8a8_moe_sort_workspace_size(tokens, topk, experts))
+
+
+def moe_sort(topk_ids, experts: int, unit_size: int = 32, workspace="auto"):
     """Stable expert sort of topk_ids int32 [T, k].  Returns a dict with
-    count [E], start [E+1], padded [E], sorted_ids [capacity], dst_row [T*k]."""
+    count [E], start [E+1], padded [E], sorted_ids [capacity], dst_row [T*k].
+    workspace: 'auto' (allocated here when T*k > 1024), None (one
+    workgroup), or a device tensor of moe_sort_workspace_size bytes; the
+    outputs are identical either way."""
     torch = _torch()
     _require_cuda(topk_ids)
     ids = topk_ids.contiguous()
@@ -432,9 +440,10 @@ def moe_sort(topk_ids, experts: int, unit_size: int = 32):
                padded=torch.empty(experts, dtype=torch.int32, device=d),
                sorted_ids=torch.empty(cap, dtype=torch.int32, device=d),
                dst_row=torch.empty(t * k, dtype=torch.int32, device=d))
+    ws, ws_bytes = _workspace(workspace, lambda: moe_sort_workspace_size(t, k, experts), d)
     _lib.call("w8a8_moe_sort", _ptr(ids), t, k, experts, unit_size, _ptr(out["count"]),
               _ptr(out["start"]), _ptr(out["padded"]), _ptr(out["sorted_ids"]), cap,
-              _ptr(out["dst_row"]), _stream(d))
+              _ptr(out["dst_row"]), _ptr(ws), ws_bytes, _stream(d))
     return out
 
 

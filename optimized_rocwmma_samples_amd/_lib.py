@@ -69,8 +69,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "w8a8_grouped_gemm": (_i32, [ctypes.POINTER(GroupDesc), _u32, _i32, _ptr, _size, _ptr]),
     "w8a8_topk_softmax": (_i32, [_ptr, _i32, _ptr, _ptr, _u32, _u32, _u32, _ptr]),
     "w8a8_moe_sort_capacity": (_size, [_u32, _u32, _u32, _u32]),
+    "w8a8_moe_sort_workspace_size": (_size, [_u32, _u32, _u32]),
     "w8a8_moe_sort": (_i32, [_ptr, _u32, _u32, _u32, _u32, _ptr, _ptr, _ptr, _ptr, _u32, _ptr,
-                             _ptr]),
+                             _ptr, _size, _ptr]),
     "w8a8_moe_gemm_workspace_size": (_size, [_u32, _u32, _u32, _u32]),
     "w8a8_moe_gemm": (_i32, [_u32, _u32, _u32, _u32, _ptr, _u32, _ptr, _u32, _u64, _ptr, _u32,
                              _ptr, _ptr, _f32, _f32, _ptr, _ptr, _i32, _ptr, _size, _ptr]),

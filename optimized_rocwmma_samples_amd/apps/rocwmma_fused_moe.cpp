@@ -27,9 +27,12 @@ static void test_fused_moe(uint32_t t, uint32_t h, uint32_t inter, uint32_t e, u
     app::Dev<int32_t>  ids((size_t)t * k), cnt(e), st(e + 1), pad(e), srt(cap), dst((size_t)t * k);
     const size_t       wsb = w8a8_moe_gemm_workspace_size(e, cap, h, inter);
     app::Dev<int8_t>   ws(wsb);
+    const size_t       swsb = w8a8_moe_sort_workspace_size(t, k, e);
+    app::Dev<int8_t>   sws(swsb);
     auto fn = [&] {
         CHECK_W8A8(w8a8_topk_softmax(dl.p, 0, w.p, ids.p, t, e, k, nullptr));
-        CHECK_W8A8(w8a8_moe_sort(ids.p, t, k, e, 32, cnt.p, st.p, pad.p, srt.p, cap, dst.p, nullptr));
+        CHECK_W8A8(w8a8_moe_sort(ids.p, t, k, e, 32, cnt.p, st.p, pad.p, srt.p, cap, dst.p,
+                                 swsb ? sws.p : nullptr, swsb, nullptr));
         CHECK_W8A8(w8a8_moe_smoothquant(dx.p, ds.p, ids.p, qa.p, ra.p, t, h, k, e, 127.f, dst.p,
                                         cap, nullptr));
         CHECK_W8A8(w8a8_moe_gemm(e, cap, 2 * inter, h, qa.p, h, dwgu.p, h, (uint64_t)2 * inter * h,

@@ -20,9 +20,11 @@ static void test_sort(uint32_t tokens, uint32_t experts, uint32_t topk, uint32_t
     }
     const uint32_t    cap = (uint32_t)w8a8_moe_sort_capacity(tokens, topk, experts, unit);
     app::Dev<int32_t> did(ids), cnt(experts), st(experts + 1), pad(experts), srt(cap), dst(total);
+    const size_t      wsb = w8a8_moe_sort_workspace_size(tokens, topk, experts);
+    app::Dev<int8_t>  ws(wsb);
     auto fn = [&] {
         CHECK_W8A8(w8a8_moe_sort(did.p, tokens, topk, experts, unit, cnt.p, st.p, pad.p, srt.p,
-                                 cap, dst.p, nullptr));
+                                 cap, dst.p, wsb ? ws.p : nullptr, wsb, nullptr));
     };
     const double ms = app::bench_ms(fn, 3, 10);
     std::cout << "[MoE Sorting] tokens=" << tokens << " experts=" << experts << " topk=" << topk

@@ -481,10 +481,16 @@ size_t w8a8_moe_sort_capacity(uint32_t tokens, uint32_t topk, uint32_t experts, 
     return (size_t)tokens * topk + (size_t)experts * unit_size;
 }
 
+size_t w8a8_moe_sort_workspace_size(uint32_t tokens, uint32_t topk, uint32_t experts)
+{
+    if(tokens == 0 || topk == 0 || experts == 0 || experts > 1024) return 0;
+    return w8a8::moe_sort_workspace_bytes(tokens, topk, experts);
+}
+
 int w8a8_moe_sort(const int32_t* topk_ids, uint32_t tokens, uint32_t topk, uint32_t experts,
                   uint32_t unit_size, int32_t* expert_count, int32_t* expert_start,
                   int32_t* padded_count, int32_t* sorted_token_ids, uint32_t sorted_capacity,
-                  int32_t* dst_row, hipStream_t stream)
+                  int32_t* dst_row, void* workspace, size_t ws_bytes, hipStream_t stream)
 {
     const char* fn = "w8a8_moe_sort";
     if(!topk_ids || !expert_count || !expert_start || !padded_count || !sorted_token_ids
@@ -500,9 +506,12 @@ int w8a8_moe_sort(const int32_t* topk_ids, uint32_t tokens, uint32_t topk, uint3
     if(sorted_capacity < need)
         return fail(W8A8_ERROR_INVALID_VALUE, "%s: sorted_capacity=%u, %zu needed", fn,
                     sorted_capacity, need);
+    if(workspace && reinterpret_cast<uintptr_t>(workspace) % 4 != 0)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: workspace must be 4-byte aligned", fn);
     return hip_status(w8a8::launch_moe_sort(topk_ids, tokens, topk, experts, unit_size,
                                             expert_count, expert_start, padded_count,
-                                            sorted_token_ids, sorted_capacity, dst_row, stream),
+                                            sorted_token_ids, sorted_capacity, dst_row, workspace,
+                                            workspace ? ws_bytes : 0, stream),
                       fn);
 }
 

@@ -50,36 +50,34 @@ __global__ void __launch_bounds__(kTopkWaves* kWave)
     if(tok >= tokens) return; // uniform per wave
     const size_t row = (size_t)tok * experts;
 
+    // cross-lane steps are DPP reductions (no LDS round trips)
     float wmax = -INFINITY;
     for(uint32_t e = lane; e < experts; e += kWave) wmax = fmaxf(wmax, load_logit<F16>(logits, row + e));
     wmax = wave_max(wmax);
     float wsum = 0.f;
     for(uint32_t e = lane; e < experts; e += kWave) wsum += expf(load_logit<F16>(logits, row + e) - wmax);
-#pragma unroll
-    for(int d = kWave / 2; d > 0; d >>= 1) wsum += __shfl_xor(wsum, d, kWave);
+    wsum            = wave_sum(wsum);
     const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
 
-    // a lane owns experts lane, lane+64, ...: `used` marks the chosen ones
-    uint64_t used = 0;
+    // a lane owns experts lane, lane+64, ...: `used` marks the chosen ones.
+    // Per pick: each lane's best unused candidate (larger logit, then lower
+    // index), the wave max of those values, then the lowest index among the
+    // lanes holding that max: the same winner as a pairwise reduction.
+    constexpr int kNone = 0x7FFFFFFF;
+    uint64_t      used  = 0;
     for(uint32_t k = 0; k < topk; ++k) {
         float bv = -INFINITY;
-        int   bi = 0x7FFFFFFF;
+        int   bi = kNone;
         int   j  = 0;
         for(uint32_t e = lane; e < experts; e += kWave, ++j)
             if(!((used >> j) & 1u)) better(bv, bi, load_logit<F16>(logits, row + e), (int)e);
-#pragma unroll
-        for(int d = kWave / 2; d > 0; d >>= 1) {
-            const float ov = __shfl_xor(bv, d, kWave);
-            const int   oi = __shfl_xor(bi, d, kWave);
-            better(bv, bi, ov, oi);
-        }
-        // every lane now holds the winner; its owner marks it used
-        if(bi != 0x7FFFFFFF && (uint32_t)bi % kWave == (uint32_t)lane)
-            used |= 1ull << ((uint32_t)bi / kWave);
+        const float m = wave_max(bv);
+        const int   w = wave_min_i32(bv == m ? bi : kNone);
+        if(w != kNone && (uint32_t)w % kWave == (uint32_t)lane) used |= 1ull << ((uint32_t)w / kWave);
         if(lane == 0) {
-            const bool ok                          = bi != 0x7FFFFFFF;
-            topk_ids[(size_t)tok * topk + k]       = ok ? bi : -1;
-            topk_w[(size_t)tok * topk + k]         = ok ? expf(bv - wmax) * inv : 0.f;
+            const bool ok                    = w != kNone;
+            topk_ids[(size_t)tok * topk + k] = ok ? w : -1;
+            topk_w[(size_t)tok * topk + k]   = ok ? expf(m - wmax) * inv : 0.f;
         }
     }
 }
@@ -136,7 +134,7 @@ __global__ void __launch_bounds__(kSortThreads)
                 expert_start[e] = carry + s - pad;
                 padded_count[e] = pad;
             }
-            carry += __shfl(s, kWave - 1, kWave);
+            carry += __builtin_amdgcn_readlane(s, kWave - 1);
         }
         if(lane == 0) {
             start[experts]        = carry;
@@ -155,7 +153,7 @@ __global__ void __launch_bounds__(kSortThreads)
         uint64_t pending = __ballot(valid);
         while(pending) {
             const int      leader = __ffsll((unsigned long long)pending) - 1;
-            const int32_t  le     = __shfl(e, leader, kWave);
+            const int32_t  le     = __builtin_amdgcn_readlane(e, leader); // leader is uniform
             const uint64_t same   = __ballot(valid && e == le);
             if(valid && e == le) rank = __popcll(same & ((1ull << lane) - 1));
             if(lane == leader) wcnt[wave * experts + le] = __popcll(same);
@@ -181,6 +179,128 @@ __global__ void __launch_bounds__(kSortThreads)
             cursor[x] += s;
         }
         __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Multi-block expert sort (with the caller's workspace of blocks x E ints):
+// the same outputs and order as moe_sort_kernel, spread over
+// ceil(total / kSortChunk) blocks of one pair per thread.
+//   1. moe_sort_count_kernel: block b counts the experts of its pairs into
+//      ws[b*E + e], and the grid fills sorted_ids with -1.
+//   2. moe_sort_offsets_kernel (one block): per expert the exclusive prefix
+//      of the block counts (in place) and the total, the padded expert
+//      prefix (count, start, padded), then ws[b*E + e] += start[e].
+//   3. moe_sort_scatter_kernel: block b ranks its pairs stably (lanes of a
+//      wave with the same expert by ballot, waves in order through LDS) and
+//      writes sorted_ids[ws[b*E + e] + rank] and dst_row.
+// Blocks cover consecutive pairs, so the order inside an expert is again
+// ascending flat order.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kSortChunk = kSortThreads;
+
+__global__ void __launch_bounds__(kSortThreads)
+    moe_sort_count_kernel(const int32_t* __restrict__ ids, uint32_t total, uint32_t experts,
+                          int32_t* ws, int32_t* sorted_ids, uint32_t sorted_cap)
+{
+    extern __shared__ int32_t cnt[]; // [E]
+    const uint32_t tid = threadIdx.x;
+    for(uint32_t e = tid; e < experts; e += kSortThreads) cnt[e] = 0;
+    __syncthreads();
+    const uint32_t p = blockIdx.x * kSortChunk + tid;
+    if(p < total) {
+        const int32_t e = ids[p];
+        if(e >= 0 && (uint32_t)e < experts) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    for(uint32_t e = tid; e < experts; e += kSortThreads)
+        ws[(size_t)blockIdx.x * experts + e] = cnt[e];
+    for(uint32_t i = blockIdx.x * kSortThreads + tid; i < sorted_cap; i += gridDim.x * kSortThreads)
+        sorted_ids[i] = -1;
+}
+
+__global__ void __launch_bounds__(kSortThreads)
+    moe_sort_offsets_kernel(uint32_t blocks, uint32_t experts, uint32_t unit, int32_t* ws,
+                            int32_t* expert_count, int32_t* expert_start, int32_t* padded_count)
+{
+    extern __shared__ int32_t sm[];
+    int32_t*       cnt   = sm;           // [E]
+    int32_t*       start = cnt + experts; // [E]
+    const uint32_t tid   = threadIdx.x;
+    const int      wave  = tid / kWave;
+    const int      lane  = tid % kWave;
+    for(uint32_t e = tid; e < experts; e += kSortThreads) {
+        int32_t run = 0;
+        for(uint32_t b = 0; b < blocks; ++b) {
+            const int32_t c                = ws[(size_t)b * experts + e];
+            ws[(size_t)b * experts + e]    = run;
+            run                           += c;
+        }
+        cnt[e] = run;
+    }
+    __syncthreads();
+    if(wave == 0) { // padded exclusive prefix, 64 experts per step
+        int32_t carry = 0;
+        for(uint32_t base = 0; base < experts; base += kWave) {
+            const uint32_t e   = base + lane;
+            const int32_t  c   = e < experts ? cnt[e] : 0;
+            const int32_t  pad = (int32_t)(((uint32_t)c + unit - 1) / unit * unit);
+            int32_t        s   = pad;
+#pragma unroll
+            for(int d = 1; d < kWave; d <<= 1) {
+                const int32_t o = __shfl_up(s, d, kWave);
+                if(lane >= d) s += o;
+            }
+            if(e < experts) {
+                start[e]        = carry + s - pad;
+                expert_count[e] = c;
+                expert_start[e] = carry + s - pad;
+                padded_count[e] = pad;
+            }
+            carry += __builtin_amdgcn_readlane(s, kWave - 1);
+        }
+        if(lane == 0) expert_start[experts] = carry;
+    }
+    __syncthreads();
+    for(uint32_t e = tid; e < experts; e += kSortThreads) {
+        const int32_t s0 = start[e];
+        for(uint32_t b = 0; b < blocks; ++b) ws[(size_t)b * experts + e] += s0;
+    }
+}
+
+__global__ void __launch_bounds__(kSortThreads)
+    moe_sort_scatter_kernel(const int32_t* __restrict__ ids, uint32_t total, uint32_t topk,
+                            uint32_t experts, const int32_t* ws, int32_t* sorted_ids,
+                            int32_t* dst_row)
+{
+    extern __shared__ int32_t wcnt[]; // [waves][E]
+    const uint32_t tid  = threadIdx.x;
+    const int      wave = tid / kWave;
+    const int      lane = tid % kWave;
+    for(uint32_t i = tid; i < experts * kSortWaves; i += kSortThreads) wcnt[i] = 0;
+    const uint32_t p     = blockIdx.x * kSortChunk + tid;
+    const int32_t  e     = p < total ? ids[p] : -1;
+    const bool     valid = e >= 0 && (uint32_t)e < experts;
+    __syncthreads();
+    int      rank    = 0;
+    uint64_t pending = __ballot(valid);
+    while(pending) {
+        const int      leader = __ffsll((unsigned long long)pending) - 1;
+        const int32_t  le     = __builtin_amdgcn_readlane(e, leader); // leader is uniform
+        const uint64_t same   = __ballot(valid && e == le);
+        if(valid && e == le) rank = __popcll(same & ((1ull << lane) - 1));
+        if(lane == leader) wcnt[wave * experts + le] = __popcll(same);
+        pending &= ~same;
+    }
+    __syncthreads();
+    if(valid) {
+        int32_t base = ws[(size_t)blockIdx.x * experts + e];
+        for(int w = 0; w < wave; ++w) base += wcnt[w * experts + e];
+        const int32_t slot = base + rank;
+        sorted_ids[slot]   = (int32_t)(p / topk);
+        dst_row[p]         = slot;
+    } else if(p < total) {
+        dst_row[p] = -1;
     }
 }
 
@@ -513,11 +633,34 @@ size_t moe_sort_lds_bytes(uint32_t experts)
     return sizeof(int32_t) * ((size_t)experts * (3 + kSortWaves) + 1);
 }
 
+size_t moe_sort_workspace_bytes(uint32_t tokens, uint32_t topk, uint32_t experts)
+{
+    const uint64_t total = (uint64_t)tokens * topk;
+    if(total <= kSortChunk) return 0; // one block: the single-workgroup kernel
+    return (size_t)((total + kSortChunk - 1) / kSortChunk) * experts * sizeof(int32_t);
+}
+
 hipError_t launch_moe_sort(const int32_t* ids, uint32_t tokens, uint32_t topk, uint32_t experts,
                            uint32_t unit, int32_t* count, int32_t* start, int32_t* padded,
-                           int32_t* sorted_ids, uint32_t sorted_cap, int32_t* dst_row,
-                           hipStream_t stream)
+                           int32_t* sorted_ids, uint32_t sorted_cap, int32_t* dst_row, void* ws,
+                           size_t ws_bytes, hipStream_t stream)
 {
+    const uint32_t total = tokens * topk;
+    const size_t   need  = moe_sort_workspace_bytes(tokens, topk, experts);
+    if(ws != nullptr && need > 0 && ws_bytes >= need) {
+        const uint32_t blocks = (total + kSortChunk - 1) / kSortChunk;
+        int32_t*       w      = static_cast<int32_t*>(ws);
+        hipLaunchKernelGGL(moe_sort_count_kernel, dim3(blocks), dim3(kSortThreads),
+                           experts * sizeof(int32_t), stream, ids, total, experts, w, sorted_ids,
+                           sorted_cap);
+        hipLaunchKernelGGL(moe_sort_offsets_kernel, dim3(1), dim3(kSortThreads),
+                           2 * experts * sizeof(int32_t), stream, blocks, experts, unit, w, count,
+                           start, padded);
+        hipLaunchKernelGGL(moe_sort_scatter_kernel, dim3(blocks), dim3(kSortThreads),
+                           (size_t)experts * kSortWaves * sizeof(int32_t), stream, ids, total, topk,
+                           experts, w, sorted_ids, dst_row);
+        return hipGetLastError();
+    }
     const size_t lds = moe_sort_lds_bytes(experts);
     if(lds > 65536) {
         static std::once_flag once;

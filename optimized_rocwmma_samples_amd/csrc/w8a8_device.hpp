@@ -41,6 +41,23 @@ __device__ __forceinline__ float wave_max(float v)
     return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
+template <int Ctrl>
+__device__ __forceinline__ int dpp_mov_i32(int v)
+{
+    return __builtin_amdgcn_update_dpp(0, v, Ctrl, 0xF, 0xF, false);
+}
+
+// Min over all 64 lanes of an int; the result is wave-uniform.
+__device__ __forceinline__ int wave_min_i32(int v)
+{
+    v = min(v, dpp_mov_i32<kDppQuadXor1>(v));
+    v = min(v, dpp_mov_i32<kDppQuadXor2>(v));
+    v = min(v, dpp_mov_i32<kDppRowHalfMirror>(v));
+    v = min(v, dpp_mov_i32<kDppRowMirror>(v));
+    return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+               min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
 // Sum over all 64 lanes in a fixed order (quad butterflies, half-row and row
 // mirrors, then the four row totals left to right); the result is
 // wave-uniform and the same on every call for the same inputs.

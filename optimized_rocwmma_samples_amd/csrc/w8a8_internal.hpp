@@ -119,10 +119,13 @@ hipError_t launch_topk_softmax(const void* logits, bool f16, float* w, int32_t* 
                                hipStream_t stream);
 
 size_t     moe_sort_lds_bytes(uint32_t experts);
+// ws (optional, moe_sort_workspace_bytes): the multi-block sort for inputs of
+// more than one block of pairs; NULL or smaller: one workgroup.
+size_t     moe_sort_workspace_bytes(uint32_t tokens, uint32_t topk, uint32_t experts);
 hipError_t launch_moe_sort(const int32_t* ids, uint32_t tokens, uint32_t topk, uint32_t experts,
                            uint32_t unit, int32_t* count, int32_t* start, int32_t* padded,
-                           int32_t* sorted_ids, uint32_t sorted_cap, int32_t* dst_row,
-                           hipStream_t stream);
+                           int32_t* sorted_ids, uint32_t sorted_cap, int32_t* dst_row, void* ws,
+                           size_t ws_bytes, hipStream_t stream);
 
 hipError_t launch_silu_mul_quant(const uint16_t* gu, uint32_t ld_gu, const float* s2,
                                  const int32_t* expert_start, const int32_t* expert_count,

@@ -239,7 +239,7 @@ def test_topk_softmax_validation(w8a8):
 
 def test_moe_sort_validation(w8a8):
     assert W.library().w8a8_moe_sort_capacity(4096, 2, 8, 32) == 4096 * 2 + 8 * 32
-    ok = [FAKE, 100, 2, 8, 32, FAKE, FAKE, FAKE, FAKE, 200 + 256, FAKE, None]
+    ok = [FAKE, 100, 2, 8, 32, FAKE, FAKE, FAKE, FAKE, 200 + 256, FAKE, None, 0, None]
     bad = list(ok); bad[9] = 200 + 255
     rc, msg = _status("w8a8_moe_sort", *bad)
     assert rc == W.ERROR_INVALID_VALUE and "capacity" in msg
@@ -249,6 +249,18 @@ def test_moe_sort_validation(w8a8):
     assert _status("w8a8_moe_sort", *bad)[0] == W.ERROR_INVALID_VALUE
     bad = list(ok); bad[4] = 0
     assert _status("w8a8_moe_sort", *bad)[0] == W.ERROR_INVALID_VALUE
+    bad = list(ok); bad[11] = ctypes.c_void_p(0x1002); bad[12] = 1 << 20
+    rc, msg = _status("w8a8_moe_sort", *bad)
+    assert rc == W.ERROR_INVALID_VALUE and "aligned" in msg
+
+
+def test_moe_sort_workspace_size(w8a8):
+    lib = W.library()
+    # 4 * E bytes per block of 1024 pairs; one block needs none
+    assert lib.w8a8_moe_sort_workspace_size(512, 2, 8) == 0
+    assert lib.w8a8_moe_sort_workspace_size(513, 2, 8) == 2 * 8 * 4
+    assert lib.w8a8_moe_sort_workspace_size(3328, 8, 128) == 26 * 128 * 4
+    assert lib.w8a8_moe_sort_workspace_size(100, 2, 2000) == 0
 
 
 def _moe_gemm_args(**kw):

@@ -72,13 +72,15 @@ def test_topk_softmax_fp16_vs_reference_kernel(w8a8, gpu):
     assert ulp_diff(host(w), host(rw)).max() <= 4
 
 
+@pytest.mark.parametrize("workspace", ["auto", None])  # multi-block / one workgroup
 @pytest.mark.parametrize("t,k,e,unit", [(4096, 2, 8, 32), (1000, 6, 64, 16), (37, 1, 5, 256),
-                                        (3000, 4, 300, 8)])
-def test_moe_sort_exact(w8a8, gpu, t, k, e, unit):
+                                        (3000, 4, 300, 8), (3328, 8, 128, 32),
+                                        (2100, 3, 1024, 4)])
+def test_moe_sort_exact(w8a8, gpu, t, k, e, unit, workspace):
     ids = routing_ids(t, e, k, t + e)
     ids[1, 0] = -1
     ids[2, k - 1] = e  # out of range: skipped
-    srt = w8a8.moe_sort(dev(ids, gpu), e, unit)
+    srt = w8a8.moe_sort(dev(ids, gpu), e, unit, workspace=workspace)
     count, start, padded, sorted_ids, dst = O.moe_sort(ids, e, unit)
     assert np.array_equal(host(srt["count"]), count)
     assert np.array_equal(host(srt["start"]), start)
