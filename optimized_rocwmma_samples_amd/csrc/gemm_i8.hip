@@ -383,16 +383,31 @@ bool gemm_packed_ok(const GemmArgs& g)
     return g.m <= kDecodeMaxM ? gemm_decode_ok(g) : (uint64_t)g.lda * GemmPacked::kBM <= kLimit;
 }
 
+// Row-major weights at 32 < m <= 64: the decode kernel re-reads all of A for
+// every 32 weight rows (A traffic twice the weight bytes at m = 64), while
+// 128 x 128 tiles read each weight tile once.  They take over when they fill
+// the chip by themselves, or with a K split when the caller gave the
+// workspace (cold weights, m = 64: W [28672, 8192] 96 -> 53 µs; W [8192,
+// 28672] only with the split).
+bool tiles_beat_decode(const GemmArgs& g, void* ws, size_t ws_bytes)
+{
+    if(g.m <= 32) return false;
+    const DenseSplit d = dense_split(g.m, g.n, g.k);
+    if(d.parts == 1) return d.tiles >= (uint64_t)device_cus() * 3 / 4;
+    return ws != nullptr && ws_bytes >= d.bytes;
+}
+
 size_t gemm_nk_workspace_bytes(const GemmArgs& g)
 {
-    if(g.m == 0 || g.n == 0 || g.k == 0 || gemm_decode_ok(g)) return 0;
+    if(g.m == 0 || g.n == 0 || g.k == 0 || (gemm_decode_ok(g) && g.m <= 32)) return 0;
     return dense_split(g.m, g.n, g.k).bytes;
 }
 
 hipError_t launch_gemm_nk(const GemmArgs& g, void* ws, size_t ws_bytes, hipStream_t stream)
 {
     if(g.m == 0 || g.n == 0) return hipSuccess;
-    if(gemm_decode_ok(g)) return launch_gemm_decode(g, false, nullptr, 0, stream);
+    if(gemm_decode_ok(g) && !tiles_beat_decode(g, ws, ws_bytes))
+        return launch_gemm_decode(g, false, nullptr, 0, stream);
     const size_t esz    = g.out_type == W8A8_OUT_I32 ? 4 : 2;
     const int    vec_ok = out_vec_ok(g);
     // The tile kernel addresses each operand through a buffer resource whose

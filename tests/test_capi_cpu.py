@@ -119,7 +119,8 @@ def test_gemm_workspace_size(w8a8):
     assert W.gemm_workspace_size(512, 4096, 4096) == 128 * 2 * 65536
     assert W.gemm_workspace_size(512, 512, 16384) == 16 * 8 * 65536
     assert W.gemm_workspace_size(8192, 4096, 4096) == 0       # fills the chip
-    assert W.gemm_workspace_size(64, 4096, 16384) == 0        # decode kernel
+    assert W.gemm_workspace_size(32, 4096, 16384) == 0        # decode kernel
+    assert W.gemm_workspace_size(64, 4096, 16384) == 32 * 8 * 65536  # 128 x 128 tiles, split
 
 
 def test_fused_validation(w8a8):
