@@ -2,11 +2,11 @@
 // Stands in for the reference's split-K and stream-K samples
 // (rocwmma_gemm_splitk.cpp:251-263, rocwmma_streamk_gemm.cpp:286-297): m <= 64
 // runs the weight-streaming kernel that splits K across the waves of each
-// block (int32 partials summed in LDS, one launch, no workspace) up to
-// m = 32; larger m runs 128 x 128 (or larger) tiles, and when those fill at
-// most half of the CUs each tile is split along K across blocks into the
-// caller's workspace (int32 partials, a fixup launch sums them), like the
-// reference's workspace-based split-K (:214).
+// block (int32 partials summed in LDS, one launch, no workspace), or 64 x 128
+// tiles where those stream the row-major weights faster; tiles that fill at
+// most half of the CUs are split along K across blocks into the caller's
+// workspace (int32 partials, a fixup launch sums them), like the reference's
+// workspace-based split-K (:214).
 // `rocwmma_gemm_splitk [M N K]`; default: BASELINE config 4, the Llama-70B MLP
 // weights [28672, 8192] and [8192, 28672] at M in {1, 16, 64}, then the
 // reference's shapes.  Result line
@@ -33,7 +33,7 @@ static void test_decode(uint32_t m, uint32_t n, uint32_t k, bool verify)
     const double ms    = app::bench_ms([&] { fn(dc.p, W8A8_OUT_F16); });
     const double bytes = (double)n * k + (double)m * k + 4.0 * (m + n) + 2.0 * m * n;
     std::cout << "[SplitK-GEMM] M=" << m << " N=" << n << " K=" << k
-              << " split_k=" << (m <= 32 ? "in-block" : wsb ? "workspace" : "none") << "  " << ms
+              << " split_k=" << (wsb ? "workspace" : m <= 64 ? "in-block" : "none") << "  " << ms
               << " ms  "
               << 2.0 * m * n * k / (ms * 1e-3) / 1e12 << " TFlops/s  "
               << bytes / (ms * 1e-3) / 1e9 << " GB/s\n";

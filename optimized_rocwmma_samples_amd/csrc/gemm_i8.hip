@@ -28,6 +28,9 @@ using GemmMain  = gemm::Cfg<256, 256, 128, 2, 2, 4, 4>;
 // 128 x 256: o_proj 47 -> 40 µs, down 146 -> 116 µs).
 using GemmMidM  = gemm::Cfg<128, 256, 128, 3, 2, 4, 4>; // 8 waves of 64 x 64, 144 KiB LDS
 using GemmSmall = gemm::Cfg<128, 128, 128, 3, 2, 4, 4>; // 8 waves of 64 x 32, 96 KiB LDS
+// m <= 64 over row-major weights (tiles_beat_decode): 4 waves of 64 x 32,
+// 4 stages (96 KiB LDS), one tile row.
+using GemmDecTile = gemm::Cfg<64, 128, 128, 4, 1, 4, 1>;
 // Packed-weight tile configurations (m > kDecodeMaxM): 256 x 256 blocks, and
 // 128 / 64-row blocks for launches that would leave most CUs idle with them
 // (pick_packed_cfg).
@@ -185,10 +188,11 @@ uint32_t device_cus()
 // down 140 -> 71 µs with 128 x 128; M = 2048 o_proj 59 -> 42 µs, down
 // 164 -> 119 µs with 128 x 256; the shapes with enough 256 x 256 tiles, e.g.
 // M = 2048 qkv or gate_up, are slower with smaller ones).
-enum class TileCfg { kMain, kMidM, kSmall };
+enum class TileCfg { kMain, kMidM, kSmall, kDecode };
 
 TileCfg pick_tile_cfg(uint32_t m, uint32_t n)
 {
+    if(m <= kDecodeMaxM) return TileCfg::kDecode;
     auto tiles = [&](uint32_t bm, uint32_t bn) {
         return (uint64_t)((m + bm - 1) / bm) * ((n + bn - 1) / bn);
     };
@@ -228,6 +232,9 @@ DenseSplit dense_split(uint32_t m, uint32_t n, uint32_t k)
         bm = GemmMidM::kBM, bn = GemmMidM::kBN, part_bytes = gemm::Partial<GemmMidM>::kBytes;
     } else if(d.cfg == TileCfg::kSmall) {
         bm = GemmSmall::kBM, bn = GemmSmall::kBN, part_bytes = gemm::Partial<GemmSmall>::kBytes;
+    } else if(d.cfg == TileCfg::kDecode) {
+        bm = GemmDecTile::kBM, bn = GemmDecTile::kBN,
+        part_bytes = gemm::Partial<GemmDecTile>::kBytes;
     }
     d.tiles             = ((m + bm - 1) / bm) * ((n + bn - 1) / bn);
     const uint32_t cus  = device_cus();
@@ -383,15 +390,16 @@ bool gemm_packed_ok(const GemmArgs& g)
     return g.m <= kDecodeMaxM ? gemm_decode_ok(g) : (uint64_t)g.lda * GemmPacked::kBM <= kLimit;
 }
 
-// Row-major weights at 32 < m <= 64: the decode kernel re-reads all of A for
-// every 32 weight rows (A traffic twice the weight bytes at m = 64), while
-// 128 x 128 tiles read each weight tile once.  They take over when they fill
+// Row-major weights at m <= 64: the decode kernel streams 32-row weight
+// panels with 32-byte pieces per lane and re-reads all of A for every panel
+// (at m = 64 twice the weight bytes from L2); 64 x 128 tiles load each
+// weight tile once as whole 128-byte rows.  They take over when they fill
 // the chip by themselves, or with a K split when the caller gave the
-// workspace (cold weights, m = 64: W [28672, 8192] 96 -> 53 µs; W [8192,
-// 28672] only with the split).
+// workspace.  Cold weights, W [28672, 8192]: m = 1 61 -> 51 µs, m = 16
+// 72 -> 54 µs, m = 32 83 -> 54 µs, m = 64 96 -> 53 µs; W [8192, 28672]
+// has 64 tiles and needs the split.
 bool tiles_beat_decode(const GemmArgs& g, void* ws, size_t ws_bytes)
 {
-    if(g.m <= 32) return false;
     const DenseSplit d = dense_split(g.m, g.n, g.k);
     if(d.parts == 1) return d.tiles >= (uint64_t)device_cus() * 3 / 4;
     return ws != nullptr && ws_bytes >= d.bytes;
@@ -399,7 +407,7 @@ bool tiles_beat_decode(const GemmArgs& g, void* ws, size_t ws_bytes)
 
 size_t gemm_nk_workspace_bytes(const GemmArgs& g)
 {
-    if(g.m == 0 || g.n == 0 || g.k == 0 || (gemm_decode_ok(g) && g.m <= 32)) return 0;
+    if(g.m == 0 || g.n == 0 || g.k == 0) return 0;
     return dense_split(g.m, g.n, g.k).bytes;
 }
 
@@ -428,8 +436,11 @@ hipError_t launch_gemm_nk(const GemmArgs& g, void* ws, size_t ws_bytes, hipStrea
                 return gemm::launch_cfg_split<GemmMain>(p, g.out_type, vec_ok, pw, d.parts, stream);
             case TileCfg::kMidM:
                 return gemm::launch_cfg_split<GemmMidM>(p, g.out_type, vec_ok, pw, d.parts, stream);
-            default:
+            case TileCfg::kSmall:
                 return gemm::launch_cfg_split<GemmSmall>(p, g.out_type, vec_ok, pw, d.parts, stream);
+            default:
+                return gemm::launch_cfg_split<GemmDecTile>(p, g.out_type, vec_ok, pw, d.parts,
+                                                           stream);
             }
         }
     }
@@ -447,7 +458,8 @@ hipError_t launch_gemm_nk(const GemmArgs& g, void* ws, size_t ws_bytes, hipStrea
             switch(pick_tile_cfg(p.m, p.n)) {
             case TileCfg::kMain: e = gemm::launch_cfg<GemmMain>(p, g.out_type, vec_ok, stream); break;
             case TileCfg::kMidM: e = gemm::launch_cfg<GemmMidM>(p, g.out_type, vec_ok, stream); break;
-            default: e = gemm::launch_cfg<GemmSmall>(p, g.out_type, vec_ok, stream); break;
+            case TileCfg::kSmall: e = gemm::launch_cfg<GemmSmall>(p, g.out_type, vec_ok, stream); break;
+            default: e = gemm::launch_cfg<GemmDecTile>(p, g.out_type, vec_ok, stream); break;
             }
             if(e != hipSuccess) return e;
         }

@@ -119,8 +119,11 @@ def test_gemm_workspace_size(w8a8):
     assert W.gemm_workspace_size(512, 4096, 4096) == 128 * 2 * 65536
     assert W.gemm_workspace_size(512, 512, 16384) == 16 * 8 * 65536
     assert W.gemm_workspace_size(8192, 4096, 4096) == 0       # fills the chip
-    assert W.gemm_workspace_size(32, 4096, 16384) == 0        # decode kernel
-    assert W.gemm_workspace_size(64, 4096, 16384) == 32 * 8 * 65536  # 128 x 128 tiles, split
+    # m <= 64: 64 x 128 tiles (32 KiB per piece) when they fill the chip or can split
+    assert W.gemm_workspace_size(32, 4096, 16384) == 32 * 8 * 32768
+    assert W.gemm_workspace_size(1, 8192, 28672) == 64 * 4 * 32768
+    assert W.gemm_workspace_size(16, 28672, 8192) == 0        # 224 tiles fill the chip
+    assert W.gemm_workspace_size(8, 1000, 512) == 0           # K too short: decode kernel
 
 
 def test_fused_validation(w8a8):
