@@ -285,7 +285,7 @@ def profiled_traffic(projs):
         return None, None
     table = {}
     for line in TRAFFIC_PROFILE.read_text().splitlines():
-        mt = re.match(r"traffic \S*gemm_i8_tile_kernel\S* grid=(\d+) .* bytes=(\d+)", line)
+        mt = re.match(r"traffic \S*gemm_i8_tile_kernel<\S*Cfg<256,256,\S* grid=(\d+) .* bytes=(\d+)", line)
         if mt:
             table[int(mt.group(1))] = int(mt.group(2))
     per = []

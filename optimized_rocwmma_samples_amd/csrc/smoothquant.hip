@@ -344,6 +344,8 @@ hipError_t launch_stream(const QuantRows& p, hipStream_t stream)
 {
     constexpr int  kGroups = THREADS / kWave / WPR;
     const size_t   lds     = (size_t)CPL * 512 * WPR * sizeof(float);
+    // one row group must span the whole row
+    if((uint64_t)CPL * 512 * WPR < p.n) return hipErrorInvalidValue;
     static int     max_blocks = [] {
         int dev = 0, cus = 256;
         if(hipGetDevice(&dev) == hipSuccess)
