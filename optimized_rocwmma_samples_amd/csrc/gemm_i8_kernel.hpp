@@ -221,6 +221,72 @@ __device__ __forceinline__ void store4(const KArgs& p, uint32_t m, uint32_t n, c
     }
 }
 
+// Dequant scales of one lane's outputs in a wave tile: sa for each 32-row
+// MFMA tile (row m = lane % 32), sb for each run of 4 columns.  Tensor-scale
+// mode (no scale vectors) folds tsa * tsb into sa and sets sb to 1, which is
+// exact, so every output is (acc * sa) * sb.  On tiles that lie inside the
+// matrix the loads are unconditional: they all go out back to back and the
+// epilogue waits for them once (per-group guarded loads each waited for
+// their own result and serialized eight memory latencies).
+template <class C>
+struct EpiScales {
+    float  sa[C::kTilesM];
+    float4 sb[C::kTilesN][4];
+
+    __device__ __forceinline__ void load(const KArgs& p, uint32_t m0, uint32_t n0, int wm, int wn,
+                                         int lane, int vec_ok)
+    {
+        const uint32_t mb = m0 + wm * C::kWaveM + (lane & 31);
+        const uint32_t nb = n0 + wn * C::kWaveN + (lane >> 5) * 4;
+        if(p.sa == nullptr && p.sb == nullptr) {
+            const float ab = p.tsa * p.tsb;
+#pragma unroll
+            for(int i = 0; i < C::kTilesM; ++i) sa[i] = ab;
+#pragma unroll
+            for(int j = 0; j < C::kTilesN; ++j)
+#pragma unroll
+                for(int g = 0; g < 4; ++g) sb[j][g] = make_float4(1.f, 1.f, 1.f, 1.f);
+            return;
+        }
+        if(p.sa == nullptr) {
+#pragma unroll
+            for(int i = 0; i < C::kTilesM; ++i) sa[i] = p.tsa;
+        } else if(m0 + C::kBM <= p.m) {
+#pragma unroll
+            for(int i = 0; i < C::kTilesM; ++i) sa[i] = p.sa[mb + i * 32];
+        } else {
+#pragma unroll
+            for(int i = 0; i < C::kTilesM; ++i)
+                sa[i] = mb + i * 32 < p.m ? p.sa[mb + i * 32] : p.tsa;
+        }
+        if(p.sb == nullptr) {
+#pragma unroll
+            for(int j = 0; j < C::kTilesN; ++j)
+#pragma unroll
+                for(int g = 0; g < 4; ++g) sb[j][g] = make_float4(p.tsb, p.tsb, p.tsb, p.tsb);
+        } else if(vec_ok && n0 + C::kBN <= p.n) {
+#pragma unroll
+            for(int j = 0; j < C::kTilesN; ++j)
+#pragma unroll
+                for(int g = 0; g < 4; ++g)
+                    sb[j][g] = *reinterpret_cast<const float4*>(p.sb + nb + j * 32 + g * 8);
+        } else {
+#pragma unroll
+            for(int j = 0; j < C::kTilesN; ++j)
+#pragma unroll
+                for(int g = 0; g < 4; ++g) {
+                    const uint32_t n = nb + j * 32 + g * 8;
+                    float4         v = make_float4(p.tsb, p.tsb, p.tsb, p.tsb);
+                    if(n + 0 < p.n) v.x = p.sb[n + 0];
+                    if(n + 1 < p.n) v.y = p.sb[n + 1];
+                    if(n + 2 < p.n) v.z = p.sb[n + 2];
+                    if(n + 3 < p.n) v.w = p.sb[n + 3];
+                    sb[j][g] = v;
+                }
+        }
+    }
+};
+
 // fp16 epilogue through LDS.  The MFMA result layout gives each lane runs of 4
 // consecutive n in 32 different rows, so storing straight from registers
 // scatters every wave store over 32 cache lines in 16-byte pieces.  Instead
@@ -233,7 +299,7 @@ __device__ __forceinline__ void epilogue_f16_lds(const KArgs& p, uint32_t m0, ui
                                                  int vec_ok, int8_t* lds, int slot, int lane,
                                                  int wm, int wn,
                                                  const v16i (&acc)[C::kTilesM][C::kTilesN],
-                                                 bool mode1, float ab)
+                                                 const EpiScales<C>& sc)
 {
     constexpr int kRowBytes  = C::kWaveN * 2;
     constexpr int kRowChunks = kRowBytes / 16;
@@ -247,33 +313,19 @@ __device__ __forceinline__ void epilogue_f16_lds(const KArgs& p, uint32_t m0, ui
     int8_t* stage = lds + slot * (C::kWaveM * kRowBytes);
 #pragma unroll
     for(int i = 0; i < C::kTilesM; ++i) {
-        const int      row = i * 32 + (lane & 31);
-        const uint32_t m   = m0 + wm * C::kWaveM + row;
-        const float    sa  = (p.sa != nullptr && m < p.m) ? p.sa[m] : p.tsa;
+        const int row = i * 32 + (lane & 31);
 #pragma unroll
         for(int j = 0; j < C::kTilesN; ++j) {
 #pragma unroll
             for(int g = 0; g < 4; ++g) {
-                const uint32_t n  = n0 + wn * C::kWaveN + j * 32 + g * 8 + (lane >> 5) * 4;
-                float4         sb = make_float4(p.tsb, p.tsb, p.tsb, p.tsb);
-                if(p.sb != nullptr) {
-                    if(vec_ok && n + 4 <= p.n)
-                        sb = *reinterpret_cast<const float4*>(p.sb + n);
-                    else {
-                        if(n + 0 < p.n) sb.x = p.sb[n + 0];
-                        if(n + 1 < p.n) sb.y = p.sb[n + 1];
-                        if(n + 2 < p.n) sb.z = p.sb[n + 2];
-                        if(n + 3 < p.n) sb.w = p.sb[n + 3];
-                    }
-                }
-                const float sbv[4] = {sb.x, sb.y, sb.z, sb.w};
-                uint32_t    h[4];
+                const float4 sb     = sc.sb[j][g];
+                const float  sbv[4] = {sb.x, sb.y, sb.z, sb.w};
+                uint32_t     h[4];
+                // two roundings (fp32 product, then fp16), as the reference's
+                // float epilogue does: never one fused mixed-precision multiply
 #pragma unroll
-                for(int e = 0; e < 4; ++e) {
-                    float f = (float)acc[i][j][g * 4 + e];
-                    f       = mode1 ? f * ab : (f * sa) * sbv[e];
-                    h[e]    = float_to_half_bits(f);
-                }
+                for(int e = 0; e < 4; ++e)
+                    h[e] = float_to_half_bits_2step(((float)acc[i][j][g * 4 + e] * sc.sa[i]) * sbv[e]);
                 const int chunk = j * 4 + g;
                 const int phys  = chunk ^ (row & (kSwz - 1));
                 v2i       pk;
@@ -373,10 +425,10 @@ __device__ __forceinline__ void add_partial(const int32_t* part, uint32_t tid,
 }
 
 template <class C, int OUT>
-__device__ __forceinline__ void tile_epilogue(const KArgs& p, uint32_t m0, uint32_t n0,
-                                              int vec_ok, int8_t* lds,
-                                              const v16i (&acc)[C::kTilesM][C::kTilesN],
-                                              int wave_base = 0);
+__device__ __forceinline__ void tile_epilogue_sc(const KArgs& p, uint32_t m0, uint32_t n0,
+                                                 int vec_ok, int8_t* lds,
+                                                 const v16i (&acc)[C::kTilesM][C::kTilesN],
+                                                 int wave_base, const EpiScales<C>& sc);
 
 // One BM x BN output tile at (m0, n0) of problem p, computed by the whole
 // block; `lds` is the block's kLdsBytes ring.  Shared by the plain, grouped
@@ -523,6 +575,9 @@ __device__ __forceinline__ void gemm_tile(const KArgs& p, uint32_t m0, uint32_t 
         mfma_tile(fa[gl & 1], fb[gl & 1]);
         interleave_mfma_vmem_ds<kMfma, C::kLoads, kDs, 1>();
     }
+    // the fp16 epilogue's scales load while the last tile's MFMAs run
+    EpiScales<C> sc;
+    if constexpr(!PART && OUT == W8A8_OUT_F16) sc.load(p, m0, n0, wm, wn, lane, vec_ok);
     {
         const int8_t* sbase = lds + ((nk - 1) % C::kStages) * C::kStageBytes;
 #pragma unroll
@@ -538,18 +593,19 @@ __device__ __forceinline__ void gemm_tile(const KArgs& p, uint32_t m0, uint32_t 
         store_partial<C>(part, acc);
         return;
     }
-    tile_epilogue<C, OUT>(p, m0, n0, vec_ok, lds, acc);
+    tile_epilogue_sc<C, OUT>(p, m0, n0, vec_ok, lds, acc, 0, sc);
 }
 
 // acc[i][j][r]: m = m0 + wm*kWaveM + i*32 + lane%32,
 //               n = n0 + wn*kWaveN + j*32 + (r/4)*8 + (lane/32)*4 + r%4.
 // A block may hold only waves wave_base, wave_base + 1, ... of the tile (the
 // split-tile fixup); each wave stages through LDS slice threadIdx.x / 64.
+// sc: the fp16 path's scales, loaded by the caller (unused for int32 output).
 template <class C, int OUT>
-__device__ __forceinline__ void tile_epilogue(const KArgs& p, uint32_t m0, uint32_t n0,
-                                              int vec_ok, int8_t* lds,
-                                              const v16i (&acc)[C::kTilesM][C::kTilesN],
-                                              int wave_base)
+__device__ __forceinline__ void tile_epilogue_sc(const KArgs& p, uint32_t m0, uint32_t n0,
+                                                 int vec_ok, int8_t* lds,
+                                                 const v16i (&acc)[C::kTilesM][C::kTilesN],
+                                                 int wave_base, const EpiScales<C>& sc)
 {
     const int   slot  = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int   wave  = wave_base + slot;
@@ -559,7 +615,7 @@ __device__ __forceinline__ void tile_epilogue(const KArgs& p, uint32_t m0, uint3
     const bool  mode1 = (p.sa == nullptr && p.sb == nullptr);
     const float ab    = p.tsa * p.tsb;
     if constexpr(OUT == W8A8_OUT_F16) {
-        epilogue_f16_lds<C>(p, m0, n0, vec_ok, lds, slot, lane, wm, wn, acc, mode1, ab);
+        epilogue_f16_lds<C>(p, m0, n0, vec_ok, lds, slot, lane, wm, wn, acc, sc);
         return;
     }
 #pragma unroll
@@ -589,6 +645,22 @@ __device__ __forceinline__ void tile_epilogue(const KArgs& p, uint32_t m0, uint3
             }
         }
     }
+}
+
+// Epilogue of a tile whose scales are not loaded yet (K-split fixups,
+// grouped and MoE fixups): one batch of scale loads, then the epilogue.
+template <class C, int OUT>
+__device__ __forceinline__ void tile_epilogue(const KArgs& p, uint32_t m0, uint32_t n0,
+                                              int vec_ok, int8_t* lds,
+                                              const v16i (&acc)[C::kTilesM][C::kTilesN],
+                                              int wave_base = 0)
+{
+    EpiScales<C> sc;
+    if constexpr(OUT == W8A8_OUT_F16) {
+        const int wave = wave_base + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+        sc.load(p, m0, n0, wave / C::kWavesN, wave % C::kWavesN, threadIdx.x % kWave, vec_ok);
+    }
+    tile_epilogue_sc<C, OUT>(p, m0, n0, vec_ok, lds, acc, wave_base, sc);
 }
 
 template <class C, int OUT>
