@@ -8,6 +8,7 @@
 #include "gemm_i8_decode_wide_kernel.hpp"
 #include "gemm_i8_kernel.hpp"
 #include "gemm_i8_pb_kernel.hpp"
+#include "gemm_i8_persist_kernel.hpp"
 #include "w8a8_internal.hpp"
 
 #include <algorithm>
@@ -405,6 +406,17 @@ bool tiles_beat_decode(const GemmArgs& g, void* ws, size_t ws_bytes)
     return ws != nullptr && ws_bytes >= d.bytes;
 }
 
+// The persistent tile kernel for a 256 x 256 launch: fp16 output, at least
+// two tiles per CU and at most 32 k-tiles per tile.  It saves a fixed cost
+// per tile (workgroup launch, cold prologue, store burst), which pays where
+// tiles are short: 2-4% at M=8192 K=4096 N=28672, 10-20% at K <= 1024,
+// nothing measurable at K=14336 with two tiles per CU.
+bool persist_pays(const KArgs& p, int out_type, int vec_ok)
+{
+    return out_type == W8A8_OUT_F16 && (p.k + GemmMain::kBK - 1) / GemmMain::kBK <= 32
+           && gemm::persist_ok<GemmMain>(p, vec_ok, device_cus());
+}
+
 size_t gemm_nk_workspace_bytes(const GemmArgs& g)
 {
     if(g.m == 0 || g.n == 0 || g.k == 0) return 0;
@@ -456,7 +468,11 @@ hipError_t launch_gemm_nk(const GemmArgs& g, void* ws, size_t ws_bytes, hipStrea
             p.sb    = g.scale_b ? g.scale_b + n0 : nullptr;
             hipError_t e;
             switch(pick_tile_cfg(p.m, p.n)) {
-            case TileCfg::kMain: e = gemm::launch_cfg<GemmMain>(p, g.out_type, vec_ok, stream); break;
+            case TileCfg::kMain:
+                e = persist_pays(p, g.out_type, vec_ok)
+                        ? gemm::launch_cfg_persist<GemmMain>(p, vec_ok, device_cus(), stream)
+                        : gemm::launch_cfg<GemmMain>(p, g.out_type, vec_ok, stream);
+                break;
             case TileCfg::kMidM: e = gemm::launch_cfg<GemmMidM>(p, g.out_type, vec_ok, stream); break;
             case TileCfg::kSmall: e = gemm::launch_cfg<GemmSmall>(p, g.out_type, vec_ok, stream); break;
             default: e = gemm::launch_cfg<GemmDecTile>(p, g.out_type, vec_ok, stream); break;

@@ -1,0 +1,328 @@
+// gemm_i8_persist_kernel.hpp -- persistent variant of the int8 tile GEMM for
+// launches of several tiles per CU with an fp16 output.
+//
+// Same arithmetic, operand layout, LDS ring and MFMA schedule as
+// gemm_i8_tile_kernel (gemm_i8_kernel.hpp); what differs is how a CU moves
+// from one tile to the next.  A one-tile-per-block launch pays, per tile, a
+// workgroup launch, a cold prologue (two k-tiles fetched before any MFMA) and
+// an epilogue whose stores every CU issues at the same moment.  Here:
+//   * one block per CU walks a fixed list of tiles: the tiles of its XCD's
+//     contiguous range, round-robin over the XCD's blocks (the same L2
+//     locality as the remapped one-tile launch);
+//   * the stage ring runs across tile boundaries: the last k-steps of tile j
+//     already fetch tile j+1's first k-tiles, so the next tile starts with its
+//     operands in LDS;
+//   * the epilogue stages through its own LDS slice (32 rows per pass), not
+//     the ring, which holds the next tile's operands;
+//   * every wave issues exactly kStores buffer stores per tile (rows or
+//     columns past the matrix use an offset past the buffer, which drops the
+//     store), so the first wait of the next tile can leave those stores in
+//     flight with an exact vmcnt and they drain behind its MFMAs.
+// Results are bit-identical to gemm_i8_tile_kernel: the same k-order per tile
+// and the same epilogue arithmetic.
+#pragma once
+
+#include "gemm_i8_kernel.hpp"
+
+namespace w8a8 {
+namespace gemm {
+
+template <class C>
+struct Persist {
+    static constexpr int kRowBytes    = C::kWaveN * 2;           // one staged fp16 row
+    static constexpr int kRowChunks   = kRowBytes / 16;
+    static constexpr int kRowsPerSt   = kWave / kRowChunks;       // rows per wave store
+    static constexpr int kPassRows    = 32;                       // one MFMA tile row
+    static constexpr int kStPerPass   = kPassRows / kRowsPerSt;
+    static constexpr int kStores      = C::kTilesM * kStPerPass;  // per wave per tile
+    static constexpr int kSliceBytes  = kPassRows * kRowBytes;    // per wave
+    static constexpr int kLdsBytes    = C::kLdsBytes + C::kWaves * kSliceBytes;
+    static constexpr int kSwz         = kRowChunks < 8 ? kRowChunks : 8;
+    static_assert(kRowChunks == 4 || kRowChunks == 8 || kRowChunks == 16, "row of 4-16 chunks");
+    static_assert(kPassRows % kRowsPerSt == 0, "whole stores per pass");
+    static_assert(kLdsBytes <= 160 * 1024, "gfx950 LDS per workgroup");
+    static_assert(C::kLoads * (C::kStages - 2) + kStores < 64, "vmcnt counter range");
+};
+
+// fp16 epilogue of one wave tile through the wave's LDS slice, 32 rows per
+// pass; every lane issues exactly Persist<C>::kStores 16-byte stores.  The
+// host guarantees N % 8 == 0, ldc % 8 == 0 and a 16-byte aligned C, so an
+// 8-column chunk is either inside the matrix or entirely past it.
+template <class C>
+__device__ __forceinline__ void epilogue_f16_persist(const KArgs& p, __amdgpu_buffer_rsrc_t rc,
+                                                     uint32_t m0, uint32_t n0, int8_t* slice,
+                                                     int lane, int wm, int wn,
+                                                     const v16i (&acc)[C::kTilesM][C::kTilesN],
+                                                     const EpiScales<C>& sc)
+{
+    using P               = Persist<C>;
+    const int      chunk  = lane % P::kRowChunks;
+    const uint32_t n      = n0 + wn * C::kWaveN + chunk * 8;
+    const bool     n_in   = n < p.n;
+#pragma unroll
+    for(int i = 0; i < C::kTilesM; ++i) {
+        const int row = lane & 31;
+#pragma unroll
+        for(int j = 0; j < C::kTilesN; ++j) {
+#pragma unroll
+            for(int g = 0; g < 4; ++g) {
+                const float4 sb     = sc.sb[j][g];
+                const float  sbv[4] = {sb.x, sb.y, sb.z, sb.w};
+                uint32_t     h[4];
+#pragma unroll
+                for(int e = 0; e < 4; ++e)
+                    h[e] = float_to_half_bits_2step(((float)acc[i][j][g * 4 + e] * sc.sa[i])
+                                                    * sbv[e]);
+                const int ch   = j * 4 + g;
+                const int phys = ch ^ (row & (P::kSwz - 1));
+                v2i       pk;
+                pk.x = (int)(h[0] | (h[1] << 16));
+                pk.y = (int)(h[2] | (h[3] << 16));
+                *reinterpret_cast<v2i*>(slice + row * P::kRowBytes + phys * 16 + (lane >> 5) * 8)
+                    = pk;
+            }
+        }
+        // read back row-contiguous (a wave's LDS accesses complete in order,
+        // so the next pass's writes cannot overtake these reads)
+#pragma unroll
+        for(int q = 0; q < P::kStPerPass; ++q) {
+            const int      r    = q * P::kRowsPerSt + lane / P::kRowChunks;
+            const int      phys = chunk ^ (r & (P::kSwz - 1));
+            const v4i      v    = *reinterpret_cast<const v4i*>(slice + r * P::kRowBytes + phys * 16);
+            const uint32_t m    = m0 + wm * C::kWaveM + i * 32 + r;
+            const uint32_t off  = (m < p.m && n_in) ? (m * p.ldc + n) * 2 : kOob;
+            __builtin_amdgcn_raw_buffer_store_b128(v, rc, off, 0, 0);
+        }
+    }
+}
+
+template <class C>
+__global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_persist_kernel(KArgs p, int vec_ok)
+{
+    using P = Persist<C>;
+    static_assert(C::kStages >= 2, "ring");
+    extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
+
+    // ---- this block's tiles -------------------------------------------------
+    // XCD x (block ids x, x + 8, ...) owns logical tiles [start_x, end_x); its
+    // per = gridDim.x / 8 blocks take them round-robin.  The host launches a
+    // multiple of 8 blocks.
+    const uint32_t tiles_m = (p.m + C::kBM - 1) / C::kBM;
+    const uint32_t tiles_n = (p.n + C::kBN - 1) / C::kBN;
+    const uint32_t total   = tiles_m * tiles_n;
+    const uint32_t per     = gridDim.x / 8;
+    const uint32_t x = blockIdx.x % 8, bi = blockIdx.x / 8;
+    const uint32_t q = total / 8, rr = total % 8;
+    const uint32_t first = x * q + min(x, rr) + bi;
+    const uint32_t end   = (x + 1) * q + min(x + 1, rr);
+    const uint32_t count = first < end ? (end - first + per - 1) / per : 0;
+    if(count == 0) return; // whole block: no barrier is left waiting
+    auto tile_of = [&](uint32_t j, uint32_t& m0, uint32_t& n0) {
+        uint32_t tm, tn;
+        tile_coords<C::kGroupM>(first + j * per, tiles_m, tiles_n, tm, tn);
+        m0 = tm * C::kBM;
+        n0 = tn * C::kBN;
+    };
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int lane = threadIdx.x % kWave;
+    const int wm   = wave / C::kWavesN;
+    const int wn   = wave % C::kWavesN;
+
+    // ---- global -> LDS loads (layout as in gemm_tile) -----------------------
+    // Wave-load i of the A (B) tile fills tile rows rowA(i) (rowB(i)); the
+    // lane fetches logical chunk chunk_of(row) of its row.  Rows and chunks are
+    // recomputed from the lane where needed (a tile change, a K tail) rather
+    // than held in registers across the loop.
+    const int lrow = lane / C::kChunks;
+    auto rowA = [&](int i) { return (uint32_t)((wave * C::kLoadsA + i) * C::kRowsPerLoad + lrow); };
+    auto rowB = [&](int i) { return (uint32_t)((wave * C::kLoadsB + i) * C::kRowsPerLoad + lrow); };
+    auto chunk_of = [&](uint32_t r) {
+        return (uint32_t)((lane % C::kChunks) ^ ((r >> C::kSwzShift) & (C::kChunks - 1)));
+    };
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t*>(p.a), 0, (int)(p.m * p.lda), kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t*>(p.b), 0, (int)(p.n * p.ldb), kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+        p.c, 0, (int)(((p.m - 1) * p.ldc + p.n) * 2), kBufferFlags);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
+
+    // load cursor: the next k-step to fetch is k-tile lkt of tile lj; va / vb
+    // hold that tile's per-lane offsets (all kOob once the list is exhausted,
+    // so the ring keeps a fixed number of loads in flight to the end)
+    const uint32_t nk = (p.k + C::kBK - 1) / C::kBK;
+    uint32_t       lj = 0, lkt = 0;
+    uint32_t       va[C::kLoadsA], vb[C::kLoadsB];
+    auto set_load_tile = [&](uint32_t j) {
+        uint32_t m0 = 0, n0 = 0;
+        const bool live = j < count;
+        if(live) tile_of(j, m0, n0);
+#pragma unroll
+        for(int i = 0; i < C::kLoadsA; ++i) {
+            const uint32_t r = rowA(i);
+            va[i] = (live && m0 + r < p.m) ? (m0 + r) * p.lda + chunk_of(r) * 16 : kOob;
+        }
+#pragma unroll
+        for(int i = 0; i < C::kLoadsB; ++i) {
+            const uint32_t r = rowB(i);
+            vb[i] = (live && n0 + r < p.n) ? (n0 + r) * p.ldb + chunk_of(r) * 16 : kOob;
+        }
+    };
+    set_load_tile(0);
+    auto issue_next = [&](int stage) {
+        const uint32_t k0     = lkt * C::kBK;
+        const bool     full_k = k0 + C::kBK <= p.k; // uniform: only a K tail is partial
+        const uint32_t sbase  = lds0 + stage * C::kStageBytes + wave * (C::kLoadsA * 1024);
+        const uint32_t sbaseb = lds0 + stage * C::kStageBytes + C::kABytes
+                                + wave * (C::kLoadsB * 1024);
+#pragma unroll
+        for(int i = 0; i < C::kLoadsA; ++i) {
+            const uint32_t v = (full_k || k0 + chunk_of(rowA(i)) * 16 < p.k) ? va[i] : kOob;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ra, (lds_void_t*)(uintptr_t)(sbase + i * 1024), 16, v, k0, 0, 0);
+        }
+#pragma unroll
+        for(int i = 0; i < C::kLoadsB; ++i) {
+            const uint32_t v = (full_k || k0 + chunk_of(rowB(i)) * 16 < p.k) ? vb[i] : kOob;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rb, (lds_void_t*)(uintptr_t)(sbaseb + i * 1024), 16, v, k0, 0, 0);
+        }
+        if(++lkt == nk) {
+            lkt = 0;
+            set_load_tile(++lj);
+        }
+    };
+
+    // ---- LDS -> register fragments (as in gemm_tile) -------------------------
+    const int frow = lane & 31;
+    const int fswz = (frow >> C::kSwzShift) & (C::kChunks - 1);
+    int       offa[C::kTilesM], offb[C::kTilesN];
+#pragma unroll
+    for(int t = 0; t < C::kTilesM; ++t) offa[t] = (wm * C::kWaveM + t * 32 + frow) * C::kBK;
+#pragma unroll
+    for(int t = 0; t < C::kTilesN; ++t)
+        offb[t] = C::kABytes + (wn * C::kWaveN + t * 32 + frow) * C::kBK;
+    int cofs[C::kSubK];
+#pragma unroll
+    for(int g = 0; g < C::kSubK; ++g) cofs[g] = ((2 * g + (lane >> 5)) ^ fswz) * 16;
+
+    using FragA = v4i[C::kTilesM];
+    using FragB = v4i[C::kTilesN];
+    auto load_frags = [&](const int8_t* sbase, int g, FragA& af, FragB& bf) {
+#pragma unroll
+        for(int t = 0; t < C::kTilesM; ++t)
+            af[t] = *reinterpret_cast<const v4i*>(sbase + offa[t] + cofs[g]);
+#pragma unroll
+        for(int t = 0; t < C::kTilesN; ++t)
+            bf[t] = *reinterpret_cast<const v4i*>(sbase + offb[t] + cofs[g]);
+    };
+    v16i acc[C::kTilesM][C::kTilesN];
+    auto mfma_tile = [&](const FragA& af, const FragB& bf) {
+#pragma unroll
+        for(int i = 0; i < C::kTilesM; ++i)
+#pragma unroll
+            for(int j = 0; j < C::kTilesN; ++j)
+                acc[i][j]
+                    = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], acc[i][j], 0, 0, 0);
+    };
+    constexpr int kMfma = C::kTilesM * C::kTilesN;
+    constexpr int kDs   = C::kTilesM + C::kTilesN;
+
+    int8_t* slice = lds + C::kLdsBytes + wave * P::kSliceBytes;
+
+    // ---- prologue: the first S k-steps --------------------------------------
+#pragma unroll
+    for(int s = 0; s < C::kStages; ++s) issue_next(s);
+    wait_vmcnt<C::kLoads * (C::kStages - 1)>();
+    block_barrier();
+
+    FragA fa[2];
+    FragB fb[2];
+    load_frags(lds, 0, fa[0], fb[0]);
+
+    // ---- tiles ----------------------------------------------------------------
+    // Every k-step: MFMA groups 0..S-2 read the next group's fragments; then
+    // [this wave's reads of the stage done, the next k-step landed] barrier;
+    // the freed stage is refilled with the k-step S ahead (possibly the next
+    // tile's), and the last group reads the next k-step's group 0.
+    uint32_t step = 0;
+    // one k-step; after_epi: the previous tile's epilogue stores are the
+    // youngest memory operations and may stay in flight at the wait
+    auto kstep = [&](bool after_epi) {
+        const int8_t* sbase = lds + (step % C::kStages) * C::kStageBytes;
+#pragma unroll
+        for(int g = 0; g + 1 < C::kSubK; ++g) {
+            load_frags(sbase, g + 1, fa[(g + 1) & 1], fb[(g + 1) & 1]);
+            mfma_tile(fa[g & 1], fb[g & 1]);
+            interleave_mfma_ds<kMfma, kDs, 0>();
+        }
+        constexpr int gl = C::kSubK - 1;
+        __builtin_amdgcn_sched_barrier(0);
+        wait_lgkmcnt0();
+        if(after_epi)
+            wait_vmcnt<C::kLoads * (C::kStages - 2) + P::kStores>();
+        else
+            wait_vmcnt<C::kLoads * (C::kStages - 2)>();
+        block_barrier();
+        issue_next(step % C::kStages);
+        load_frags(lds + ((step + 1) % C::kStages) * C::kStageBytes, 0, fa[(gl + 1) & 1],
+                   fb[(gl + 1) & 1]);
+        mfma_tile(fa[gl & 1], fb[gl & 1]);
+        interleave_mfma_vmem_ds<kMfma, C::kLoads, kDs, 1>();
+        ++step;
+    };
+    for(uint32_t j = 0; j < count; ++j) {
+        uint32_t m0, n0;
+        tile_of(j, m0, n0);
+#pragma unroll
+        for(int i = 0; i < C::kTilesM; ++i)
+#pragma unroll
+            for(int jj = 0; jj < C::kTilesN; ++jj) acc[i][jj] = v16i{0};
+        for(uint32_t kt = 0; kt + 1 < nk; ++kt) kstep(kt == 0 && j > 0);
+        // last k-step peeled: the epilogue's scales load while it runs
+        EpiScales<C> sc;
+        sc.load(p, m0, n0, wm, wn, lane, vec_ok);
+        kstep(nk == 1 && j > 0);
+        __builtin_amdgcn_sched_barrier(0);
+        epilogue_f16_persist<C>(p, rc, m0, n0, slice, lane, wm, wn, acc, sc);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    wait_vmcnt<0>(); // no global->LDS write may outlive the workgroup's LDS
+}
+
+template <class C>
+void raise_persist_lds_once()
+{
+    static std::once_flag once;
+    std::call_once(once, [] {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_i8_persist_kernel<C>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  Persist<C>::kLdsBytes);
+        (void)hipGetLastError();
+    });
+}
+
+// Whether the persistent kernel applies: fp16 output, several tiles per CU
+// (blocks = CUs, a multiple of 8), 8-column chunks that never straddle N,
+// 16-byte aligned rows of C, and C within the 32-bit buffer range.
+template <class C>
+bool persist_ok(const KArgs& p, int vec_ok, uint32_t cus)
+{
+    const uint64_t tiles = (uint64_t)((p.m + C::kBM - 1) / C::kBM) * ((p.n + C::kBN - 1) / C::kBN);
+    return vec_ok && cus >= 8 && cus % 8 == 0 && tiles >= 2ull * cus && p.n % 8 == 0
+           && p.ldc % 8 == 0 && reinterpret_cast<uintptr_t>(p.c) % 16 == 0
+           && ((uint64_t)(p.m - 1) * p.ldc + p.n) * 2 < 0x80000000ull;
+}
+
+template <class C>
+hipError_t launch_cfg_persist(const KArgs& p, int vec_ok, uint32_t cus, hipStream_t stream)
+{
+    raise_persist_lds_once<C>();
+    hipLaunchKernelGGL((gemm_i8_persist_kernel<C>), dim3(cus), dim3(C::kThreads),
+                       Persist<C>::kLdsBytes, stream, p, vec_ok);
+    return hipGetLastError();
+}
+
+} // namespace gemm
+} // namespace w8a8

@@ -67,6 +67,28 @@ def test_tile_configs_exact(w8a8, gpu, m, n, k):
     assert_f16_bitexact(host(c), O.dequant_f16(acc, sa, sb))
 
 
+# Launches of at least two 256 x 256 tiles per CU with K <= 4096 and an fp16
+# output run the persistent kernel: one block per CU walks its tiles, the
+# stage ring runs across tile boundaries and each tile's epilogue stores stay
+# in flight into the next tile.  Tile counts are for a 256-CU device.
+PERSIST_SHAPES = [
+    (4100, 8200, 160),   # 561 tiles, ragged edges, 2 k-tiles (K tail)
+    (8192, 8192, 128),   # 1024 tiles, one k-tile per tile
+    (4096, 8200, 2000),  # 528 tiles, 16 k-tiles (K tail)
+]
+
+
+@pytest.mark.parametrize("m,n,k", PERSIST_SHAPES)
+def test_persistent_tiles_exact(w8a8, gpu, m, n, k):
+    a, b, sa, sb = inputs(m, n, k, 7 * m + n + 3 * k)
+    ad, bd = dev(a, gpu), dev(b, gpu)
+    acc = O.gemm_i32(a, b)
+    c = w8a8.gemm(ad, bd, dev(sa, gpu), dev(sb, gpu))
+    assert_f16_bitexact(host(c), O.dequant_f16(acc, sa, sb))
+    c1 = w8a8.gemm(ad, bd, tensor_scale_a=0.5, tensor_scale_b=0.25)
+    assert_f16_bitexact(host(c1), O.dequant_f16(acc, tsa=0.5, tsb=0.25))
+
+
 # K split (workspace given) of launches whose 128 x 128 tiles fill at most
 # half of the 256 CUs: tiles x pieces
 SPLIT_SHAPES = [
