@@ -272,28 +272,45 @@ def bench_decode(torch, w8a8, dev, gen, iters=20):
                         "(two weight copies per shape alternate: MALL-cold)", "layers": results}
 
 
-TRAFFIC_PROFILE = ROOT / "profiles" / "gemm_i8_tile_kernel__cfg3_llama3_8b_m8192_and_cfg2.md"
+TRAFFIC_PROFILE = ROOT / "profiles" / "gemm_i8_persist_and_tile_kernels__cfg3_llama3_8b_and_cfg2.md"
+TRAFFIC_SECTION = "## HBM-side traffic of the cfg3 projections"
 
 
-def profiled_traffic(projs):
+def projection_kernel(p, cus):
+    """Which 256 x 256 kernel the library runs for an fp16 projection GEMM:
+    the persistent kernel when there are at least two tiles per CU and at
+    most 32 k-tiles of 128 (persist_pays, csrc/gemm_i8.hip), otherwise the
+    one-tile-per-block kernel."""
+    tiles = -(-p["m"] // 256) * -(-p["n"] // 256)
+    return "persist" if tiles >= 2 * cus and -(-p["k"] // 128) <= 32 else "tile"
+
+
+def profiled_traffic(projs, cus):
     """HBM-side bytes per launch of the projection GEMMs, averaged like
     `achieved`, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
-    (scaled by the calibration copy); None when the profile does not cover
-    these grids."""
+    of a bench run without the extras (scaled by the calibration copy).  The
+    persistent kernel launches one block per CU for every projection it runs,
+    so its row is the average over those launches; tile-kernel rows are keyed
+    by their grid.  None when the profile does not cover these launches."""
     import re
     if not TRAFFIC_PROFILE.exists():
         return None, None
-    table = {}
+    table, on = {}, False
     for line in TRAFFIC_PROFILE.read_text().splitlines():
-        mt = re.match(r"traffic \S*gemm_i8_tile_kernel<\S*Cfg<256,256,\S* grid=(\d+) .* bytes=(\d+)", line)
-        if mt:
-            table[int(mt.group(1))] = int(mt.group(2))
+        if line.startswith("## "):
+            on = line.startswith(TRAFFIC_SECTION)
+            continue
+        mt = re.match(r"traffic \S*gemm_i8_(tile|persist)_kernel<\S*Cfg<256,256,\S* grid=(\d+) .* bytes=(\d+)",
+                      line)
+        if on and mt:
+            table[(mt.group(1), int(mt.group(2)))] = int(mt.group(3))
     per = []
     for p in projs:
-        grid = -(-p["m"] // 256) * -(-p["n"] // 256) * 512  # 256x256 tiles, 512 threads
-        if grid not in table:
+        kind = projection_kernel(p, cus)
+        grid = cus * 512 if kind == "persist" else -(-p["m"] // 256) * -(-p["n"] // 256) * 512
+        if (kind, grid) not in table:
             return None, None
-        per.append(table[grid])
+        per.append(table[(kind, grid)])
     return sum(per) / len(per), per
 
 
@@ -499,7 +516,9 @@ def main(argv=None) -> int:
                          "gemm_TOPS": ops / (gm * 1e-3) / 1e12})
     log(json.dumps(per_proj))
 
-    traffic, traffic_per = profiled_traffic(projs)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    traffic, traffic_per = profiled_traffic(projs, cus)
+    kinds = [projection_kernel(p, cus) for p in projs]
     algo_bytes = [p["m"] * p["k"] + p["n"] * p["k"] + 2 * p["m"] * p["n"] + 4 * (p["m"] + p["n"])
                   for p in projs]
     roofline = {"bound": "mfma", "achieved": gemm_tops, "peak": PEAK_INT8_OPS / 1e12,
@@ -509,8 +528,16 @@ def main(argv=None) -> int:
                 "traffic_source": (f"{TRAFFIC_PROFILE.relative_to(ROOT)} (rocprofv3 FETCH_SIZE x2.0 "
                                    "+ WRITE_SIZE x1.0, calibrated on a 2^30-byte copy; "
                                    "FETCH_SIZE includes MALL hits)") if traffic else None,
-                "kernel": "gemm_i8_tile_kernel<Cfg<256,256,128,2,2,4,4>, F16>",
+                "kernel": " + ".join(
+                    f"{'gemm_i8_persist_kernel<Cfg<256,256,128,2,2,4,4>>' if kd == 'persist' else 'gemm_i8_tile_kernel<Cfg<256,256,128,2,2,4,4>, F16>'} ({', '.join(nm for (nm, _, _), k2 in zip(LLAMA3_8B, kinds) if k2 == kd)})"
+                    for kd in dict.fromkeys(kinds)),
+                "traffic_note": "per-projection entries of the persistent kernel are its average "
+                                "over the projections it runs (one block per CU each)",
                 "avg_launch_us": gemm_avg_us,
+                "avg_launch_us_per_kernel": {
+                    kd: sum(g for g, k2 in zip(g_ms, kinds) if k2 == kd) * 1e3
+                        / sum(1 for k2 in kinds if k2 == kd)
+                    for kd in dict.fromkeys(kinds)},
                 "note": "int8 ops (2*M*N*K) per launch / average launch duration over the four "
                         "projection GEMMs; peak = 5.0 POP/s dense int8"}
 
