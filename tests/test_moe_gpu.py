@@ -257,6 +257,38 @@ def test_moe_gemm_tail_split_exact(w8a8, gpu, counts, k, n):
         assert_f16_bitexact(cf[pick], O.dequant_f16(acc, sa[pick], sw[x]))
 
 
+# About 1000 tiles of 256 rows over four experts (four rounds of the CUs),
+# fp16 and int32, with the tail split (workspace) and without.
+def test_moe_gemm_many_tiles_exact(w8a8, gpu):
+    import torch
+    counts, k, n, unit = [2000, 1500, 2500, 1800], 1024, 8192, 32
+    count = np.array(counts, np.int32)
+    padded = -(-count // unit) * unit
+    start = np.concatenate([[0], np.cumsum(padded)]).astype(np.int32)
+    rows, e = int(start[-1]), len(counts)
+    assert _tile_rows(counts, rows)[1] == 256
+    seed = 4242
+    a = G.int8(seed, G.TID_A, (rows, k))
+    w = G.int8(seed, G.TID_B, (e, n, k))
+    sa = G.uniform(seed, G.TID_SA, (rows,), 1e-3, 1e-2)
+    sw = G.uniform(seed, G.TID_SB, (e, n), 1e-3, 1e-2)
+    args = (dev(a, gpu), dev(w, gpu), dev(start, gpu), dev(count, gpu))
+    kw = dict(scale_a=dev(sa, gpu), scale_w=dev(sw, gpu))
+    ws = torch.empty(w8a8.moe_gemm_workspace_size(e, rows, n, k), dtype=torch.uint8, device=gpu)
+    ci = host(w8a8.moe_gemm(*args, out_dtype=torch.int32, workspace=None))
+    cf = host(w8a8.moe_gemm(*args, workspace=ws, **kw))
+    cf0 = host(w8a8.moe_gemm(*args, workspace=None, **kw))
+    for x in range(e):
+        r0, r1 = start[x], start[x] + count[x]
+        assert_f16_bitexact(cf[r0:r1], cf0[r0:r1])
+        assert_f16_bitexact(cf[r0:r1], O.dequant_f16(ci[r0:r1], sa[r0:r1], sw[x]))
+        pick = np.unique(np.concatenate([np.arange(r0, r0 + 8), np.arange(r1 - 40, r1),
+                                         np.random.default_rng(x).integers(r0, r1, 24)]))
+        acc = O.gemm_i32(a[pick], w[x])
+        assert_i32_equal(ci[pick], acc)
+        assert_f16_bitexact(cf[pick], O.dequant_f16(acc, sa[pick], sw[x]))
+
+
 def test_moe_gemm_leaves_padding_rows(w8a8, gpu):
     import torch
     t, k, e, h, n, unit = 100, 2, 4, 128, 64, 32
