@@ -336,6 +336,8 @@ hipError_t launch_stream_norm(const NormRows& p, hipStream_t stream)
 {
     constexpr int kGroups = THREADS / kWave / WPR;
     const size_t  lds     = (size_t)CPL * 512 * WPR * sizeof(float) * (QUANT ? 2 : 1);
+    // one row group must span the whole row
+    if((uint64_t)CPL * 512 * WPR < p.n) return hipErrorInvalidValue;
     const void*   kernel  = reinterpret_cast<const void*>(
         rmsq_stream_kernel<CPL, WPR, THREADS, BPC, RES, YOUT, QUANT>);
     static int    max_blocks = [] {
