@@ -437,6 +437,9 @@ def main(argv=None) -> int:
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--settle-ms", type=float, default=200.0,
+                    help="untimed steps for at least this long before the warmup steps "
+                         "(the GPU's clocks ramp up from idle)")
     ap.add_argument("--m", type=int, default=8192, help="tokens per projection")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=256)
@@ -476,10 +479,21 @@ def main(argv=None) -> int:
             if events is not None:
                 events[i][2].record()
 
+    # The GPU raises its clocks from idle over some tens of ms: a cold start's
+    # first 10 steps take ~2.1 ms each against ~1.58 ms once settled (50 ms
+    # in).  The step runs untimed for at least --settle-ms before the W
+    # warmup steps, so the timed steps see the steady state a continuously
+    # loaded GPU runs at.
+    t_settle = time.perf_counter() + args.settle_ms / 1e3
+    settle_steps = 0
+    while time.perf_counter() < t_settle:
+        step()
+        torch.cuda.synchronize()
+        settle_steps += 1
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    log("warmup done")
+    log(f"settle ({settle_steps} steps, {args.settle_ms:.0f} ms) and warmup done")
 
     # timed region: exactly `steps` steps, synchronized on both sides
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -579,6 +593,7 @@ def main(argv=None) -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_ms": args.settle_ms,
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",
