@@ -27,6 +27,11 @@
 namespace w8a8 {
 namespace gemm {
 
+// Cache-policy operand of the buffer builtins: the NT (non-temporal) bit.
+constexpr int kCpolNonTemporal = 2;
+// MI355X's last-level cache (MALL, AMD Infinity Cache): 256 MB.
+constexpr uint64_t kMallBytes = 256ull << 20;
+
 template <class C>
 struct Persist {
     static constexpr int kRowBytes    = C::kWaveN * 2;           // one staged fp16 row
@@ -48,12 +53,16 @@ struct Persist {
 // pass; every lane issues exactly Persist<C>::kStores 16-byte stores.  The
 // host guarantees N % 8 == 0, ldc % 8 == 0 and a 16-byte aligned C, so an
 // 8-column chunk is either inside the matrix or entirely past it.
+// nt: non-temporal stores, for outputs larger than the MALL (they cannot
+// stay resident, and write-allocating them leaves the MALL full of dirty
+// lines that the next kernel pays to write back: the quantizer that follows
+// the 470 MB gate_up output of cfg3 runs 62 instead of 89 us).
 template <class C>
 __device__ __forceinline__ void epilogue_f16_persist(const KArgs& p, __amdgpu_buffer_rsrc_t rc,
                                                      uint32_t m0, uint32_t n0, int8_t* slice,
                                                      int lane, int wm, int wn,
                                                      const v16i (&acc)[C::kTilesM][C::kTilesN],
-                                                     const EpiScales<C>& sc)
+                                                     const EpiScales<C>& sc, int nt)
 {
     using P               = Persist<C>;
     const int      chunk  = lane % P::kRowChunks;
@@ -91,13 +100,16 @@ __device__ __forceinline__ void epilogue_f16_persist(const KArgs& p, __amdgpu_bu
             const v4i      v    = *reinterpret_cast<const v4i*>(slice + r * P::kRowBytes + phys * 16);
             const uint32_t m    = m0 + wm * C::kWaveM + i * 32 + r;
             const uint32_t off  = (m < p.m && n_in) ? (m * p.ldc + n) * 2 : kOob;
-            __builtin_amdgcn_raw_buffer_store_b128(v, rc, off, 0, 0);
+            if(nt)
+                __builtin_amdgcn_raw_buffer_store_b128(v, rc, off, 0, kCpolNonTemporal);
+            else
+                __builtin_amdgcn_raw_buffer_store_b128(v, rc, off, 0, 0);
         }
     }
 }
 
 template <class C>
-__global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_persist_kernel(KArgs p, int vec_ok)
+__global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_persist_kernel(KArgs p, int vec_ok, int nt)
 {
     using P = Persist<C>;
     static_assert(C::kStages >= 2, "ring");
@@ -285,7 +297,7 @@ __global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_persist_kernel(KArgs p
         sc.load(p, m0, n0, wm, wn, lane, vec_ok);
         kstep(nk == 1 && j > 0);
         __builtin_amdgcn_sched_barrier(0);
-        epilogue_f16_persist<C>(p, rc, m0, n0, slice, lane, wm, wn, acc, sc);
+        epilogue_f16_persist<C>(p, rc, m0, n0, slice, lane, wm, wn, acc, sc, nt);
         __builtin_amdgcn_sched_barrier(0);
     }
     wait_vmcnt<0>(); // no global->LDS write may outlive the workgroup's LDS
@@ -319,8 +331,9 @@ template <class C>
 hipError_t launch_cfg_persist(const KArgs& p, int vec_ok, uint32_t cus, hipStream_t stream)
 {
     raise_persist_lds_once<C>();
+    const int nt = (uint64_t)p.m * p.ldc * 2 > kMallBytes;
     hipLaunchKernelGGL((gemm_i8_persist_kernel<C>), dim3(cus), dim3(C::kThreads),
-                       Persist<C>::kLdsBytes, stream, p, vec_ok);
+                       Persist<C>::kLdsBytes, stream, p, vec_ok, nt);
     return hipGetLastError();
 }
 

@@ -75,6 +75,7 @@ PERSIST_SHAPES = [
     (4100, 8200, 160),   # 561 tiles, ragged edges, 2 k-tiles (K tail)
     (8192, 8192, 128),   # 1024 tiles, one k-tile per tile
     (4096, 8200, 2000),  # 528 tiles, 16 k-tiles (K tail)
+    (8192, 16400, 128),  # 2080 tiles, a 269 MB output (over the 256 MB MALL): non-temporal stores
 ]
 
 
