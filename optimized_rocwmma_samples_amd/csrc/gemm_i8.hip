@@ -40,7 +40,7 @@ using GemmPacked128 = gemm::PbCfg<128, 4, 2, 4>;
 using GemmPacked64  = gemm::PbCfg<64, 4, 2, 4>;
 // Decode configurations: <32-row m tiles, 32-row weight tiles, waves, ring>.
 using DecSmall   = gemm::DecCfg<1, 1, 4, 3>; // m <= 32, or <= 16 packed
-using DecSmallW  = gemm::DecCfg<1, 2, 8, 3>; // packed, 16 < m <= 32, many slabs
+using DecSmallW  = gemm::DecCfg<1, 2, 8, 3>; // packed, 8 <= m <= 32, many slabs
 using DecMid     = gemm::DecCfg<2, 1, 8, 3>; // 32 < m <= 64
 using DecMidW    = gemm::DecCfg<2, 2, 8, 2>; // packed, 32 < m <= 64, many slabs
 // packed, 32 < m <= 64 with a split-K workspace: 8 half slabs per block share
@@ -313,7 +313,9 @@ hipError_t launch_gemm_decode(const GemmArgs& g, bool packed, void* ws, size_t w
             }
         }
         if(packed) {
-            if(g.m <= 16 || (g.m <= 32 && !wide))
+            // 8 <= m <= 16 on many slabs: 64 weight rows per block halve the
+            // re-reads of the activation rows (M=16 N=28672: 54 -> 52 us)
+            if((g.m <= 16 && (!wide || g.m < 8)) || (g.m <= 32 && !wide))
                 e = gemm::launch_decode<DecSmall, true>(p, g.out_type, vec_ok, stream);
             else if(g.m <= 32)
                 e = gemm::launch_decode<DecSmallW, true>(p, g.out_type, vec_ok, stream);
