@@ -395,6 +395,24 @@ int w8a8_fused_sq_gemm_packed(const void* x, const float* smooth_scale, const in
     if(reinterpret_cast<uintptr_t>(q) % 16 != 0 || k % 16 != 0)
         return fail(W8A8_ERROR_NOT_SUPPORTED,
                     "w8a8_fused_sq_gemm_packed: needs a 16-byte aligned q and k %% 16 == 0 (k=%u)", k);
+    // a few rows: one kernel quantizes them per block and streams the weights
+    if(w8a8::decode_fuse_ok(m, k) && reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 8 == 0
+       && reinterpret_cast<uintptr_t>(smooth_scale) % 16 == 0) {
+        int vrc = validate_gemm("w8a8_fused_sq_gemm_packed", m, n, k, q, w_packed, c, k, k, ldc,
+                                W8A8_OUT_F16, W8A8_LAYOUT_A_ROW_B_NK);
+        if(vrc != W8A8_SUCCESS) return vrc;
+        if(reinterpret_cast<uintptr_t>(w_packed) % 16 != 0)
+            return fail(W8A8_ERROR_INVALID_VALUE,
+                        "w8a8_fused_sq_gemm_packed: w_packed must be 16-byte aligned");
+        const w8a8::GemmArgs g{m, n, k, q, w_packed, c, k, k, ldc, row_scale, scale_w,
+                               1.f, 1.f, W8A8_OUT_F16};
+        if(w8a8::gemm_packed_ok(g)) {
+            const w8a8::FuseArgs f{static_cast<const uint16_t*>(x), smooth_scale, q, row_scale,
+                                   ldx, 127.f};
+            return hip_status(w8a8::launch_gemm_decode_fused(g, f, stream),
+                              "w8a8_fused_sq_gemm_packed");
+        }
+    }
     int rc = w8a8_smoothquant(x, smooth_scale, q, row_scale, m, k, 127.f, ldx, k, stream);
     if(rc != W8A8_SUCCESS) return rc;
     return w8a8_gemm_packed(m, n, k, q, w_packed, c, k, ldc, row_scale, scale_w, 1.f, 1.f,

@@ -292,6 +292,33 @@ bool gemm_decode_ok(const GemmArgs& g)
     return g.m <= kDecodeMaxM && (uint64_t)(g.m - 1) * g.lda + g.k < 0x7FFFFFFFull;
 }
 
+// Rows quantized inside the decode kernel (w8a8_fused_sq_gemm_packed at
+// m <= kFuseRows and k <= kFuseMaxK): every block quantizes whole rows before
+// its A-dependent MFMAs, a prologue that grows with K.  It pays where it is
+// short and blocks share a CU: M = 1, W1 [28672, 8192] 49.5 -> 47.2 us; at
+// W2 [8192, 28672] (one block per CU, 28672-element rows) 48.9 -> 54.5 us,
+// so longer rows keep the separate quantizer.
+constexpr uint32_t kFuseMaxK = 8192;
+bool decode_fuse_ok(uint32_t m, uint32_t k)
+{
+    const uint64_t ka = (uint64_t)gemm::packed_ktiles(k) * gemm::kPackK;
+    return m >= 1 && m <= gemm::kFuseRows && k <= kFuseMaxK
+           && DecSmall::kLdsBytes + m * ka <= 160 * 1024;
+}
+
+hipError_t launch_gemm_decode_fused(const GemmArgs& g, const FuseArgs& f, hipStream_t stream)
+{
+    const gemm::FuseQ fq{f.x, f.s, f.q, f.r, f.ldx, gemm::packed_ktiles(g.k) * gemm::kPackK, f.qmax};
+    const int      vec_ok = out_vec_ok(g);
+    const uint32_t step   = weight_panel_rows(g, true);
+    for(uint32_t n0 = 0; n0 < g.n; n0 += step) {
+        const KArgs      p = n_panel(g, n0, std::min(step, g.n - n0), true);
+        const hipError_t e = gemm::launch_decode_fused<DecSmall>(p, fq, vec_ok, stream);
+        if(e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 hipError_t launch_gemm_decode(const GemmArgs& g, bool packed, void* ws, size_t ws_bytes,
                               hipStream_t stream)
 {

@@ -44,10 +44,105 @@ struct DecCfg {
     static_assert(kLdsBytes <= 128 * 1024, "partials must fit in LDS");
 };
 
+// SmoothQuant of the activation rows folded into the decode kernel (m <=
+// kFuseRows, packed weights): every block quantizes the rows itself into LDS
+// (a few KiB, read from L2 while the block's first weight fragments are in
+// flight) and block (0, 0) also writes q and the row scales.  Same
+// per-element operations as the quantizer kernels (rocwmma_smoothquant.cpp:
+// 58-122): p = float(x) * s; r = max|p| / qmax; inv = r > 0 ? 1 / r : 0;
+// q = int8(clamp(rint(p * inv), -qmax, qmax)); the maximum does not depend
+// on the order of the reduction, so q and r are bit-identical.
+constexpr uint32_t kFuseRows = 4;
+struct FuseQ {
+    const uint16_t* x;    // [m, ldx] fp16 activations (16-byte aligned rows)
+    const float*    s;    // [k] smoothing scale (16-byte aligned)
+    int8_t*         q;    // [m, k] quantized rows out
+    float*          r;    // [m] row scales out
+    uint32_t        ldx;  // ldx % 8 == 0
+    uint32_t        ka;   // LDS row pitch: k rounded up to kPackK (zero padded)
+    float           qmax;
+};
+
+// Block-wide: quantize the m (<= kFuseRows) rows into qa (pitch fq.ka) and
+// return their row scales in rs.  red: LDS scratch of KW * kFuseRows floats.
+template <class C>
+__device__ __forceinline__ void fuse_quantize(const FuseQ& fq, uint32_t m, uint32_t k, int8_t* qa,
+                                              float* red, float (&rs)[kFuseRows])
+{
+    const uint32_t tid    = threadIdx.x;
+    const int      lane   = tid % kWave;
+    const int      wave   = tid / kWave;
+    const uint32_t chunks = k / 8;
+    auto smoothed = [&](uint32_t r, uint32_t c, float (&v)[8]) {
+        const v4i    raw = *reinterpret_cast<const v4i*>(fq.x + (size_t)r * fq.ldx + c * 8);
+        const float4 s0  = *reinterpret_cast<const float4*>(fq.s + c * 8);
+        const float4 s1  = *reinterpret_cast<const float4*>(fq.s + c * 8 + 4);
+        v[0] = half_bits_to_float((uint32_t)raw.x & 0xFFFFu) * s0.x;
+        v[1] = half_bits_to_float((uint32_t)raw.x >> 16) * s0.y;
+        v[2] = half_bits_to_float((uint32_t)raw.y & 0xFFFFu) * s0.z;
+        v[3] = half_bits_to_float((uint32_t)raw.y >> 16) * s0.w;
+        v[4] = half_bits_to_float((uint32_t)raw.z & 0xFFFFu) * s1.x;
+        v[5] = half_bits_to_float((uint32_t)raw.z >> 16) * s1.y;
+        v[6] = half_bits_to_float((uint32_t)raw.w & 0xFFFFu) * s1.z;
+        v[7] = half_bits_to_float((uint32_t)raw.w >> 16) * s1.w;
+    };
+    float amax[kFuseRows];
+#pragma unroll
+    for(uint32_t r = 0; r < kFuseRows; ++r) amax[r] = 0.f;
+    for(uint32_t c = tid; c < chunks; c += C::kThreads) {
+#pragma unroll
+        for(uint32_t r = 0; r < kFuseRows; ++r) {
+            if(r < m) {
+                float v[8];
+                smoothed(r, c, v);
+#pragma unroll
+                for(int e = 0; e < 8; ++e) amax[r] = fmaxf(amax[r], fabsf(v[e]));
+            }
+        }
+    }
+#pragma unroll
+    for(uint32_t r = 0; r < kFuseRows; ++r) {
+        amax[r] = wave_max(amax[r]);
+        if(lane == 0) red[wave * kFuseRows + r] = amax[r];
+    }
+    __syncthreads();
+    float inv[kFuseRows];
+    const bool first_block = blockIdx.x == 0 && blockIdx.y == 0;
+#pragma unroll
+    for(uint32_t r = 0; r < kFuseRows; ++r) {
+        float a = 0.f;
+#pragma unroll
+        for(int w = 0; w < C::kKW; ++w) a = fmaxf(a, red[w * kFuseRows + r]);
+        rs[r]  = a / fq.qmax;
+        inv[r] = rs[r] > 0.f ? 1.f / rs[r] : 0.f;
+        if(first_block && tid == r && r < m) fq.r[r] = rs[r];
+    }
+    // rows of kPackK-padded chunks; the padding is zero
+    for(uint32_t c = tid; c < fq.ka / 8; c += C::kThreads) {
+#pragma unroll
+        for(uint32_t r = 0; r < kFuseRows; ++r) {
+            if(r < m) {
+                v2i pk = {0, 0};
+                if(c < chunks) {
+                    float v[8];
+                    smoothed(r, c, v);
+                    pk.x = (int)pack4_i8(quant_i8(v[0], inv[r], fq.qmax), quant_i8(v[1], inv[r], fq.qmax),
+                                         quant_i8(v[2], inv[r], fq.qmax), quant_i8(v[3], inv[r], fq.qmax));
+                    pk.y = (int)pack4_i8(quant_i8(v[4], inv[r], fq.qmax), quant_i8(v[5], inv[r], fq.qmax),
+                                         quant_i8(v[6], inv[r], fq.qmax), quant_i8(v[7], inv[r], fq.qmax));
+                    if(first_block) *reinterpret_cast<v2i*>(fq.q + (size_t)r * k + c * 8) = pk;
+                }
+                *reinterpret_cast<v2i*>(qa + r * fq.ka + c * 8) = pk;
+            }
+        }
+    }
+    __syncthreads();
+}
+
 // PACKED: p.b is the packed weight buffer (p.ldb unused).  Otherwise p.b is
 // W [n, ldb] with K contiguous.
-template <class C, int OUT, bool PACKED>
-__global__ void __launch_bounds__(C::kThreads) gemm_i8_decode_kernel(KArgs p, int vec_ok)
+template <class C, int OUT, bool PACKED, bool FUSE = false>
+__global__ void __launch_bounds__(C::kThreads) gemm_i8_decode_kernel(KArgs p, int vec_ok, FuseQ fq)
 {
     extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
 
@@ -93,7 +188,9 @@ __global__ void __launch_bounds__(C::kThreads) gemm_i8_decode_kernel(KArgs p, in
     using ATile = v4i[C::kMT * 4];
     BTile bq[C::kRing];
     ATile aq[C::kRing];
-    auto issue = [&](int slot, uint32_t kt) {
+    // FUSE: the quantized rows in LDS after the partials area, pitch fq.ka
+    int8_t* qa = lds + C::kLdsBytes;
+    auto issue_b = [&](int slot, uint32_t kt) {
         // k-tiles outside [kt0, kt1) read at kOob: zeros, no memory traffic
         const bool live = kt < kt1;
         if constexpr(PACKED) {
@@ -115,6 +212,24 @@ __global__ void __launch_bounds__(C::kThreads) gemm_i8_decode_kernel(KArgs p, in
                 }
             }
         }
+    };
+    auto issue_a = [&](int slot, uint32_t kt) {
+        const bool live = kt < kt1;
+        if constexpr(FUSE) {
+#pragma unroll
+            for(int i = 0; i < C::kMT; ++i) {
+                const uint32_t row = mbase + i * 32 + (lane & 31);
+                const bool     use = live && row < p.m;
+                // the address stays inside the quantized rows whatever the lane
+                const int8_t*  src = qa + (use ? row * fq.ka + kt * kPackK : 0u) + (lane >> 5) * 16;
+#pragma unroll
+                for(int g = 0; g < 4; ++g) {
+                    const v4i v         = *reinterpret_cast<const v4i*>(src + g * 32);
+                    aq[slot][i * 4 + g] = use ? v : v4i{0};
+                }
+            }
+            return;
+        }
 #pragma unroll
         for(int i = 0; i < C::kMT; ++i) {
             // The k offset goes into voffset so the range check sees it: the
@@ -126,6 +241,10 @@ __global__ void __launch_bounds__(C::kThreads) gemm_i8_decode_kernel(KArgs p, in
             for(int g = 0; g < 4; ++g)
                 aq[slot][i * 4 + g] = __builtin_amdgcn_raw_buffer_load_b128(ra, v + g * 32, 0, 0);
         }
+    };
+    auto issue = [&](int slot, uint32_t kt) {
+        issue_b(slot, kt);
+        issue_a(slot, kt);
     };
 
     v16i acc[C::kMT][C::kNT];
@@ -146,8 +265,18 @@ __global__ void __launch_bounds__(C::kThreads) gemm_i8_decode_kernel(KArgs p, in
     };
 
     // ---- stream the wave's k range with a RING-deep register ring ----------
+    float rs[kFuseRows];
+    if constexpr(FUSE) {
+        // the first weight fragments load while the block quantizes A
 #pragma unroll
-    for(int d = 0; d + 1 < C::kRing; ++d) issue(d, kt0 + d);
+        for(int d = 0; d + 1 < C::kRing; ++d) issue_b(d, kt0 + d);
+        fuse_quantize<C>(fq, p.m, p.k, qa, reinterpret_cast<float*>(lds), rs);
+#pragma unroll
+        for(int d = 0; d + 1 < C::kRing; ++d) issue_a(d, kt0 + d);
+    } else {
+#pragma unroll
+        for(int d = 0; d + 1 < C::kRing; ++d) issue(d, kt0 + d);
+    }
     uint32_t kt = kt0;
     if constexpr(C::kRing == 3) {
         for(; kt + 3 <= kt1; kt += 3) {
@@ -200,7 +329,14 @@ __global__ void __launch_bounds__(C::kThreads) gemm_i8_decode_kernel(KArgs p, in
         const uint32_t m  = mbase + i * 32 + (lane & 31);
         const uint32_t n  = nbase + j * 32 + q * 8 + (lane >> 5) * 4;
         float          sa = p.tsa;
-        if(OUT == W8A8_OUT_F16 && p.sa != nullptr && m < p.m) sa = p.sa[m];
+        if constexpr(FUSE) {
+            // this block's own row scales (block (0, 0) may still be writing p.sa)
+#pragma unroll
+            for(uint32_t r = 0; r < kFuseRows; ++r)
+                if(m == r) sa = rs[r];
+        } else if(OUT == W8A8_OUT_F16 && p.sa != nullptr && m < p.m) {
+            sa = p.sa[m];
+        }
         float4 sb = make_float4(p.tsb, p.tsb, p.tsb, p.tsb);
         if(OUT == W8A8_OUT_F16 && p.sb != nullptr) {
             if(vec_ok && n + 4 <= p.n)
@@ -238,7 +374,27 @@ hipError_t launch_decode(const KArgs& p, int out_type, int vec_ok, hipStream_t s
     }
     const dim3 grid((p.n + C::kNT * 32 - 1) / (C::kNT * 32), (p.m + C::kMT * 32 - 1) / (C::kMT * 32));
     hipLaunchKernelGGL(kern[out_type == W8A8_OUT_I32 ? 0 : 1], grid, dim3(C::kThreads),
-                       C::kLdsBytes, stream, p, vec_ok);
+                       C::kLdsBytes, stream, p, vec_ok, FuseQ{});
+    return hipGetLastError();
+}
+
+// The decode kernel with the activation quantization folded in (packed
+// weights, fp16 output, p.m <= kFuseRows, C::kMT == 1).  p.sa must be fq.r.
+// The host checks C::kLdsBytes + p.m * fq.ka <= 160 KiB.
+template <class C>
+hipError_t launch_decode_fused(const KArgs& p, const FuseQ& fq, int vec_ok, hipStream_t stream)
+{
+    static_assert(C::kMT == 1, "one 32-row m tile holds the fused rows");
+    const void* kern = reinterpret_cast<const void*>(
+        &gemm_i8_decode_kernel<C, W8A8_OUT_F16, true, true>);
+    static std::once_flag once;
+    std::call_once(once, [&] {
+        (void)hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        (void)hipGetLastError();
+    });
+    const dim3 grid((p.n + C::kNT * 32 - 1) / (C::kNT * 32), 1);
+    hipLaunchKernelGGL((gemm_i8_decode_kernel<C, W8A8_OUT_F16, true, true>), grid,
+                       dim3(C::kThreads), C::kLdsBytes + p.m * fq.ka, stream, p, vec_ok, fq);
     return hipGetLastError();
 }
 

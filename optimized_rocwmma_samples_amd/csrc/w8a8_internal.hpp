@@ -73,6 +73,20 @@ size_t     gemm_nk_workspace_bytes(const GemmArgs& g);
 // waves of a block.  `packed`: g.b holds packed weights (g.ldb unused).
 constexpr uint32_t kDecodeMaxM = 64;
 bool       gemm_decode_ok(const GemmArgs& g);
+// The decode kernel with the activation quantization folded in (packed
+// weights, fp16 output, m <= 4 when decode_fuse_ok): x fp16 [m, ldx] (16-byte
+// aligned rows), s [k] (16-byte aligned); q [m, k] and r [m] are written as
+// by the quantizer, and g.a = q, g.scale_a = r.
+struct FuseArgs {
+    const uint16_t* x;
+    const float*    s;
+    int8_t*         q;
+    float*          r;
+    uint32_t        ldx;
+    float           qmax;
+};
+bool       decode_fuse_ok(uint32_t m, uint32_t k);
+hipError_t launch_gemm_decode_fused(const GemmArgs& g, const FuseArgs& f, hipStream_t stream);
 hipError_t launch_gemm_decode(const GemmArgs& g, bool packed, void* ws, size_t ws_bytes,
                               hipStream_t stream);
 

@@ -169,6 +169,35 @@ def config4_weights(gpu):
     return out
 
 
+# m <= 4 and k <= 8192: the quantization runs inside the decode kernel
+# (every block quantizes the rows into LDS; block (0, 0) writes q and the row
+# scales); k = 28672 keeps the separate quantizer.  q, r and c must equal the
+# quantizer + GEMM path bit for bit.
+FUSED_SMALL = [(1, 1000, 4112, 4112), (2, 777, 2048, 2056), (3, 4096, 28672, 28672),
+               (4, 64, 16, 24), (4, 28672, 8192, 8192)]
+
+
+@pytest.mark.parametrize("m,n,k,ldx", FUSED_SMALL)
+def test_fused_decode_small_m(w8a8, gpu, m, n, k, ldx):
+    import torch
+    seed = 5000 + m + n + k
+    xw = G.activations(seed, m, ldx)
+    x = np.ascontiguousarray(xw[:, :k])
+    s = G.uniform(seed, G.TID_S, (k,), 0.5, 2.0)
+    w = G.int8(seed, G.TID_B, (n, k))
+    sb = G.uniform(seed, G.TID_SB, (n,), 1e-3, 1e-2)
+    xd = dev(xw, gpu)[:, :k]          # rows of ldx elements
+    sd, sbd = dev(s, gpu), dev(sb, gpu)
+    pw = w8a8.pack_weights(dev(w, gpu))
+    c, q, r = w8a8.fused_sq_gemm_packed(xd, sd, pw, sbd)
+    qo, ro = O.smoothquant(x, s)
+    assert np.array_equal(host(q), qo) and np.array_equal(host(r), ro)
+    assert_f16_bitexact(host(c), O.dequant_f16(O.gemm_i32(qo, w), ro, sb))
+    q2, r2 = w8a8.smoothquant(xd, sd)
+    c2 = w8a8.gemm_packed(q2, pw, r2, sbd)
+    assert np.array_equal(host(c).view(np.uint16), host(c2).view(np.uint16))
+
+
 @pytest.mark.parametrize("m", [1, 16, 64])
 def test_config4_fused_decode(w8a8, gpu, config4_weights, m):
     seed = G.config_seed(4)
