@@ -58,9 +58,9 @@ def trace(directory: str, match: str = "w8a8|gemm|sq_|neg") -> str:
             continue
         dur = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
         groups[(short_name(name), _grid(r))].append(dur)
-    out = [f"{'kernel':60s} {'grid':>9s} {'calls':>5s} {'avg_us':>10s} {'min_us':>10s}"]
+    out = [f"{'kernel':84s} {'grid':>9s} {'calls':>5s} {'avg_us':>10s} {'min_us':>10s}"]
     for (name, grid), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
-        out.append(f"{name[:60]:60s} {grid:>9s} {len(d):5d} {sum(d) / len(d) / 1e3:10.2f} "
+        out.append(f"{name[:84]:84s} {grid:>9s} {len(d):5d} {sum(d) / len(d) / 1e3:10.2f} "
                    f"{min(d) / 1e3:10.2f}")
     return "\n".join(out)
 
