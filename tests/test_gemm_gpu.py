@@ -90,6 +90,19 @@ def test_persistent_tiles_exact(w8a8, gpu, m, n, k):
     assert_f16_bitexact(host(c1), O.dequant_f16(acc, tsa=0.5, tsb=0.25))
 
 
+def test_persistent_tiles_strided_output(w8a8, gpu):
+    # the persistent kernel's stores into rows of ldc > n: columns past n keep
+    # what they held (every store past the matrix is dropped)
+    import torch
+    m, n, k, ldc = 4100, 8200, 160, 8208
+    a, b, sa, sb = inputs(m, n, k, 99)
+    big = torch.full((m, ldc), 7.0, dtype=torch.float16, device=gpu)
+    w8a8.gemm(dev(a, gpu), dev(b, gpu), dev(sa, gpu), dev(sb, gpu), out=big[:, :n])
+    hb = host(big)
+    assert_f16_bitexact(np.ascontiguousarray(hb[:, :n]), O.dequant_f16(O.gemm_i32(a, b), sa, sb))
+    assert (hb[:, n:] == 7.0).all()
+
+
 # K split (workspace given) of launches whose 128 x 128 tiles fill at most
 # half of the 256 CUs: tiles x pieces
 SPLIT_SHAPES = [
