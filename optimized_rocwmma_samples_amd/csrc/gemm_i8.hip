@@ -301,14 +301,15 @@ bool gemm_decode_ok(const GemmArgs& g)
 constexpr uint32_t kFuseMaxK = 8192;
 bool decode_fuse_ok(uint32_t m, uint32_t k)
 {
-    const uint64_t ka = (uint64_t)gemm::packed_ktiles(k) * gemm::kPackK;
+    const uint64_t pitch = (uint64_t)gemm::packed_ktiles(k) * gemm::kPackK + gemm::kFusePad;
     return m >= 1 && m <= gemm::kFuseRows && k <= kFuseMaxK
-           && DecSmall::kLdsBytes + m * ka <= 160 * 1024;
+           && DecSmall::kLdsBytes + m * pitch <= 160 * 1024;
 }
 
 hipError_t launch_gemm_decode_fused(const GemmArgs& g, const FuseArgs& f, hipStream_t stream)
 {
-    const gemm::FuseQ fq{f.x, f.s, f.q, f.r, f.ldx, gemm::packed_ktiles(g.k) * gemm::kPackK, f.qmax};
+    const uint32_t    ka = gemm::packed_ktiles(g.k) * gemm::kPackK;
+    const gemm::FuseQ fq{f.x, f.s, f.q, f.r, f.ldx, ka, ka + gemm::kFusePad, f.qmax};
     const int      vec_ok = out_vec_ok(g);
     const uint32_t step   = weight_panel_rows(g, true);
     for(uint32_t n0 = 0; n0 < g.n; n0 += step) {

@@ -53,17 +53,21 @@ struct DecCfg {
 // q = int8(clamp(rint(p * inv), -qmax, qmax)); the maximum does not depend
 // on the order of the reduction, so q and r are bit-identical.
 constexpr uint32_t kFuseRows = 4;
+// LDS row pitch = ka + kFusePad: the fused rows' 16-byte fragment reads at one
+// k offset (up to 4 rows x 2 lane halves) then fall on distinct bank groups.
+constexpr uint32_t kFusePad = 32;
 struct FuseQ {
     const uint16_t* x;    // [m, ldx] fp16 activations (16-byte aligned rows)
     const float*    s;    // [k] smoothing scale (16-byte aligned)
     int8_t*         q;    // [m, k] quantized rows out
     float*          r;    // [m] row scales out
     uint32_t        ldx;  // ldx % 8 == 0
-    uint32_t        ka;   // LDS row pitch: k rounded up to kPackK (zero padded)
+    uint32_t        ka;   // LDS row length: k rounded up to kPackK (zero padded)
+    uint32_t        pitch; // LDS row pitch: ka + kFusePad
     float           qmax;
 };
 
-// Block-wide: quantize the m (<= kFuseRows) rows into qa (pitch fq.ka) and
+// Block-wide: quantize the m (<= kFuseRows) rows into qa (pitch fq.pitch) and
 // return their row scales in rs.  red: LDS scratch of KW * kFuseRows floats.
 template <class C>
 __device__ __forceinline__ void fuse_quantize(const FuseQ& fq, uint32_t m, uint32_t k, int8_t* qa,
@@ -132,7 +136,7 @@ __device__ __forceinline__ void fuse_quantize(const FuseQ& fq, uint32_t m, uint3
                                          quant_i8(v[6], inv[r], fq.qmax), quant_i8(v[7], inv[r], fq.qmax));
                     if(first_block) *reinterpret_cast<v2i*>(fq.q + (size_t)r * k + c * 8) = pk;
                 }
-                *reinterpret_cast<v2i*>(qa + r * fq.ka + c * 8) = pk;
+                *reinterpret_cast<v2i*>(qa + r * fq.pitch + c * 8) = pk;
             }
         }
     }
@@ -188,7 +192,7 @@ __global__ void __launch_bounds__(C::kThreads) gemm_i8_decode_kernel(KArgs p, in
     using ATile = v4i[C::kMT * 4];
     BTile bq[C::kRing];
     ATile aq[C::kRing];
-    // FUSE: the quantized rows in LDS after the partials area, pitch fq.ka
+    // FUSE: the quantized rows in LDS after the partials area, pitch fq.pitch
     int8_t* qa = lds + C::kLdsBytes;
     auto issue_b = [&](int slot, uint32_t kt) {
         // k-tiles outside [kt0, kt1) read at kOob: zeros, no memory traffic
@@ -220,8 +224,12 @@ __global__ void __launch_bounds__(C::kThreads) gemm_i8_decode_kernel(KArgs p, in
             for(int i = 0; i < C::kMT; ++i) {
                 const uint32_t row = mbase + i * 32 + (lane & 31);
                 const bool     use = live && row < p.m;
-                // the address stays inside the quantized rows whatever the lane
-                const int8_t*  src = qa + (use ? row * fq.ka + kt * kPackK : 0u) + (lane >> 5) * 16;
+                // Lanes past the last row read that row's bytes (one address,
+                // a broadcast, not a bank conflict) and drop them; past kt1
+                // every lane reads row 0's first bytes.  The address stays
+                // inside the quantized rows whatever the lane.
+                const uint32_t rowc = row < p.m ? row : p.m - 1;
+                const int8_t*  src  = qa + (live ? rowc * fq.pitch + kt * kPackK : 0u) + (lane >> 5) * 16;
 #pragma unroll
                 for(int g = 0; g < 4; ++g) {
                     const v4i v         = *reinterpret_cast<const v4i*>(src + g * 32);
@@ -380,7 +388,7 @@ hipError_t launch_decode(const KArgs& p, int out_type, int vec_ok, hipStream_t s
 
 // The decode kernel with the activation quantization folded in (packed
 // weights, fp16 output, p.m <= kFuseRows, C::kMT == 1).  p.sa must be fq.r.
-// The host checks C::kLdsBytes + p.m * fq.ka <= 160 KiB.
+// The host checks C::kLdsBytes + p.m * fq.pitch <= 160 KiB.
 template <class C>
 hipError_t launch_decode_fused(const KArgs& p, const FuseQ& fq, int vec_ok, hipStream_t stream)
 {
@@ -394,7 +402,7 @@ hipError_t launch_decode_fused(const KArgs& p, const FuseQ& fq, int vec_ok, hipS
     });
     const dim3 grid((p.n + C::kNT * 32 - 1) / (C::kNT * 32), 1);
     hipLaunchKernelGGL((gemm_i8_decode_kernel<C, W8A8_OUT_F16, true, true>), grid,
-                       dim3(C::kThreads), C::kLdsBytes + p.m * fq.ka, stream, p, vec_ok, fq);
+                       dim3(C::kThreads), C::kLdsBytes + p.m * fq.pitch, stream, p, vec_ok, fq);
     return hipGetLastError();
 }
 
