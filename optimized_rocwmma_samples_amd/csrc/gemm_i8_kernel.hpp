@@ -294,6 +294,28 @@ struct EpiScales {
 // (now idle) LDS ring, rows of kWaveN fp16 with 16-byte chunks XOR-swizzled
 // by row, then reads it back row-contiguous: every lane stores 16 bytes and
 // a wave store covers whole 128-byte lines of 64 // (kWaveN / 8) rows.
+// fp16 output rows staged in LDS as rows of kRowChunks 16-byte chunks (8
+// columns each).  In the MFMA layout lane (row, half = lane >> 5) holds
+// columns [4 * half, 4 * half + 4) of a chunk and writes them as 8 bytes; the
+// read-back takes whole chunks.  An 8-byte write is served per half-wave (32
+// rows, one half) over 32 banks = 128 bytes, so the chunk is XOR-swizzled with
+// the row bits above the rows that share a 128-byte window and the half flips
+// with row bit 3: the 32 writes then fill each of the window's 16 8-byte slots
+// twice, with no conflict cycles.  The read-back swaps the halves back on the
+// rows that flipped them.
+template <int kRowChunks>
+struct StageSwz {
+    static_assert(kRowChunks == 4 || kRowChunks == 8 || kRowChunks == 16, "row of 4-16 chunks");
+    static constexpr int kSwz   = kRowChunks < 8 ? kRowChunks : 8;
+    static constexpr int kShift = kRowChunks == 4 ? 1 : 0; // 64-byte rows: two per window
+    __device__ static __forceinline__ int  chunk(int ch, int row) { return ch ^ ((row >> kShift) & (kSwz - 1)); }
+    __device__ static __forceinline__ int  half(int h, int row) { return h ^ ((row >> 3) & 1); }
+    __device__ static __forceinline__ v4i  unswap(v4i v, int row)
+    {
+        return ((row >> 3) & 1) ? v4i{v.z, v.w, v.x, v.y} : v;
+    }
+};
+
 template <class C>
 __device__ __forceinline__ void epilogue_f16_lds(const KArgs& p, uint32_t m0, uint32_t n0,
                                                  int vec_ok, int8_t* lds, int slot, int lane,
@@ -306,7 +328,7 @@ __device__ __forceinline__ void epilogue_f16_lds(const KArgs& p, uint32_t m0, ui
     constexpr int kRowsPerSt = kWave / kRowChunks; // rows one wave store covers
     static_assert(kRowChunks == 4 || kRowChunks == 8 || kRowChunks == 16, "row of 4-16 chunks");
     static_assert(C::kWaves * C::kWaveM * kRowBytes <= C::kLdsBytes, "staging fits the ring");
-    constexpr int kSwz = kRowChunks < 8 ? kRowChunks : 8;
+    using S = StageSwz<kRowChunks>;
 
     // every wave's fragment reads and LDS loads are done: the ring is free
     block_barrier();
@@ -326,12 +348,12 @@ __device__ __forceinline__ void epilogue_f16_lds(const KArgs& p, uint32_t m0, ui
 #pragma unroll
                 for(int e = 0; e < 4; ++e)
                     h[e] = float_to_half_bits_2step(((float)acc[i][j][g * 4 + e] * sc.sa[i]) * sbv[e]);
-                const int chunk = j * 4 + g;
-                const int phys  = chunk ^ (row & (kSwz - 1));
+                const int phys = S::chunk(j * 4 + g, row);
                 v2i       pk;
                 pk.x = (int)(h[0] | (h[1] << 16));
                 pk.y = (int)(h[2] | (h[3] << 16));
-                *reinterpret_cast<v2i*>(stage + row * kRowBytes + phys * 16 + (lane >> 5) * 8) = pk;
+                *reinterpret_cast<v2i*>(stage + row * kRowBytes + phys * 16
+                                        + S::half(lane >> 5, row) * 8) = pk;
             }
         }
     }
@@ -343,8 +365,8 @@ __device__ __forceinline__ void epilogue_f16_lds(const KArgs& p, uint32_t m0, ui
 #pragma unroll
     for(int q = 0; q < C::kWaveM / kRowsPerSt; ++q) {
         const int      row  = q * kRowsPerSt + lane / kRowChunks;
-        const int      phys = chunk ^ (row & (kSwz - 1));
-        const v4i      v    = *reinterpret_cast<const v4i*>(stage + row * kRowBytes + phys * 16);
+        const int      phys = S::chunk(chunk, row);
+        const v4i      v    = S::unswap(*reinterpret_cast<const v4i*>(stage + row * kRowBytes + phys * 16), row);
         const uint32_t m    = m0 + wm * C::kWaveM + row;
         if(m >= p.m || n >= p.n) continue;
         uint16_t* dst = reinterpret_cast<uint16_t*>(p.c) + (size_t)m * p.ldc + n;

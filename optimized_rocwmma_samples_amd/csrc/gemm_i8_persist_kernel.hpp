@@ -42,7 +42,6 @@ struct Persist {
     static constexpr int kStores      = C::kTilesM * kStPerPass;  // per wave per tile
     static constexpr int kSliceBytes  = kPassRows * kRowBytes;    // per wave
     static constexpr int kLdsBytes    = C::kLdsBytes + C::kWaves * kSliceBytes;
-    static constexpr int kSwz         = kRowChunks < 8 ? kRowChunks : 8;
     static_assert(kRowChunks == 4 || kRowChunks == 8 || kRowChunks == 16, "row of 4-16 chunks");
     static_assert(kPassRows % kRowsPerSt == 0, "whole stores per pass");
     static_assert(kLdsBytes <= 160 * 1024, "gfx950 LDS per workgroup");
@@ -65,6 +64,7 @@ __device__ __forceinline__ void epilogue_f16_persist(const KArgs& p, __amdgpu_bu
                                                      const EpiScales<C>& sc, int nt)
 {
     using P               = Persist<C>;
+    using S               = StageSwz<P::kRowChunks>;
     const int      chunk  = lane % P::kRowChunks;
     const uint32_t n      = n0 + wn * C::kWaveN + chunk * 8;
     const bool     n_in   = n < p.n;
@@ -82,13 +82,12 @@ __device__ __forceinline__ void epilogue_f16_persist(const KArgs& p, __amdgpu_bu
                 for(int e = 0; e < 4; ++e)
                     h[e] = float_to_half_bits_2step(((float)acc[i][j][g * 4 + e] * sc.sa[i])
                                                     * sbv[e]);
-                const int ch   = j * 4 + g;
-                const int phys = ch ^ (row & (P::kSwz - 1));
+                const int phys = S::chunk(j * 4 + g, row);
                 v2i       pk;
                 pk.x = (int)(h[0] | (h[1] << 16));
                 pk.y = (int)(h[2] | (h[3] << 16));
-                *reinterpret_cast<v2i*>(slice + row * P::kRowBytes + phys * 16 + (lane >> 5) * 8)
-                    = pk;
+                *reinterpret_cast<v2i*>(slice + row * P::kRowBytes + phys * 16
+                                        + S::half(lane >> 5, row) * 8) = pk;
             }
         }
         // read back row-contiguous (a wave's LDS accesses complete in order,
@@ -96,8 +95,8 @@ __device__ __forceinline__ void epilogue_f16_persist(const KArgs& p, __amdgpu_bu
 #pragma unroll
         for(int q = 0; q < P::kStPerPass; ++q) {
             const int      r    = q * P::kRowsPerSt + lane / P::kRowChunks;
-            const int      phys = chunk ^ (r & (P::kSwz - 1));
-            const v4i      v    = *reinterpret_cast<const v4i*>(slice + r * P::kRowBytes + phys * 16);
+            const int      phys = S::chunk(chunk, r);
+            const v4i      v    = S::unswap(*reinterpret_cast<const v4i*>(slice + r * P::kRowBytes + phys * 16), r);
             const uint32_t m    = m0 + wm * C::kWaveM + i * 32 + r;
             const uint32_t off  = (m < p.m && n_in) ? (m * p.ldc + n) * 2 : kOob;
             if(nt)
