@@ -42,15 +42,17 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def make_projection(torch, gen, dev, m, k, n):
-    x = torch.randn((m, k), generator=gen, device=dev, dtype=torch.float32)
-    ncols = max(1, round(0.005 * k))
-    cols = torch.randperm(k, generator=gen, device=dev)[:ncols]
-    x[:, cols] *= 20.0
-    x = x.to(torch.float16)
-    s = torch.rand(k, generator=gen, device=dev) * 1.5 + 0.5
-    w = torch.randint(-127, 128, (n, k), generator=gen, device=dev, dtype=torch.int8)
-    sb = torch.rand(n, generator=gen, device=dev) * 9e-3 + 1e-3
+def make_projection(torch, dev, m, k, n):
+    """cfg3 inputs of one projection from the seeded streams of
+    optimized_rocwmma_samples_amd.datagen (seed 0x5EED0003; tensor ids X, s,
+    B, sb), the same values the cfg3 parity tests check, copied to HBM."""
+    from optimized_rocwmma_samples_amd import datagen as G
+
+    seed = G.config_seed(3)
+    x = torch.from_numpy(G.activations(seed, m, k)).to(dev)
+    s = torch.from_numpy(G.uniform(seed, G.TID_S, (k,), 0.5, 2.0)).to(dev)
+    w = torch.from_numpy(G.int8(seed, G.TID_B, (n, k))).to(dev)
+    sb = torch.from_numpy(G.uniform(seed, G.TID_SB, (n,), 1e-3, 1e-2)).to(dev)
     q = torch.empty((m, k), dtype=torch.int8, device=dev)
     r = torch.empty(m, dtype=torch.float32, device=dev)
     c = torch.empty((m, n), dtype=torch.float16, device=dev)
@@ -314,16 +316,23 @@ def profiled_traffic(projs, cus):
     return sum(per) / len(per), per
 
 
-def bench_cfg3_smaller_m(torch, w8a8, dev, gen, steps=10, sets=3):
+def bench_cfg3_smaller_m(torch, w8a8, dev, base, steps=10, sets=3):
     """Config 3 at its smaller token counts (M = 512, 2048): SmoothQuant +
     GEMM over the four Llama-3-8B projections, as in the headline step, with
     the dense GEMM's K-split workspace preallocated (the launches whose tiles
-    fill at most half of the CUs use it).  `sets` copies of the weights are
-    used in turn so each step streams its weights from HBM (3 x 216 MB)."""
+    fill at most half of the CUs use it).  Inputs are the first M rows of the
+    headline's (datagen) activations; `sets` copies of its weights are used in
+    turn so each step streams its weights from HBM (3 x 216 MB)."""
+    def sub(p, m, copy):
+        return dict(x=p["x"][:m], s=p["s"], w=p["w"].clone() if copy else p["w"], sb=p["sb"],
+                    q=torch.empty((m, p["k"]), dtype=torch.int8, device=dev),
+                    r=torch.empty(m, dtype=torch.float32, device=dev),
+                    c=torch.empty((m, p["n"]), dtype=torch.float16, device=dev),
+                    m=m, k=p["k"], n=p["n"])
+
     out = []
     for m in (512, 2048):
-        projs = [[make_projection(torch, gen, dev, m, k, n) for (_, k, n) in LLAMA3_8B]
-                 for _ in range(sets)]
+        projs = [[sub(p, m, i > 0) for p in base] for i in range(sets)]
         ws_bytes = max(w8a8.gemm_workspace_size(m, n, k) for (_, k, n) in LLAMA3_8B)
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
         ops = sum(2.0 * m * n * k for (_, k, n) in LLAMA3_8B)
@@ -432,6 +441,93 @@ def bench_moe(torch, w8a8, dev, gen, iters=10):
             "frac_mfma": (ops_gu + ops_d) / (total_us * 1e-6) / PEAK_INT8_OPS}
 
 
+def bench_hipblaslt_yardstick(torch, projs, iters=10):
+    """Same-box yardstick: hipBLASLt's int8 GEMM (torch._int_mm, int32 output,
+    no quantizer and no dequant) on the cfg3 projections, in TOPS."""
+    out = []
+    for (name, k, n), p in zip(LLAMA3_8B, projs):
+        a, bt = p["q"], p["w"].t()  # [M, K] and the [K, N] view of the [N, K] weights
+        for _ in range(3):
+            torch._int_mm(a, bt)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            torch._int_mm(a, bt)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / iters
+        out.append({"proj": name, "K": k, "N": n, "us": us,
+                    "TOPS": 2.0 * p["m"] * n * k / (us * 1e-6) / 1e12})
+    return out
+
+
+def measured_peaks(torch, dev, cus):
+    """Ceilings measured on this GPU in this run (libw8a8_peaks.so, built from
+    csrc/peaks.hip): the int8 MFMA-only loop (random and zero operands), a
+    streaming copy over 2 x 1 GiB, and the launch floor of back-to-back
+    launches replayed from a graph (48 per replay, as the cfg1 quantizer is
+    timed)."""
+    import ctypes
+
+    lib_path = ROOT / "optimized_rocwmma_samples_amd" / "lib" / "libw8a8_peaks.so"
+    lib = ctypes.CDLL(str(lib_path))
+    lib.w8a8_peak_mfma_ops.restype = ctypes.c_double
+    lib.w8a8_peak_mfma_ops.argtypes = [ctypes.c_uint32, ctypes.c_uint32]
+    lib.w8a8_peak_mfma.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int, ctypes.c_void_p,
+                                   ctypes.c_void_p]
+    lib.w8a8_peak_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                   ctypes.c_uint32, ctypes.c_void_p]
+    lib.w8a8_peak_empty.argtypes = [ctypes.c_void_p]
+
+    def check(rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed: hipError {rc}")
+
+    def timed(launch, reps):
+        st = torch.cuda.current_stream(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for _ in range(2):
+            launch(st.cuda_stream)
+        e0.record(st)
+        for _ in range(reps):
+            launch(st.cuda_stream)
+        e1.record(st)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / reps  # seconds per launch
+
+    out = {}
+    blocks, iters = cus, 4096
+    sink = torch.empty(blocks * 4, dtype=torch.int32, device=dev)
+    ops = lib.w8a8_peak_mfma_ops(blocks, iters)
+    for name, rnd in (("random", 1), ("zeros", 0)):
+        t_end = time.perf_counter() + 0.2  # let the clocks settle under this load
+        while time.perf_counter() < t_end:
+            check(lib.w8a8_peak_mfma(blocks, iters, rnd, sink.data_ptr(),
+                                     torch.cuda.current_stream(dev).cuda_stream), "peak_mfma")
+            torch.cuda.synchronize()
+        sec = timed(lambda s, r=rnd: check(lib.w8a8_peak_mfma(blocks, iters, r, sink.data_ptr(), s),
+                                            "peak_mfma"), 10)
+        out[f"mfma_i8_{name}_TOPS"] = ops / sec / 1e12
+    out["mfma_note"] = (f"v_mfma_i32_32x32x32_i8 only, {blocks} blocks x 4 waves x 8 independent "
+                        f"accumulators, {iters} rounds; operands held in registers")
+    nbytes = 1 << 30
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(3)
+    dst = torch.empty_like(src)
+    best = 0.0
+    for mult in (4, 8, 16):
+        sec = timed(lambda s, b=cus * mult: check(lib.w8a8_peak_copy(src.data_ptr(), dst.data_ptr(),
+                                                                      nbytes, b, s), "peak_copy"), 10)
+        best = max(best, 2 * nbytes / sec / 1e9)
+    out["copy_GBps"] = best
+    out["copy_note"] = "2^30 bytes read + 2^30 bytes written per launch, 16 B per lane access"
+    del src, dst
+    calls = [lambda: check(lib.w8a8_peak_empty(torch.cuda.current_stream(dev).cuda_stream),
+                           "peak_empty")] * 48
+    out["launch_floor_us"] = graph_us(torch, calls)
+    out["launch_floor_note"] = "empty kernel, 48 launches per captured-graph replay"
+    return out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
@@ -465,7 +561,8 @@ def main(argv=None) -> int:
     gen.manual_seed(0x5EED0003)
 
     log(f"{w8a8.version()} on {torch.cuda.get_device_name(dev)}")
-    projs = [make_projection(torch, gen, dev, args.m, k, n) for (_, k, n) in LLAMA3_8B]
+    projs = [make_projection(torch, dev, args.m, k, n) for (_, k, n) in LLAMA3_8B]
+    log("cfg3 inputs generated (datagen streams, seed 0x5EED0003)")
     total_ops = sum(2.0 * p["m"] * p["n"] * p["k"] for p in projs)
 
     def step(events=None):
@@ -536,7 +633,7 @@ def main(argv=None) -> int:
     algo_bytes = [p["m"] * p["k"] + p["n"] * p["k"] + 2 * p["m"] * p["n"] + 4 * (p["m"] + p["n"])
                   for p in projs]
     roofline = {"bound": "mfma", "achieved": gemm_tops, "peak": PEAK_INT8_OPS / 1e12,
-                "unit": "TFLOP/s", "frac": gemm_tops * 1e12 / PEAK_INT8_OPS, "traffic": traffic,
+                "unit": "TOPS", "frac": gemm_tops * 1e12 / PEAK_INT8_OPS, "traffic": traffic,
                 "traffic_per_projection": traffic_per,
                 "algorithmic_bytes_per_projection": algo_bytes,
                 "traffic_source": (f"{TRAFFIC_PROFILE.relative_to(ROOT)} (rocprofv3 FETCH_SIZE x2.0 "
@@ -555,17 +652,28 @@ def main(argv=None) -> int:
                 "note": "int8 ops (2*M*N*K) per launch / average launch duration over the four "
                         "projection GEMMs; peak = 5.0 POP/s dense int8"}
 
+    peaks = measured_peaks(torch, dev, cus)
+    log(json.dumps(peaks))
+    roofline["peak_measured"] = peaks["mfma_i8_random_TOPS"]
+    roofline["frac_measured"] = gemm_tops / peaks["mfma_i8_random_TOPS"]
+    roofline["peak_measured_note"] = ("int8 MFMA-only loop on random operands, same run "
+                                      "(measured_peaks)")
+
     extras = {}
     if not args.no_extras:
         extras["smoothquant_cfg1"] = bench_quantizer(torch, w8a8, dev, gen)
+        extras["smoothquant_cfg1"]["frac_copy_measured"] = (extras["smoothquant_cfg1"]["GBps"]
+                                                           / peaks["copy_GBps"])
         log(json.dumps(extras["smoothquant_cfg1"]))
         extras["smoothquant_sweep"] = bench_quantizer_sweep(torch, w8a8, dev, gen)
         log(json.dumps(extras["smoothquant_sweep"]))
         extras["rmsnorm_smoothquant"] = bench_rmsnorm_sq(torch, w8a8, dev, gen)
         log(json.dumps(extras["rmsnorm_smoothquant"]))
+        extras["hipblaslt_int_mm_cfg3"] = bench_hipblaslt_yardstick(torch, projs)
+        log(json.dumps(extras["hipblaslt_int_mm_cfg3"]))
         extras["gemm_cfg2"] = bench_gemm_4096(torch, w8a8, dev, gen)
         log(json.dumps(extras["gemm_cfg2"]))
-        extras["cfg3_smaller_m"] = bench_cfg3_smaller_m(torch, w8a8, dev, gen)
+        extras["cfg3_smaller_m"] = bench_cfg3_smaller_m(torch, w8a8, dev, projs)
         log(json.dumps(extras["cfg3_smaller_m"]))
         extras["decode_cfg4"] = bench_decode(torch, w8a8, dev, gen)
         log(json.dumps(extras["decode_cfg4"]))
@@ -599,14 +707,17 @@ def main(argv=None) -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic (seeded N(0,1) activations with 0.5% x20 outlier columns, "
-                "U{-127..127} int8 weights)",
+        "data": "synthetic: the seeded counter-based streams of datagen.py (N(0,1) "
+                "activations with 0.5% x20 outlier columns, U[0.5,2] smooth scale, "
+                "U{-127..127} int8 weights, U[1e-3,1e-2] channel scales), the cfg3 parity "
+                "tests' inputs",
         "config": {"workload": "cfg3 fused SmoothQuant + W8A8 GEMM, Llama-3-8B projections "
                                "qkv/o_proj/gate_up/down",
                    "m": args.m, "projections": [[n_, k, n] for (n_, k, n) in LLAMA3_8B],
                    "parallelism": "single GPU"},
         "frac_mfma_peak": value * 1e12 / PEAK_INT8_OPS,
         "roofline": roofline,
+        "measured_peaks": peaks,
         "cpu_baseline": cpu,
         "per_projection": per_proj,
         **extras,

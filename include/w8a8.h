@@ -277,8 +277,12 @@ size_t w8a8_grouped_gemm_workspace_size(uint32_t num_groups);
  * Runs every group's w8a8_gemm in one launch.  Replaces grouped_gemm_kernel
  * (rocwmma_grouped_gemm.cpp:104-178), whose host code uploads the descriptor
  * array with a tile_offset prefix in it (:180-226): here `groups` is a HOST array,
- * validated, then copied into `workspace` (hipMemcpyAsync on `stream`; the
- * host array may be reused when the call returns).  Every group needs the
+ * validated, then copied into `workspace` by one hipMemcpyAsync on `stream`.
+ * The call returns before that copy runs: the host array must stay valid and
+ * unchanged until the stream has reached it (synchronize the stream, or an
+ * event recorded after the call, before reusing it).  A HIP graph that
+ * captures the call records the copy, so every replay reads the host array
+ * again: keep it alive and unchanged for as long as the graph may run.  Every group needs the
  * fast-path layout (16-byte aligned a/b, lda, ldb, k multiples of 16) and
  * m*lda, n*ldb < 2^31 (W8A8_ERROR_NOT_SUPPORTED otherwise).
  */

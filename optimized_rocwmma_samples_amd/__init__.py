@@ -399,10 +399,19 @@ def grouped_gemm(problems, out_dtype=None, outs=None):
     otype = OUT_I32 if results[0].dtype == torch.int32 else OUT_F16
     ws_bytes = int(library().w8a8_grouped_gemm_workspace_size(len(problems)))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    # the call stages the host descriptors before it returns; the workspace is
-    # freed through torch's caching allocator, which orders reuse on the stream
+    # The descriptors are copied from this host array by an asynchronous copy
+    # on the stream: keep the array alive until an event recorded after the
+    # call has completed.  The workspace is freed through torch's caching
+    # allocator, which orders its reuse on the stream.
     _lib.call("w8a8_grouped_gemm", descs, len(problems), otype, _ptr(ws), ws_bytes, _stream(dev))
+    done = torch.cuda.Event()
+    done.record(torch.cuda.current_stream(dev))
+    _pending_descs[:] = [(e, d) for (e, d) in _pending_descs if not e.query()]
+    _pending_descs.append((done, descs))
     return results
+
+
+_pending_descs: list = []  # (event, host descriptor array) of grouped_gemm calls in flight
 
 
 def topk_softmax(logits, topk: int):

@@ -15,11 +15,13 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cerrno>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <initializer_list>
 #include <iostream>
 #include <memory>
 #include <string>
@@ -47,28 +49,72 @@
 namespace app {
 
 // ---------------------------------------------------------------- options
+// Command line of a CLI: positional sizes (the reference's `[M N K]`
+// grammar), --verify / --no-verify, -h / --help, and the CLI's own extra
+// flags.  Every check here runs before the first HIP call, so argument errors
+// end with status 1 and a usage line on any host, GPU or not.
 struct Options {
     bool                     verify = false;
-    std::vector<std::string> pos; // positional arguments
+    std::vector<std::string> pos;   // positional arguments
+    std::vector<std::string> flags; // extra flags given (from the CLI's list)
+    const char*              usage = "";
+    bool has(const char* f) const { return std::find(flags.begin(), flags.end(), f) != flags.end(); }
 };
 
-inline Options parse(int argc, char** argv)
+[[noreturn]] inline void usage_error(const Options& o, const std::string& msg)
+{
+    std::cerr << "[ERROR] " << msg << "\nusage: " << o.usage << "\n";
+    std::exit(1);
+}
+
+inline Options parse(int argc, char** argv, const char* usage,
+                     std::initializer_list<const char*> extra = {})
 {
     Options o;
+    o.usage = usage;
 #if defined(W8A8_CPU_VERIFY)
     o.verify = true;
 #endif
     if(const char* v = std::getenv("W8A8_VERIFY")) o.verify = o.verify || std::atoi(v) != 0;
     for(int i = 1; i < argc; ++i) {
-        std::string a = argv[i];
-        if(a == "--verify")
+        const std::string a = argv[i];
+        if(a == "-h" || a == "--help") {
+            std::cout << "usage: " << usage << "\n";
+            std::exit(0);
+        } else if(a == "--verify") {
             o.verify = true;
-        else if(a == "--no-verify")
+        } else if(a == "--no-verify") {
             o.verify = false;
-        else
+        } else if(a.size() > 1 && a[0] == '-') {
+            bool known = false;
+            for(const char* f : extra) known = known || a == f;
+            if(!known) usage_error(o, "unknown option " + a);
+            o.flags.push_back(a);
+        } else {
             o.pos.push_back(a);
+        }
     }
     return o;
+}
+
+// The positional sizes: none (the CLI runs its default suite) or exactly one
+// of the allowed counts, each a decimal integer in [1, 2^31).
+inline std::vector<uint32_t> sizes(const Options& o, std::initializer_list<size_t> counts)
+{
+    if(o.pos.empty()) return {};
+    bool ok = false;
+    for(size_t c : counts) ok = ok || o.pos.size() == c;
+    if(!ok) usage_error(o, "wrong number of sizes (" + std::to_string(o.pos.size()) + ")");
+    std::vector<uint32_t> v;
+    for(const std::string& a : o.pos) {
+        char*              end = nullptr;
+        errno                  = 0;
+        const long long    x   = std::strtoll(a.c_str(), &end, 10);
+        if(a.empty() || *end != '\0' || errno != 0 || x < 1 || x >= (1ll << 31))
+            usage_error(o, "size '" + a + "' is not an integer in [1, 2^31)");
+        v.push_back((uint32_t)x);
+    }
+    return v;
 }
 
 inline void banner(const char* title)

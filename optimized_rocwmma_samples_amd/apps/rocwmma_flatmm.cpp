@@ -53,11 +53,11 @@ static void test_flatmm(uint32_t m, uint32_t n, uint32_t k, bool verify)
 
 int main(int argc, char* argv[])
 {
-    const app::Options o = app::parse(argc, argv);
+    const app::Options o = app::parse(argc, argv, "rocwmma_flatmm [M N K] [--verify]");
+    const auto         d = app::sizes(o, {3});
     app::banner("W8A8 GEMM over packed weights (MI355X gfx950)");
-    if(o.pos.size() >= 3) {
-        test_flatmm(std::atoi(o.pos[0].c_str()), std::atoi(o.pos[1].c_str()),
-                    std::atoi(o.pos[2].c_str()), o.verify);
+    if(!d.empty()) {
+        test_flatmm(d[0], d[1], d[2], o.verify);
         return 0;
     }
     for(uint32_t m : {128u, 256u, 512u, 1024u, 4096u}) test_flatmm(m, 4096, 4096, o.verify);

@@ -80,12 +80,13 @@ static void test_fused_moe(uint32_t t, uint32_t h, uint32_t inter, uint32_t e, u
 
 int main(int argc, char* argv[])
 {
-    const app::Options o = app::parse(argc, argv);
+    const app::Options o = app::parse(
+        argc, argv, "rocwmma_fused_moe [TOKENS HIDDEN INTER EXPERTS TOPK] [--verify]");
+    const auto d = app::sizes(o, {5});
+    if(!d.empty() && d[4] > d[3]) app::usage_error(o, "TOPK must not exceed EXPERTS");
     app::banner("W8A8 MoE FFN (MI355X gfx950)");
-    if(o.pos.size() >= 5) {
-        test_fused_moe(std::atoi(o.pos[0].c_str()), std::atoi(o.pos[1].c_str()),
-                       std::atoi(o.pos[2].c_str()), std::atoi(o.pos[3].c_str()),
-                       std::atoi(o.pos[4].c_str()), o.verify);
+    if(!d.empty()) {
+        test_fused_moe(d[0], d[1], d[2], d[3], d[4], o.verify);
         return 0;
     }
     test_fused_moe(3328, 4096, 14336, 8, 2, o.verify);

@@ -68,14 +68,14 @@ static void test_quant_gemm(uint32_t m, uint32_t n, uint32_t k, bool sample, boo
 
 int main(int argc, char* argv[])
 {
-    app::Options o      = app::parse(argc, argv);
-    bool         sample = false;
-    std::vector<std::string> pos;
-    for(auto& a : o.pos) (a == "--sample-layout" ? (void)(sample = true) : pos.push_back(a));
+    const app::Options o = app::parse(
+        argc, argv, "rocwmma_gemm_quantized [M N K] [--sample-layout] [--verify]",
+        {"--sample-layout"});
+    const bool sample = o.has("--sample-layout");
+    const auto d      = app::sizes(o, {3});
     app::banner("W8A8 Quantized GEMM, int8 MFMA (MI355X gfx950)");
-    if(pos.size() >= 3) {
-        test_quant_gemm(std::atoi(pos[0].c_str()), std::atoi(pos[1].c_str()),
-                        std::atoi(pos[2].c_str()), sample, o.verify);
+    if(!d.empty()) {
+        test_quant_gemm(d[0], d[1], d[2], sample, o.verify);
         return 0;
     }
     test_quant_gemm(3840, 4096, 4096, sample, o.verify);

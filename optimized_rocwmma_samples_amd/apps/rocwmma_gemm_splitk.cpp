@@ -56,11 +56,11 @@ static void test_decode(uint32_t m, uint32_t n, uint32_t k, bool verify)
 
 int main(int argc, char* argv[])
 {
-    const app::Options o = app::parse(argc, argv);
+    const app::Options o = app::parse(argc, argv, "rocwmma_gemm_splitk [M N K] [--verify]");
+    const auto         d = app::sizes(o, {3});
     app::banner("W8A8 decode GEMM, split-K inside the block (MI355X gfx950)");
-    if(o.pos.size() >= 3) {
-        test_decode(std::atoi(o.pos[0].c_str()), std::atoi(o.pos[1].c_str()),
-                    std::atoi(o.pos[2].c_str()), o.verify);
+    if(!d.empty()) {
+        test_decode(d[0], d[1], d[2], o.verify);
         return 0;
     }
     for(uint32_t m : {1u, 16u, 64u}) {

@@ -62,7 +62,8 @@ static void test_grouped(const std::vector<std::array<uint32_t, 3>>& sizes, bool
 
 int main(int argc, char* argv[])
 {
-    const app::Options o = app::parse(argc, argv);
+    const app::Options o = app::parse(argc, argv, "rocwmma_grouped_gemm [--verify]");
+    (void)app::sizes(o, {});
     app::banner("W8A8 Grouped GEMM (MI355X gfx950)");
     test_grouped({{256, 4096, 4096}, {512, 4096, 4096}, {128, 4096, 4096}, {768, 4096, 4096}},
                  o.verify);

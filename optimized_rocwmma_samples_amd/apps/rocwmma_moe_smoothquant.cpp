@@ -62,7 +62,8 @@ static void test_moe_smoothquant(uint32_t tokens, uint32_t hidden, uint32_t expe
 
 int main(int argc, char* argv[])
 {
-    const app::Options o = app::parse(argc, argv);
+    const app::Options o = app::parse(argc, argv, "rocwmma_moe_smoothquant [--verify]");
+    (void)app::sizes(o, {});
     app::banner("W8A8 MoE SmoothQuant (MI355X gfx950)");
     test_moe_smoothquant(3328, 4096, 32, 5, o.verify);
     test_moe_smoothquant(3328, 4096, 8, 2, o.verify);

@@ -48,12 +48,14 @@ static void test_sort(uint32_t tokens, uint32_t experts, uint32_t topk, uint32_t
 
 int main(int argc, char* argv[])
 {
-    const app::Options o = app::parse(argc, argv);
+    const app::Options o = app::parse(argc, argv, "rocwmma_moe_sorting [TOKENS EXPERTS TOPK] [--verify]");
+    const auto         d = app::sizes(o, {3});
     uint32_t           tokens = 3328, experts = 8, topk = 4, unit = 32;
-    if(o.pos.size() >= 3) {
-        tokens  = std::atoi(o.pos[0].c_str());
-        experts = std::atoi(o.pos[1].c_str());
-        topk    = std::atoi(o.pos[2].c_str());
+    if(!d.empty()) {
+        tokens  = d[0];
+        experts = d[1];
+        topk    = d[2];
+        if(topk > experts) app::usage_error(o, "TOPK must not exceed EXPERTS");
     }
     app::banner("W8A8 MoE Sorting, stable (MI355X gfx950)");
     test_sort(tokens, experts, topk, unit, o.verify);

@@ -162,11 +162,12 @@ void test_add_rmsnorm(uint32_t M, uint32_t N, bool verify, bool fused_sq)
 
 int main(int argc, char* argv[])
 {
-    const app::Options o = app::parse(argc, argv);
+    const app::Options o = app::parse(argc, argv, "rocwmma_rmsnorm2d [M N] [--verify]");
+    const auto         d = app::sizes(o, {2});
     uint32_t           M = 3328, N = 4096;
-    if(o.pos.size() >= 2) {
-        M = (uint32_t)std::atoi(o.pos[0].c_str());
-        N = (uint32_t)std::atoi(o.pos[1].c_str());
+    if(!d.empty()) {
+        M = d[0];
+        N = d[1];
     }
     app::banner("W8A8 RMSNorm2D / Add+RMSNorm2D (+ SmoothQuant) (MI355X gfx950)");
     test_rmsnorm(M, N, o.verify);

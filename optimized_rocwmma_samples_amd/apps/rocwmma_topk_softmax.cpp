@@ -35,12 +35,14 @@ static void test_topk(uint32_t t, uint32_t e, uint32_t k, bool verify)
 
 int main(int argc, char* argv[])
 {
-    const app::Options o = app::parse(argc, argv);
+    const app::Options o = app::parse(argc, argv, "rocwmma_topk_softmax [TOKENS EXPERTS TOPK] [--verify]");
+    const auto         d = app::sizes(o, {3});
     uint32_t           t = 128, e = 8, k = 4;
-    if(o.pos.size() >= 3) {
-        t = std::atoi(o.pos[0].c_str());
-        e = std::atoi(o.pos[1].c_str());
-        k = std::atoi(o.pos[2].c_str());
+    if(!d.empty()) {
+        t = d[0];
+        e = d[1];
+        k = d[2];
+        if(k > e) app::usage_error(o, "TOPK must not exceed EXPERTS");
     }
     app::banner("W8A8 MoE TopK-Softmax (MI355X gfx950)");
     test_topk(t, e, k, o.verify);

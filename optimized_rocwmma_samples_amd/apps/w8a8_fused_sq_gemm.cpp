@@ -46,11 +46,11 @@ static void test_fused(uint32_t m, uint32_t n, uint32_t k, bool verify)
 
 int main(int argc, char* argv[])
 {
-    const app::Options o = app::parse(argc, argv);
+    const app::Options o = app::parse(argc, argv, "w8a8_fused_sq_gemm [M N K] [--verify]");
+    const auto         d = app::sizes(o, {3});
     app::banner("W8A8 fused SmoothQuant + GEMM (MI355X gfx950)");
-    if(o.pos.size() >= 3) {
-        test_fused(std::atoi(o.pos[0].c_str()), std::atoi(o.pos[1].c_str()),
-                   std::atoi(o.pos[2].c_str()), o.verify);
+    if(!d.empty()) {
+        test_fused(d[0], d[1], d[2], o.verify);
         return 0;
     }
     const uint32_t shapes[4][2] = {{4096, 6144}, {4096, 4096}, {4096, 28672}, {14336, 4096}};

@@ -257,13 +257,14 @@ static int validate_gemm(const char* fn, uint32_t m, uint32_t n, uint32_t k, con
     return W8A8_SUCCESS;
 }
 
-int w8a8_gemm(uint32_t m, uint32_t n, uint32_t k, const int8_t* a, const int8_t* b, void* c,
-              uint32_t lda, uint32_t ldb, uint32_t ldc, const float* scale_a,
-              const float* scale_b, float tensor_scale_a, float tensor_scale_b, int out_type,
-              int layout, void* workspace, size_t workspace_bytes, hipStream_t stream)
+// w8a8_gemm body (arguments validated by the caller; `fn`
+// names the entry point in error messages).
+static int gemm_entry(const char* fn, uint32_t m, uint32_t n, uint32_t k, const int8_t* a,
+                      const int8_t* b, void* c, uint32_t lda, uint32_t ldb, uint32_t ldc,
+                      const float* scale_a, const float* scale_b, float tensor_scale_a,
+                      float tensor_scale_b, int out_type, int layout, void* workspace,
+                      size_t workspace_bytes, hipStream_t stream)
 {
-    int rc = validate_gemm("w8a8_gemm", m, n, k, a, b, c, lda, ldb, ldc, out_type, layout);
-    if(rc != W8A8_SUCCESS) return rc;
 
     w8a8::GemmArgs g{m, n, k, a, b, c, lda, ldb, ldc, scale_a, scale_b,
                      tensor_scale_a, tensor_scale_b, out_type};
@@ -272,33 +273,44 @@ int w8a8_gemm(uint32_t m, uint32_t n, uint32_t k, const int8_t* a, const int8_t*
         const size_t need = w8a8_gemm_workspace_size(m, n, k, layout);
         if(workspace == nullptr || workspace_bytes < need) {
             // No room to repack: strided generic kernel over the sample layout.
-            return hip_status(w8a8::launch_gemm_generic(g, 1, lda, 1, ldb, stream),
-                              "w8a8_gemm(generic)");
+            return hip_status(w8a8::launch_gemm_generic(g, 1, lda, 1, ldb, stream), fn);
         }
         if(reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
-            return fail(W8A8_ERROR_INVALID_VALUE, "w8a8_gemm: workspace must be 256-byte aligned");
+            return fail(W8A8_ERROR_INVALID_VALUE, "%s: workspace must be 256-byte aligned", fn);
         const uint32_t kp  = round_up16(k);
         int8_t*        at  = static_cast<int8_t*>(workspace);
         int8_t*        bt  = at + ((size_t)m * kp + 255) / 256 * 256;
         hipError_t     e   = w8a8::launch_transpose_i8(a, lda, at, kp, m, k, stream);
         if(e == hipSuccess) e = w8a8::launch_transpose_i8(b, ldb, bt, kp, n, k, stream);
-        if(e != hipSuccess) return hip_status(e, "w8a8_gemm(repack)");
+        if(e != hipSuccess) return hip_status(e, fn);
         g.a   = at;
         g.b   = bt;
         g.lda = kp;
         g.ldb = kp;
         g.k   = kp; // zero padding contributes nothing
-        return hip_status(w8a8::launch_gemm_nk(g, nullptr, 0, stream), "w8a8_gemm");
+        return hip_status(w8a8::launch_gemm_nk(g, nullptr, 0, stream), fn);
     }
 
     if(workspace && reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
-        return fail(W8A8_ERROR_INVALID_VALUE, "w8a8_gemm: workspace must be 16-byte aligned");
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: workspace must be 16-byte aligned", fn);
     if(!w8a8::gemm_fast_path_ok(g))
-        return hip_status(w8a8::launch_gemm_generic(g, lda, 1, ldb, 1, stream),
-                          "w8a8_gemm(generic)");
+        return hip_status(w8a8::launch_gemm_generic(g, lda, 1, ldb, 1, stream), fn);
     return hip_status(w8a8::launch_gemm_nk(g, workspace, workspace ? workspace_bytes : 0, stream),
-                      "w8a8_gemm");
+                      fn);
 }
+
+int w8a8_gemm(uint32_t m, uint32_t n, uint32_t k, const int8_t* a, const int8_t* b, void* c,
+              uint32_t lda, uint32_t ldb, uint32_t ldc, const float* scale_a,
+              const float* scale_b, float tensor_scale_a, float tensor_scale_b, int out_type,
+              int layout, void* workspace, size_t workspace_bytes, hipStream_t stream)
+{
+    const char* fn = "w8a8_gemm";
+    int         rc = validate_gemm(fn, m, n, k, a, b, c, lda, ldb, ldc, out_type, layout);
+    if(rc != W8A8_SUCCESS) return rc;
+    return gemm_entry(fn, m, n, k, a, b, c, lda, ldb, ldc, scale_a, scale_b, tensor_scale_a,
+                      tensor_scale_b, out_type, layout, workspace, workspace_bytes, stream);
+}
+
 
 int w8a8_fused_sq_gemm(const void* x, const float* smooth_scale, const int8_t* w,
                        const float* scale_w, void* c, uint32_t m, uint32_t n, uint32_t k,

@@ -71,7 +71,7 @@ __global__ void __launch_bounds__(256) gemm_i8_generic_kernel(KArgs p, size_t sa
             f = f * (p.tsa * p.tsb);
         else
             f = (f * (p.sa ? p.sa[m] : p.tsa)) * (p.sb ? p.sb[n] : p.tsb);
-        reinterpret_cast<uint16_t*>(p.c)[(size_t)m * p.ldc + n] = float_to_half_bits(f);
+        reinterpret_cast<uint16_t*>(p.c)[(size_t)m * p.ldc + n] = float_to_half_bits_2step(f);
     }
 }
 

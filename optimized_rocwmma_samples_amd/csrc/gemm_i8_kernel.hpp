@@ -206,7 +206,7 @@ __device__ __forceinline__ void store4(const KArgs& p, uint32_t m, uint32_t n, c
         for(int e = 0; e < 4; ++e) {
             float f = (float)v[e];
             f       = mode1 ? f * ab : (f * sa) * sbv[e];
-            h[e]    = float_to_half_bits(f);
+            h[e]    = float_to_half_bits_2step(f);
         }
         uint16_t* dst = reinterpret_cast<uint16_t*>(p.c) + (size_t)m * p.ldc + n;
         if(vec_ok && n + 4 <= p.n) {

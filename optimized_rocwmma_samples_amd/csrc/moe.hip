@@ -577,15 +577,16 @@ __global__ void __launch_bounds__(256)
     }
     uint16_t* dst = out + (size_t)t * ldo + c0;
     if(vec && c0 + 8 <= n) {
-        uint4 v;
-        v.x = (uint32_t)float_to_half_bits(acc[0]) | ((uint32_t)float_to_half_bits(acc[1]) << 16);
-        v.y = (uint32_t)float_to_half_bits(acc[2]) | ((uint32_t)float_to_half_bits(acc[3]) << 16);
-        v.z = (uint32_t)float_to_half_bits(acc[4]) | ((uint32_t)float_to_half_bits(acc[5]) << 16);
-        v.w = (uint32_t)float_to_half_bits(acc[6]) | ((uint32_t)float_to_half_bits(acc[7]) << 16);
-        *reinterpret_cast<uint4*>(dst) = v;
+        // two roundings (the fp32 sum, then fp16): the last fma must not fold
+        // into a mixed-precision fma that rounds to fp16 once
+        auto pk = [&](int x) {
+            return (uint32_t)float_to_half_bits_2step(acc[x])
+                   | ((uint32_t)float_to_half_bits_2step(acc[x + 1]) << 16);
+        };
+        *reinterpret_cast<uint4*>(dst) = make_uint4(pk(0), pk(2), pk(4), pk(6));
     } else {
         for(int x = 0; x < 8; ++x)
-            if(c0 + x < n) dst[x] = float_to_half_bits(acc[x]);
+            if(c0 + x < n) dst[x] = float_to_half_bits_2step(acc[x]);
     }
 }
 

@@ -16,6 +16,9 @@ expert s=9, W_down=10, sb_down=11.
 """
 from __future__ import annotations
 
+import concurrent.futures as _cf
+import os
+
 import numpy as np
 
 GOLDEN = np.uint64(0x9E3779B97F4A7C15)
@@ -27,6 +30,21 @@ TID_LOGITS, TID_EXPERT_S, TID_W_DOWN, TID_SB_DOWN = 8, 9, 10, 11
 TID_RESIDUAL, TID_GAMMA = 12, 13  # RMSNorm residual stream and weight
 
 _CHUNK = 1 << 22
+# numpy releases the GIL inside its ufuncs, so chunks generate in parallel
+# threads; every element is a function of its index alone, so the values do
+# not depend on the thread count.
+_THREADS = max(1, min(16, os.cpu_count() or 1))
+
+
+def _parallel(starts, fn) -> None:
+    starts = list(starts)
+    if len(starts) <= 1 or _THREADS == 1:
+        for s in starts:
+            fn(s)
+        return
+    with _cf.ThreadPoolExecutor(max_workers=_THREADS) as ex:
+        for _ in ex.map(fn, starts):
+            pass
 
 
 def config_seed(cfg: int) -> int:
@@ -47,9 +65,12 @@ def hash64(seed: int, tid: int, start: int, count: int) -> np.ndarray:
 
 def _chunked(total: int, fn, dtype) -> np.ndarray:
     out = np.empty(total, dtype=dtype)
-    for s in range(0, total, _CHUNK):
+
+    def one(s):
         n = min(_CHUNK, total - s)
         out[s:s + n] = fn(s, n)
+
+    _parallel(range(0, total, _CHUNK), one)
     return out
 
 
@@ -104,7 +125,8 @@ def activations(seed: int, m: int, k: int, outlier_frac: float = 0.005,
     cols = outlier_columns(seed, k, outlier_frac)
     out = np.empty((m, k), dtype=np.float16)
     rows_per = max(1, _CHUNK // max(k, 1))
-    for r0 in range(0, m, rows_per):
+
+    def one(r0):
         r1 = min(m, r0 + rows_per)
         h = hash64(seed, TID_X, 2 * r0 * k, 2 * (r1 - r0) * k)
         u = (h >> np.uint64(11)).astype(np.float64) * (2.0 ** -53)
@@ -112,6 +134,8 @@ def activations(seed: int, m: int, k: int, outlier_frac: float = 0.005,
         z = z.reshape(r1 - r0, k)
         z[:, cols] *= outlier_scale
         out[r0:r1] = z.astype(np.float16)
+
+    _parallel(range(0, m, rows_per), one)
     return out
 
 

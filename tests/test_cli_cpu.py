@@ -1,0 +1,159 @@
+"""Sample CLIs and their runner, without a GPU: argument errors end with status 1
+and a usage line before any HIP call; on a host with no GPU the first HIP call
+ends the program with status 1 (the reference's CHECK_HIP behaviour,
+rocwmma_smoothquant.cpp:35-37); the runner's scraping of result lines follows
+the reference runner's rules (benchmark.sh:178-189) and its PASS / FAIL /
+TIMEOUT / SKIP accounting is checked on stub executables."""
+from __future__ import annotations
+
+import csv
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+BIN = ROOT / "optimized_rocwmma_samples_amd" / "bin"
+sys.path.insert(0, str(ROOT))
+
+from optimized_rocwmma_samples_amd import benchmark as B  # noqa: E402
+
+# name -> (number of sizes it takes, a valid size list)
+CLIS = {
+    "rocwmma_smoothquant": (2, ["256", "4096"]),
+    "rocwmma_moe_smoothquant": (0, []),
+    "rocwmma_rmsnorm2d": (2, ["256", "4096"]),
+    "rocwmma_gemm_quantized": (3, ["512", "512", "512"]),
+    "w8a8_fused_sq_gemm": (3, ["512", "1024", "4096"]),
+    "rocwmma_gemm_splitk": (3, ["16", "4096", "4096"]),
+    "rocwmma_flatmm": (3, ["64", "4096", "4096"]),
+    "rocwmma_grouped_gemm": (0, []),
+    "rocwmma_topk_softmax": (3, ["1024", "64", "5"]),
+    "rocwmma_moe_sorting": (3, ["1024", "32", "4"]),
+    "rocwmma_fused_moe": (5, ["256", "1024", "2048", "8", "2"]),
+}
+
+
+def _gpu_visible() -> bool:
+    try:
+        import torch
+        return torch.cuda.device_count() > 0
+    except Exception:
+        return False
+
+
+def run(name, *args, timeout=60):
+    exe = BIN / name
+    if not exe.exists():
+        pytest.skip(f"{exe} not built (python -m optimized_rocwmma_samples_amd.build)")
+    return subprocess.run([str(exe), *args], stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                          text=True, timeout=timeout)
+
+
+@pytest.mark.parametrize("name", sorted(CLIS))
+def test_help(name):
+    r = run(name, "--help")
+    assert r.returncode == 0 and r.stdout.startswith(f"usage: {name}")
+
+
+@pytest.mark.parametrize("name", sorted(CLIS))
+def test_argument_errors(name):
+    count, good = CLIS[name]
+    bad_lists = [["--no-such-option"], good + ["7"]]
+    if count:
+        bad_lists += [good[:-1], good[:-1] + ["x"], good[:-1] + ["0"], good[:-1] + ["-5"],
+                      good[:-1] + ["2147483648"], good[:-1] + ["12abc"]]
+    for args in bad_lists:
+        r = run(name, *args)
+        assert r.returncode == 1, (args, r.returncode, r.stdout, r.stderr)
+        assert "[ERROR]" in r.stderr and f"usage: {name}" in r.stderr, (args, r.stderr)
+        assert r.stdout == "", (args, r.stdout)  # nothing ran
+
+
+@pytest.mark.parametrize("name", ["rocwmma_topk_softmax", "rocwmma_moe_sorting"])
+def test_topk_over_experts(name):
+    r = run(name, "64", "4", "5")
+    assert r.returncode == 1 and "TOPK must not exceed EXPERTS" in r.stderr
+
+
+def test_fused_moe_topk_over_experts():
+    r = run("rocwmma_fused_moe", "64", "256", "512", "4", "5")
+    assert r.returncode == 1 and "TOPK must not exceed EXPERTS" in r.stderr
+
+
+@pytest.mark.skipif(_gpu_visible(), reason="a GPU is visible: the CLI would run for real")
+@pytest.mark.parametrize("name", sorted(CLIS))
+def test_no_device_exits_1(name):
+    r = run(name, *CLIS[name][1])
+    assert r.returncode == 1 and "HIP" in r.stderr, (r.returncode, r.stderr)
+
+
+# ---------------------------------------------------------------- the runner
+@pytest.mark.parametrize("line,desc,expect", [
+    ("[SmoothQuant] M=3328 N=4096  0.0104 ms  3929.1 GB/s", "d",
+     [("SmoothQuant bw", 3929.1, "GB/s")]),
+    ("[QuantGEMM-INT8] M=4096 N=4096 K=4096  0.065 ms  2116.2 TFlops/s", "d",
+     [("QuantGEMM-INT8", 2116.2, "TFlops/s")]),
+    ("  HGEMM   TFlops/s=591.3", "HGEMM 8192^3", [("HGEMM 8192^3", 591.3, "TFlops/s")]),
+    ("[MoE-SmoothQuant] tokens=3328 hidden=4096 experts=8 topk=2  0.02 ms  2800 GB/s", "d",
+     [("MoE-SmoothQuant bw", 2800.0, "GB/s")]),
+    ("Device: AMD Instinct MI355X  (gfx950)", "d", []),
+    ("  PASSED  q mismatches=0", "d", []),
+])
+def test_scrape(line, desc, expect):
+    got = [(r.metric, r.value, r.unit) for r in B.scrape(line, desc)]
+    assert got == expect
+
+
+def _stub(path: Path, body: str) -> None:
+    path.write_text("#!/bin/sh\n" + body + "\n")
+    path.chmod(0o755)
+
+
+def test_runner_outcomes(tmp_path):
+    bindir = tmp_path / "bin"
+    bindir.mkdir()
+    _stub(bindir / "rocwmma_smoothquant",
+          'echo "[SmoothQuant] M=$1 N=$2  0.010 ms  4000 GB/s"')
+    _stub(bindir / "rocwmma_gemm_quantized", 'echo "[QuantGEMM-INT8] M=1  1 ms  2500 TFlops/s"; exit 3')
+    _stub(bindir / "rocwmma_topk_softmax", 'echo "[TopK-Softmax] 1 ms 30 GB/s"; echo "  FAILED  ids"')
+    _stub(bindir / "rocwmma_moe_sorting", "sleep 20")
+    out = tmp_path / "report.txt"
+    rc = B.main(["-b", str(bindir), "-o", str(out), "--csv", "--timeout", "2", "-s",
+                 "rocwmma_smoothquant,rocwmma_gemm_quantized,rocwmma_topk_softmax,"
+                 "rocwmma_moe_sorting,rocwmma_flatmm"])
+    assert rc == 1  # a failure and a timeout
+    text = out.read_text()
+    n_sq = sum(1 for e in B.SUITE if "rocwmma_smoothquant" in e.binary)
+    n_gq = sum(1 for e in B.SUITE if "rocwmma_gemm_quantized" in e.binary)
+    assert text.count("[PASS]") == n_sq
+    assert text.count("[FAIL]") == n_gq + 1  # exit 3 (each entry) + the FAILED line
+    assert text.count("[TIMEOUT]") == 1 and text.count("[SKIP]") == 1  # sleep; no flatmm stub
+    rows = list(csv.reader(out.with_suffix(".csv").read_text().splitlines()))
+    assert rows[0] == ["sample", "description", "metric", "value", "unit", "pct_peak"]
+    body = rows[1:]
+    assert len(body) == n_sq and all(r[0] == "rocwmma_smoothquant" for r in body)
+    assert body[0][2:] == ["SmoothQuant bw", "4000", "GB/s", "50.0"]
+
+
+def test_runner_missing_build_dir(tmp_path):
+    assert B.main(["-b", str(tmp_path / "nope"), "-o", str(tmp_path / "r.txt")]) == 1
+
+
+def test_runner_all_pass_exit_0(tmp_path):
+    bindir = tmp_path / "bin"
+    bindir.mkdir()
+    _stub(bindir / "rocwmma_grouped_gemm", 'echo "[GroupedGEMM] G=4  1 ms  1400 TFlops/s"')
+    rc = B.main(["-b", str(bindir), "-o", str(tmp_path / "r.txt"), "-s", "rocwmma_grouped_gemm"])
+    assert rc == 0
+
+
+def test_shell_entry_points_exist():
+    pkg = ROOT / "optimized_rocwmma_samples_amd"
+    for name in ("build.sh", "benchmark.sh"):
+        assert os.access(pkg / name, os.X_OK), name
+    r = subprocess.run([str(pkg / "build.sh"), "-g", "gfx942"], stdout=subprocess.PIPE,
+                       stderr=subprocess.PIPE, text=True, timeout=60)
+    assert r.returncode == 1 and "gfx950" in r.stderr

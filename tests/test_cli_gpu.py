@@ -1,0 +1,69 @@
+"""The sample CLIs on the GPU: every CLI in bin/ runs a small case with its CPU
+check on (--verify), ends with status 0, prints PASSED and no FAILED, and each
+of its result lines scrapes by the reference runner's rules
+(benchmark.sh:178-189) into at least one value.  The runner itself runs two
+entries end to end and writes its CSV."""
+from __future__ import annotations
+
+import csv
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+BIN = ROOT / "optimized_rocwmma_samples_amd" / "bin"
+sys.path.insert(0, str(ROOT))
+
+from optimized_rocwmma_samples_amd import benchmark as B  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    ("rocwmma_smoothquant", ["256", "4096"]),
+    ("rocwmma_moe_smoothquant", []),
+    ("rocwmma_rmsnorm2d", ["256", "4096"]),
+    ("rocwmma_gemm_quantized", ["512", "512", "512"]),
+    ("rocwmma_gemm_quantized", ["384", "256", "320", "--sample-layout"]),
+    ("w8a8_fused_sq_gemm", ["512", "4096", "4096"]),
+    ("rocwmma_gemm_splitk", ["16", "4096", "4096"]),
+    ("rocwmma_gemm_splitk", ["512", "512", "16384"]),
+    ("rocwmma_flatmm", ["64", "4096", "4096"]),
+    ("rocwmma_flatmm", ["512", "4096", "4096"]),
+    ("rocwmma_grouped_gemm", []),
+    ("rocwmma_topk_softmax", ["1024", "64", "5"]),
+    ("rocwmma_moe_sorting", ["1024", "32", "4"]),
+    ("rocwmma_fused_moe", ["256", "1024", "2048", "8", "2"]),
+]
+
+
+@pytest.mark.parametrize("name,args", CASES, ids=[f"{n}-{'_'.join(a) or 'defaults'}"
+                                                  for n, a in CASES])
+def test_cli_verify(gpu, name, args):
+    exe = BIN / name
+    assert exe.exists(), f"{exe} not built"
+    print(f"running {name} {' '.join(args)} --verify", flush=True)
+    r = subprocess.run([str(exe), *args, "--verify"], stdout=subprocess.PIPE,
+                       stderr=subprocess.STDOUT, text=True, timeout=110)
+    assert r.returncode == 0, r.stdout[-3000:]
+    lines = r.stdout.splitlines()
+    assert any(l.strip().startswith("PASSED") for l in lines), r.stdout[-3000:]
+    assert not any(l.strip().startswith("FAILED") for l in lines), r.stdout[-3000:]
+    # every timed line (" ms ") carries a value the runner scrapes; a label
+    # line of its own (the grouped CLI's group list) carries none
+    timed = [l for l in lines if " ms " in l]
+    assert timed, r.stdout[-3000:]
+    for l in timed:
+        assert B.scrape(l, name), l
+
+
+def test_runner_end_to_end(gpu, tmp_path):
+    out = tmp_path / "report.txt"
+    rc = B.main(["-o", str(out), "--csv", "--verify", "--timeout", "110",
+                 "-s", "rocwmma_smoothquant,rocwmma_topk_softmax"])
+    assert rc == 0, out.read_text()[-3000:]
+    rows = list(csv.reader(out.with_suffix(".csv").read_text().splitlines()))
+    assert rows[0] == ["sample", "description", "metric", "value", "unit", "pct_peak"]
+    assert {r[0] for r in rows[1:]} == {"rocwmma_smoothquant", "rocwmma_topk_softmax"}
+    assert all(float(r[3]) > 0 for r in rows[1:])

@@ -252,3 +252,60 @@ def test_fused_sq_gemm(w8a8, gpu):
     qo, ro = O.smoothquant(x, s)
     assert np.array_equal(host(q), qo) and np.array_equal(host(r), ro)
     assert_f16_bitexact(host(c), O.dequant_f16(O.gemm_i32(qo, w), ro, sb))
+
+
+# fused SmoothQuant + W8A8 GEMM on the Llama-3-8B
+# projections at M in {512, 2048, 8192}.  These are the headline launches:
+# at M = 8192 qkv / o_proj / gate_up (K = 4096, 32 k-tiles) run the persistent
+# kernel and down (K = 14336) the one-tile-per-block kernel; at M = 512 the
+# small tiles with the K split (workspace allocated as the bench does).
+# q and r are checked in full; c is checked bit-exact on the first and last
+# tile rows (256 rows each) plus 256 seeded random rows.
+CFG3_PROJECTIONS = [("qkv", 4096, 6144), ("o_proj", 4096, 4096), ("gate_up", 4096, 28672),
+                    ("down", 14336, 4096)]
+CFG3_M = [512, 2048, 8192]
+_cfg3_cache: dict = {}
+
+
+def cfg3_inputs(k, n):
+    """Seeded cfg3 inputs at the largest M (smaller M take the first rows:
+    every element is a function of its flat index)."""
+    seed = G.config_seed(3)
+    if ("x", k) not in _cfg3_cache:
+        _cfg3_cache[("x", k)] = G.activations(seed, max(CFG3_M), k)
+        _cfg3_cache[("s", k)] = G.uniform(seed, G.TID_S, (k,), 0.5, 2.0)
+    if ("w", n, k) not in _cfg3_cache:
+        _cfg3_cache[("w", n, k)] = G.int8(seed, G.TID_B, (n, k))
+        _cfg3_cache[("sb", n, k)] = G.uniform(seed, G.TID_SB, (n,), 1e-3, 1e-2)
+    return (_cfg3_cache[("x", k)], _cfg3_cache[("s", k)], _cfg3_cache[("w", n, k)],
+            _cfg3_cache[("sb", n, k)])
+
+
+def cfg3_rows(m, seed):
+    tile = 256
+    rng = np.random.default_rng(seed)
+    return np.unique(np.concatenate([np.arange(min(tile, m)), np.arange(max(0, m - tile), m),
+                                     rng.integers(0, m, 256)]))
+
+
+@pytest.mark.parametrize("m", CFG3_M)
+@pytest.mark.parametrize("name,k,n", CFG3_PROJECTIONS)
+def test_config3_fused_projection(w8a8, gpu, name, k, n, m):
+    import torch
+    xf, s, w, sb = cfg3_inputs(k, n)
+    x = xf[:m]
+    wd, sbd = dev(w, gpu), dev(sb, gpu)
+    c, q, r = w8a8.fused_sq_gemm(dev(x, gpu), dev(s, gpu), wd, sbd)
+    qo, ro = O.smoothquant(x, s)
+    assert np.array_equal(host(q), qo), f"{name} m={m}: quantized activations differ"
+    assert np.array_equal(host(r).view(np.uint32), ro.view(np.uint32)), f"{name} m={m}: row scales"
+    rows = cfg3_rows(m, m + k + n)
+    rows_d = torch.from_numpy(rows).to(gpu)
+    got = host(c.index_select(0, rows_d))
+    acc = O.gemm_i32(np.ascontiguousarray(qo[rows]), w)
+    assert_f16_bitexact(got, O.dequant_f16(acc, ro[rows], sb))
+    if w8a8.gemm_workspace_size(m, n, k) > 0:
+        # the K-split launch (workspace) equals the unsplit one everywhere
+        none = torch.empty(0, dtype=torch.uint8, device=gpu)
+        c2, _, _ = w8a8.fused_sq_gemm(dev(x, gpu), dev(s, gpu), wd, sbd, workspace=none)
+        assert torch.equal(c.view(torch.int16), c2.view(torch.int16)), f"{name} m={m}: split"
