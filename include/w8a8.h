@@ -160,6 +160,31 @@ int w8a8_gemm(uint32_t m, uint32_t n, uint32_t k, const int8_t* a, const int8_t*
               int layout, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * Bytes of the per-GPU scratch array w8a8_gemm_noalloc uses (32 MiB).
+ */
+#define W8A8_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/*
+ * w8a8_gemm without a workspace argument and without any allocation: the
+ * workspace w8a8_gemm would take (K-split partials, the sample layout's
+ * repack) is a scratch array the library holds on each GPU it runs on, of
+ * W8A8_NOALLOC_SCRATCH_BYTES, kept until the process ends.  Results are
+ * bit-identical to w8a8_gemm given a workspace of that size.  Shapes whose
+ * w8a8_gemm_workspace_size exceeds it return W8A8_ERROR_INVALID_VALUE
+ * before any HIP call.  The entry point calls no allocating routine (no
+ * hipMalloc / hipFree), for callers that cannot allocate: code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation.
+ * Every call on one GPU shares that GPU's array, and nothing in it needs
+ * clearing between calls (each call writes what it reads); calls that overlap
+ * on one GPU (several streams, several host threads) race on it and must be
+ * ordered.  No counterpart in the reference.
+ */
+int w8a8_gemm_noalloc(uint32_t m, uint32_t n, uint32_t k, const int8_t* a, const int8_t* b,
+                      void* c, uint32_t lda, uint32_t ldb, uint32_t ldc, const float* scale_a,
+                      const float* scale_b, float tensor_scale_a, float tensor_scale_b,
+                      int out_type, int layout, hipStream_t stream);
+
+/*
  * Fused SmoothQuant + W8A8 GEMM for one linear layer:
  *   (q, r) = smoothquant(x, smooth_scale)       q int8 [m, k], r fp32 [m]
  *   c      = half((float(q . w^T) * r[m]) * scale_w[n])

@@ -257,7 +257,7 @@ static int validate_gemm(const char* fn, uint32_t m, uint32_t n, uint32_t k, con
     return W8A8_SUCCESS;
 }
 
-// w8a8_gemm body (arguments validated by the caller; `fn`
+// w8a8_gemm and w8a8_gemm_noalloc (arguments validated by the caller; `fn`
 // names the entry point in error messages).
 static int gemm_entry(const char* fn, uint32_t m, uint32_t n, uint32_t k, const int8_t* a,
                       const int8_t* b, void* c, uint32_t lda, uint32_t ldb, uint32_t ldc,
@@ -311,6 +311,26 @@ int w8a8_gemm(uint32_t m, uint32_t n, uint32_t k, const int8_t* a, const int8_t*
                       tensor_scale_b, out_type, layout, workspace, workspace_bytes, stream);
 }
 
+int w8a8_gemm_noalloc(uint32_t m, uint32_t n, uint32_t k, const int8_t* a, const int8_t* b,
+                      void* c, uint32_t lda, uint32_t ldb, uint32_t ldc, const float* scale_a,
+                      const float* scale_b, float tensor_scale_a, float tensor_scale_b,
+                      int out_type, int layout, hipStream_t stream)
+{
+    const char* fn = "w8a8_gemm_noalloc";
+    int         rc = validate_gemm(fn, m, n, k, a, b, c, lda, ldb, ldc, out_type, layout);
+    if(rc != W8A8_SUCCESS) return rc;
+    const size_t need = w8a8_gemm_workspace_size(m, n, k, layout);
+    if(need > W8A8_NOALLOC_SCRATCH_BYTES)
+        return fail(W8A8_ERROR_INVALID_VALUE,
+                    "%s: m=%u n=%u k=%u needs %zu bytes of scratch, the library holds %zu per GPU "
+                    "(call w8a8_gemm with a workspace instead)",
+                    fn, m, n, k, need, (size_t)W8A8_NOALLOC_SCRATCH_BYTES);
+    void*      scratch = nullptr;
+    hipError_t e       = w8a8::noalloc_scratch(&scratch);
+    if(e != hipSuccess) return hip_status(e, fn);
+    return gemm_entry(fn, m, n, k, a, b, c, lda, ldb, ldc, scale_a, scale_b, tensor_scale_a,
+                      tensor_scale_b, out_type, layout, scratch, W8A8_NOALLOC_SCRATCH_BYTES, stream);
+}
 
 int w8a8_fused_sq_gemm(const void* x, const float* smooth_scale, const int8_t* w,
                        const float* scale_w, void* c, uint32_t m, uint32_t n, uint32_t k,

@@ -538,4 +538,35 @@ hipError_t launch_transpose_i8(const int8_t* src, uint32_t lds_src, int8_t* dst,
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Scratch of w8a8_gemm_noalloc: a file-scope device array.  Every GPU that
+// loads this code object holds its own copy until the process ends; host code
+// uses it only through the device address hipGetSymbolAddress returns, looked
+// up once per device with that device current (the array's name is a host
+// stand-in, not a device address).  The K-split partials that live in it are
+// written in full before they are read, so nothing is cleared between calls;
+// calls that overlap on one GPU share the array and race.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) int8_t scratch[W8A8_NOALLOC_SCRATCH_BYTES];
+
+hipError_t noalloc_scratch(void** ptr)
+{
+    constexpr int      kMaxDevices = 64;
+    static std::mutex  mu;
+    static void*       addr[kMaxDevices] = {};
+    int                dev               = 0;
+    hipError_t         e                 = hipGetDevice(&dev);
+    if(e != hipSuccess) return e;
+    if(dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if(addr[dev] == nullptr) {
+        void* p = nullptr;
+        e       = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if(e != hipSuccess) return e;
+        addr[dev] = p;
+    }
+    *ptr = addr[dev];
+    return hipSuccess;
+}
+
 } // namespace w8a8

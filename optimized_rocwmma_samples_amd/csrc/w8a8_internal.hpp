@@ -68,6 +68,9 @@ bool       gemm_fast_path_ok(const GemmArgs& g);
 // fill at most half the CUs and ws_bytes >= gemm_nk_workspace_bytes(g).
 hipError_t launch_gemm_nk(const GemmArgs& g, void* ws, size_t ws_bytes, hipStream_t stream);
 size_t     gemm_nk_workspace_bytes(const GemmArgs& g);
+// Device address of the current GPU's W8A8_NOALLOC_SCRATCH_BYTES scratch
+// array (resolved once per device; gemm_i8.hip).
+hipError_t noalloc_scratch(void** ptr);
 
 // Decode kernel (m <= kDecodeMaxM): weights streamed once, split-K across the
 // waves of a block.  `packed`: g.b holds packed weights (g.ldb unused).
