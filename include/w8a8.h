@@ -160,6 +160,27 @@ int w8a8_gemm(uint32_t m, uint32_t n, uint32_t k, const int8_t* a, const int8_t*
               int layout, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * Stream-K GEMM: replaces streamk_gemm_kernel + streamk_reduce_kernel
+ * (rocwmma_streamk_gemm.cpp:86-211, host :213-284).  Same arithmetic and
+ * arguments as w8a8_gemm, primary layout only (A [m, lda] row-major, B
+ * [n, ldb] K-contiguous, 16-byte aligned, lda, ldb, k multiples of 16, A and
+ * B each under 2 GiB).  All tiles' k-tiles are cut into `blocks` contiguous
+ * equal ranges (0: one per CU; never more than the problem's k-tiles), one
+ * block each, as the reference sample's units_per_cta (:223-226); a tile
+ * covered by several blocks is summed in int32 by the last of them to finish
+ * (one launch, no host synchronisation), so C equals w8a8_gemm's bit for bit.
+ * workspace: 16-byte aligned, w8a8_gemm_streamk_workspace_size bytes (tile
+ * counters and partials; cleared by the call itself, no memset).  Calls
+ * sharing a workspace must be ordered on one stream.
+ */
+size_t w8a8_gemm_streamk_workspace_size(uint32_t m, uint32_t n, uint32_t k, uint32_t blocks);
+int w8a8_gemm_streamk(uint32_t m, uint32_t n, uint32_t k, const int8_t* a, const int8_t* b,
+                      void* c, uint32_t lda, uint32_t ldb, uint32_t ldc, const float* scale_a,
+                      const float* scale_b, float tensor_scale_a, float tensor_scale_b,
+                      int out_type, uint32_t blocks, void* workspace, size_t workspace_bytes,
+                      hipStream_t stream);
+
+/*
  * Bytes of the per-GPU scratch array w8a8_gemm_noalloc uses (32 MiB).
  */
 #define W8A8_NOALLOC_SCRATCH_BYTES (32u << 20)

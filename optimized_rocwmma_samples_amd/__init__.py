@@ -35,6 +35,7 @@ from ._lib import (  # noqa: F401
 
 __all__ = [
     "library", "version", "smoothquant", "moe_smoothquant", "gemm", "gemm_workspace_size",
+    "gemm_streamk",
     "fused_sq_gemm", "W8A8Error", "PackedWeights", "pack_weights", "pack_weights_size",
     "gemm_packed", "gemm_packed_workspace_size", "fused_sq_gemm_packed", "grouped_gemm",
     "topk_softmax", "moe_sort", "moe_sort_workspace_size", "moe_gemm", "moe_gemm_workspace_size", "moe_silu_mul_quant",
@@ -222,6 +223,28 @@ def gemm(a, b, scale_a=None, scale_b=None, tensor_scale_a: float = 1.0,
     _lib.call("w8a8_gemm", m, n, k, _ptr(a), _ptr(b), _ptr(c), lda, ldb, c.stride(0),
               _ptr(scale_a), _ptr(scale_b), float(tensor_scale_a), float(tensor_scale_b), otype,
               layout, _ptr(workspace), workspace.numel() if workspace is not None else 0,
+              _stream(a.device))
+    return c
+
+
+def gemm_streamk(a, b, scale_a=None, scale_b=None, tensor_scale_a: float = 1.0,
+                 tensor_scale_b: float = 1.0, out_dtype=None, blocks: int = 0, out=None,
+                 workspace=None):
+    """w8a8_gemm_streamk: the GEMM of gemm() (a int8 [M, K], b int8 [N, K]) with
+    every tile's k-tiles cut into `blocks` equal ranges (0: one per CU)."""
+    torch = _torch()
+    _require_cuda(a, b, scale_a, scale_b)
+    out_dtype = out_dtype or torch.float16
+    m, k = a.shape
+    n = b.shape[0]
+    c = out if out is not None else torch.empty((m, n), dtype=out_dtype, device=a.device)
+    otype = OUT_I32 if c.dtype == torch.int32 else OUT_F16
+    if workspace is None:
+        ws_bytes = int(library().w8a8_gemm_streamk_workspace_size(m, n, k, blocks))
+        workspace = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=a.device)
+    _lib.call("w8a8_gemm_streamk", m, n, k, _ptr(a), _ptr(b), _ptr(c), a.stride(0), b.stride(0),
+              c.stride(0), _ptr(scale_a), _ptr(scale_b), float(tensor_scale_a),
+              float(tensor_scale_b), otype, blocks, _ptr(workspace), workspace.numel(),
               _stream(a.device))
     return c
 

@@ -58,6 +58,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                          _f32, _i32, _i32, _ptr, _size, _ptr]),
     "w8a8_gemm_noalloc": (_i32, [_u32, _u32, _u32, _ptr, _ptr, _ptr, _u32, _u32, _u32, _ptr, _ptr,
                                  _f32, _f32, _i32, _i32, _ptr]),
+    "w8a8_gemm_streamk_workspace_size": (_size, [_u32, _u32, _u32, _u32]),
+    "w8a8_gemm_streamk": (_i32, [_u32, _u32, _u32, _ptr, _ptr, _ptr, _u32, _u32, _u32, _ptr, _ptr,
+                                 _f32, _f32, _i32, _u32, _ptr, _size, _ptr]),
     "w8a8_fused_sq_gemm": (_i32, [_ptr, _ptr, _ptr, _ptr, _ptr, _u32, _u32, _u32, _u32, _u32,
                                   _u32, _ptr, _ptr, _ptr, _size, _ptr]),
     "w8a8_pack_weights_size": (_size, [_u32, _u32]),

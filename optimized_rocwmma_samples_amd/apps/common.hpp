@@ -56,9 +56,17 @@ namespace app {
 struct Options {
     bool                     verify = false;
     std::vector<std::string> pos;   // positional arguments
-    std::vector<std::string> flags; // extra flags given (from the CLI's list)
+    std::vector<std::string> flags; // extra flags given (from the CLI's list), "--name=value" whole
     const char*              usage = "";
     bool has(const char* f) const { return std::find(flags.begin(), flags.end(), f) != flags.end(); }
+    // value of "--name=value" for an extra flag listed as "--name="; nullptr if absent
+    const char* value(const char* f) const
+    {
+        const std::string pre = f;
+        for(const std::string& g : flags)
+            if(g.compare(0, pre.size(), pre) == 0) return g.c_str() + pre.size();
+        return nullptr;
+    }
 };
 
 [[noreturn]] inline void usage_error(const Options& o, const std::string& msg)
@@ -87,7 +95,11 @@ inline Options parse(int argc, char** argv, const char* usage,
             o.verify = false;
         } else if(a.size() > 1 && a[0] == '-') {
             bool known = false;
-            for(const char* f : extra) known = known || a == f;
+            for(const char* f : extra) {
+                const std::string e = f;
+                known = known || a == e
+                        || (!e.empty() && e.back() == '=' && a.compare(0, e.size(), e) == 0);
+            }
             if(!known) usage_error(o, "unknown option " + a);
             o.flags.push_back(a);
         } else {

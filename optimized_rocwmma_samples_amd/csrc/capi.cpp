@@ -332,6 +332,36 @@ int w8a8_gemm_noalloc(uint32_t m, uint32_t n, uint32_t k, const int8_t* a, const
                       tensor_scale_b, out_type, layout, scratch, W8A8_NOALLOC_SCRATCH_BYTES, stream);
 }
 
+size_t w8a8_gemm_streamk_workspace_size(uint32_t m, uint32_t n, uint32_t k, uint32_t blocks)
+{
+    return w8a8::streamk_workspace_bytes(m, n, k, blocks);
+}
+
+int w8a8_gemm_streamk(uint32_t m, uint32_t n, uint32_t k, const int8_t* a, const int8_t* b,
+                      void* c, uint32_t lda, uint32_t ldb, uint32_t ldc, const float* scale_a,
+                      const float* scale_b, float tensor_scale_a, float tensor_scale_b,
+                      int out_type, uint32_t blocks, void* workspace, size_t workspace_bytes,
+                      hipStream_t stream)
+{
+    const char* fn = "w8a8_gemm_streamk";
+    int rc = validate_gemm(fn, m, n, k, a, b, c, lda, ldb, ldc, out_type, W8A8_LAYOUT_A_ROW_B_NK);
+    if(rc != W8A8_SUCCESS) return rc;
+    w8a8::GemmArgs g{m, n, k, a, b, c, lda, ldb, ldc, scale_a, scale_b,
+                     tensor_scale_a, tensor_scale_b, out_type};
+    if(!w8a8::streamk_shape_ok(g))
+        return fail(W8A8_ERROR_INVALID_VALUE,
+                    "%s: needs 16-byte aligned a/b, lda, ldb, k %% 16 == 0 and A, B under 2 GiB "
+                    "(m=%u n=%u k=%u lda=%u ldb=%u)",
+                    fn, m, n, k, lda, ldb);
+    const size_t need = w8a8::streamk_workspace_bytes(m, n, k, blocks);
+    if(workspace == nullptr || workspace_bytes < need)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: workspace of %zu bytes, %zu needed", fn,
+                    workspace ? workspace_bytes : (size_t)0, need);
+    if(reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: workspace must be 16-byte aligned", fn);
+    return hip_status(w8a8::launch_gemm_streamk(g, blocks, workspace, stream), fn);
+}
+
 int w8a8_fused_sq_gemm(const void* x, const float* smooth_scale, const int8_t* w,
                        const float* scale_w, void* c, uint32_t m, uint32_t n, uint32_t k,
                        uint32_t ldx, uint32_t ldw, uint32_t ldc, int8_t* q, float* row_scale,

@@ -9,6 +9,7 @@
 #include "gemm_i8_kernel.hpp"
 #include "gemm_i8_pb_kernel.hpp"
 #include "gemm_i8_persist_kernel.hpp"
+#include "gemm_i8_streamk_kernel.hpp"
 #include "w8a8_internal.hpp"
 
 #include <algorithm>
@@ -453,6 +454,44 @@ size_t gemm_nk_workspace_bytes(const GemmArgs& g)
     return dense_split(g.m, g.n, g.k).bytes;
 }
 
+// One 256 x 256 launch (a panel).  When its tiles make whole rounds over the
+// CUs plus a last round at most half full, and the whole rounds are whole
+// columns of tiles, the columns of the last round run as 128 x 256 tiles in
+// a launch of their own: twice the tiles, each half the work, so that round
+// keeps every CU busy for about half as long (cfg3 gate_up at M = 2048:
+// 8 x 112 tiles = 3 rounds + 128 tiles; the last 16 columns become one
+// round of 256 tiles of 128 x 256).  The same k-order per output, so the
+// result is bit-identical to the single launch.
+hipError_t launch_main(const KArgs& p, int out_type, int vec_ok, hipStream_t stream)
+{
+    const uint32_t cus   = device_cus();
+    const uint32_t tm    = (p.m + GemmMain::kBM - 1) / GemmMain::kBM;
+    const uint32_t tiles = tm * ((p.n + GemmMain::kBN - 1) / GemmMain::kBN);
+    const uint32_t full = tiles / cus, rest = tiles % cus;
+    const uint32_t mid_rows = (p.m + GemmMidM::kBM - 1) / GemmMidM::kBM;
+    if(full >= 1 && rest > 0 && rest * 2 <= cus && (full * cus) % tm == 0) {
+        const uint32_t n1   = full * cus / tm * GemmMain::kBN; // < p.n: rest > 0
+        const uint32_t n2   = p.n - n1;
+        const size_t   esz  = out_type == W8A8_OUT_I32 ? 4 : 2;
+        if((uint64_t)mid_rows * ((n2 + GemmMidM::kBN - 1) / GemmMidM::kBN) <= cus) {
+            KArgs head = p, tail = p;
+            head.n     = n1;
+            tail.n     = n2;
+            tail.b     = p.b + (size_t)n1 * p.ldb;
+            tail.c     = static_cast<int8_t*>(p.c) + (size_t)n1 * esz;
+            tail.sb    = p.sb ? p.sb + n1 : nullptr;
+            hipError_t e = persist_pays(head, out_type, vec_ok)
+                               ? gemm::launch_cfg_persist<GemmMain>(head, vec_ok, cus, stream)
+                               : gemm::launch_cfg<GemmMain>(head, out_type, vec_ok, stream);
+            if(e != hipSuccess) return e;
+            return gemm::launch_cfg<GemmMidM>(tail, out_type, vec_ok, stream);
+        }
+    }
+    return persist_pays(p, out_type, vec_ok)
+               ? gemm::launch_cfg_persist<GemmMain>(p, vec_ok, cus, stream)
+               : gemm::launch_cfg<GemmMain>(p, out_type, vec_ok, stream);
+}
+
 hipError_t launch_gemm_nk(const GemmArgs& g, void* ws, size_t ws_bytes, hipStream_t stream)
 {
     if(g.m == 0 || g.n == 0) return hipSuccess;
@@ -498,11 +537,7 @@ hipError_t launch_gemm_nk(const GemmArgs& g, void* ws, size_t ws_bytes, hipStrea
             p.sb    = g.scale_b ? g.scale_b + n0 : nullptr;
             hipError_t e;
             switch(pick_tile_cfg(p.m, p.n)) {
-            case TileCfg::kMain:
-                e = persist_pays(p, g.out_type, vec_ok)
-                        ? gemm::launch_cfg_persist<GemmMain>(p, vec_ok, device_cus(), stream)
-                        : gemm::launch_cfg<GemmMain>(p, g.out_type, vec_ok, stream);
-                break;
+            case TileCfg::kMain: e = launch_main(p, g.out_type, vec_ok, stream); break;
             case TileCfg::kMidM: e = gemm::launch_cfg<GemmMidM>(p, g.out_type, vec_ok, stream); break;
             case TileCfg::kSmall: e = gemm::launch_cfg<GemmSmall>(p, g.out_type, vec_ok, stream); break;
             default: e = gemm::launch_cfg<GemmDecTile>(p, g.out_type, vec_ok, stream); break;
@@ -511,6 +546,73 @@ hipError_t launch_gemm_nk(const GemmArgs& g, void* ws, size_t ws_bytes, hipStrea
         }
     }
     return hipSuccess;
+}
+
+namespace {
+
+// Explicit stream-K (w8a8_gemm_streamk): every tile of the problem in the
+// stream-K schedule over `blocks` blocks (0: one per CU), the reference
+// sample's decomposition (rocwmma_streamk_gemm.cpp:223-226).  The tile is
+// the largest of 256 x 256, 128 x 256 and 128 x 128 that leaves each block
+// at least 8 k-tiles (else 128 x 128); never more blocks than k-tiles.
+struct ExplicitSk {
+    TileCfg      cfg;
+    gemm::SkPlan plan;
+    size_t       bytes;
+};
+
+ExplicitSk explicit_streamk(uint32_t m, uint32_t n, uint32_t k, uint32_t blocks)
+{
+    const uint32_t G  = blocks ? blocks : device_cus();
+    const uint32_t nk = (k + 127) / 128;
+    auto plan = [&](uint32_t bm, uint32_t bn) {
+        const uint32_t tiles = ((m + bm - 1) / bm) * ((n + bn - 1) / bn);
+        return gemm::SkPlan{nk, tiles, (uint32_t)std::min<uint64_t>(G, (uint64_t)tiles * nk)};
+    };
+    ExplicitSk e{TileCfg::kMain, plan(GemmMain::kBM, GemmMain::kBN), 0};
+    if(e.plan.total() < 8ull * G) e = ExplicitSk{TileCfg::kMidM, plan(GemmMidM::kBM, GemmMidM::kBN), 0};
+    if(e.plan.total() < 8ull * G) e = ExplicitSk{TileCfg::kSmall, plan(GemmSmall::kBM, GemmSmall::kBN), 0};
+    e.bytes = e.cfg == TileCfg::kMain   ? gemm::sk_workspace_bytes<GemmMain>(e.plan)
+              : e.cfg == TileCfg::kMidM ? gemm::sk_workspace_bytes<GemmMidM>(e.plan)
+                                        : gemm::sk_workspace_bytes<GemmSmall>(e.plan);
+    return e;
+}
+
+} // namespace
+
+bool streamk_shape_ok(const GemmArgs& g)
+{
+    constexpr uint64_t kLimit = 0x7FFFFFFFull;
+    return gemm_fast_path_ok(g) && (uint64_t)g.m * g.lda <= kLimit
+           && (uint64_t)g.n * g.ldb <= kLimit;
+}
+
+size_t streamk_workspace_bytes(uint32_t m, uint32_t n, uint32_t k, uint32_t blocks)
+{
+    if(m == 0 || n == 0 || k == 0) return 0;
+    return explicit_streamk(m, n, k, blocks).bytes;
+}
+
+uint32_t streamk_blocks(uint32_t m, uint32_t n, uint32_t k, uint32_t blocks)
+{
+    if(m == 0 || n == 0 || k == 0) return 0;
+    return explicit_streamk(m, n, k, blocks).plan.blocks;
+}
+
+hipError_t launch_gemm_streamk(const GemmArgs& g, uint32_t blocks, void* ws, hipStream_t stream)
+{
+    if(g.m == 0 || g.n == 0) return hipSuccess;
+    const ExplicitSk e      = explicit_streamk(g.m, g.n, g.k, blocks);
+    const KArgs      p      = make_kargs(g);
+    const int        vec_ok = out_vec_ok(g);
+    switch(e.cfg) {
+    case TileCfg::kMain:
+        return gemm::launch_cfg_streamk<GemmMain>(p, g.out_type, vec_ok, 0, e.plan, ws, stream);
+    case TileCfg::kMidM:
+        return gemm::launch_cfg_streamk<GemmMidM>(p, g.out_type, vec_ok, 0, e.plan, ws, stream);
+    default:
+        return gemm::launch_cfg_streamk<GemmSmall>(p, g.out_type, vec_ok, 0, e.plan, ws, stream);
+    }
 }
 
 hipError_t launch_gemm_generic(const GemmArgs& g, size_t sam, size_t sak, size_t sbn, size_t sbk,

@@ -452,15 +452,16 @@ __device__ __forceinline__ void tile_epilogue_sc(const KArgs& p, uint32_t m0, ui
                                                  const v16i (&acc)[C::kTilesM][C::kTilesN],
                                                  int wave_base, const EpiScales<C>& sc);
 
-// One BM x BN output tile at (m0, n0) of problem p, computed by the whole
-// block; `lds` is the block's kLdsBytes ring.  Shared by the plain, grouped
-// and MoE kernels, which differ only in how a block finds its tile.
-// PART: only k-tiles [kt0, kt0 + nkt) are summed and the int32 accumulators
-// go to `part` (store_partial layout) instead of through the epilogue.
-template <class C, int OUT, bool PART = false>
-__device__ __forceinline__ void gemm_tile(const KArgs& p, uint32_t m0, uint32_t n0, int vec_ok,
-                                          int8_t* lds, uint32_t kt0 = 0, uint32_t nkt = 0,
-                                          int32_t* part = nullptr)
+// The int32 accumulators of one BM x BN output tile at (m0, n0) of problem
+// p over k-tiles [kt0, kt0 + nk) (nk >= 1), computed by the whole block;
+// `lds` is the block's kLdsBytes ring, free again when this returns.
+// SCALES: the fp16 epilogue's scales go into `sc` while the last k-tile's
+// MFMAs run.
+template <class C, bool SCALES>
+__device__ __forceinline__ void gemm_tile_acc(const KArgs& p, uint32_t m0, uint32_t n0,
+                                              int vec_ok, int8_t* lds, uint32_t kt0,
+                                              uint32_t nk, v16i (&acc)[C::kTilesM][C::kTilesN],
+                                              EpiScales<C>& sc)
 {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); // wave-uniform
     const int lane = threadIdx.x % kWave;
@@ -532,7 +533,6 @@ __device__ __forceinline__ void gemm_tile(const KArgs& p, uint32_t m0, uint32_t 
 #pragma unroll
     for(int g = 0; g < C::kSubK; ++g) cofs[g] = ((2 * g + (lane >> 5)) ^ fswz) * 16;
 
-    v16i acc[C::kTilesM][C::kTilesN];
 #pragma unroll
     for(int i = 0; i < C::kTilesM; ++i)
 #pragma unroll
@@ -558,8 +558,6 @@ __device__ __forceinline__ void gemm_tile(const KArgs& p, uint32_t m0, uint32_t 
     };
     constexpr int kMfma = C::kTilesM * C::kTilesN;
     constexpr int kDs   = C::kTilesM + C::kTilesN;
-
-    const uint32_t nk = PART ? nkt : (p.k + C::kBK - 1) / C::kBK;
 
     // ---- prologue: fill every stage of the ring ----------------------------
     // Tiles past K are still issued (every lane then reads kOob: zeros, no
@@ -598,8 +596,7 @@ __device__ __forceinline__ void gemm_tile(const KArgs& p, uint32_t m0, uint32_t 
         interleave_mfma_vmem_ds<kMfma, C::kLoads, kDs, 1>();
     }
     // the fp16 epilogue's scales load while the last tile's MFMAs run
-    EpiScales<C> sc;
-    if constexpr(!PART && OUT == W8A8_OUT_F16) sc.load(p, m0, n0, wm, wn, lane, vec_ok);
+    if constexpr(SCALES) sc.load(p, m0, n0, wm, wn, lane, vec_ok);
     {
         const int8_t* sbase = lds + ((nk - 1) % C::kStages) * C::kStageBytes;
 #pragma unroll
@@ -610,12 +607,28 @@ __device__ __forceinline__ void gemm_tile(const KArgs& p, uint32_t m0, uint32_t 
         mfma_tile(fa[(C::kSubK - 1) & 1], fb[(C::kSubK - 1) & 1]);
     }
     wait_vmcnt<0>(); // no global->LDS write may outlive the workgroup's LDS
+}
 
+// One BM x BN output tile at (m0, n0) of problem p, computed by the whole
+// block; `lds` is the block's kLdsBytes ring.  Shared by the plain, grouped
+// and MoE kernels, which differ only in how a block finds its tile.
+// PART: only k-tiles [kt0, kt0 + nkt) are summed and the int32 accumulators
+// go to `part` (store_partial layout) instead of through the epilogue.
+template <class C, int OUT, bool PART = false>
+__device__ __forceinline__ void gemm_tile(const KArgs& p, uint32_t m0, uint32_t n0, int vec_ok,
+                                          int8_t* lds, uint32_t kt0 = 0, uint32_t nkt = 0,
+                                          int32_t* part = nullptr)
+{
+    v16i         acc[C::kTilesM][C::kTilesN];
+    EpiScales<C> sc;
     if constexpr(PART) {
+        gemm_tile_acc<C, false>(p, m0, n0, vec_ok, lds, kt0, nkt, acc, sc);
         store_partial<C>(part, acc);
-        return;
+    } else {
+        gemm_tile_acc<C, OUT == W8A8_OUT_F16>(p, m0, n0, vec_ok, lds, 0,
+                                              (p.k + C::kBK - 1) / C::kBK, acc, sc);
+        tile_epilogue_sc<C, OUT>(p, m0, n0, vec_ok, lds, acc, 0, sc);
     }
-    tile_epilogue_sc<C, OUT>(p, m0, n0, vec_ok, lds, acc, 0, sc);
 }
 
 // acc[i][j][r]: m = m0 + wm*kWaveM + i*32 + lane%32,
@@ -696,12 +709,16 @@ __global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_tile_kernel(KArgs p, i
     gemm_tile<C, OUT>(p, tm * C::kBM, tn * C::kBN, vec_ok, lds);
 }
 
-// K split of a launch whose tiles fill at most half of the CUs: block b runs
-// piece b % parts of tile b / parts (k-tiles [part * nk / parts,
+// K split of a launch whose tiles fill at most half of the CUs: logical
+// block b runs piece b % parts of tile b / parts (k-tiles [part * nk / parts,
 // (part + 1) * nk / parts)) and stores its int32 accumulators to
 // ws + b * Partial<C>::kInts; gemm_i8_split_fixup_kernel then sums each
 // tile's pieces in order (exact) and runs the tile epilogue, in kPieces
-// blocks of kFixupWaves waves per tile.
+// blocks of kFixupWaves waves per tile.  Logical ids are contiguous per XCD
+// (xcd_remap): the tiles of one XCD share their B panels in its L2, so each
+// weight panel comes from HBM once (with hardware ids the GROUP_M tiles of a
+// panel sat on different XCDs and each fetched it: M=512 K=14336 N=4096 read
+// the weights four times).
 template <class C, int OUT>
 __global__ void __launch_bounds__(C::kThreads, 1)
     gemm_i8_split_kernel(KArgs p, int vec_ok, int32_t* ws, uint32_t parts)
@@ -709,13 +726,14 @@ __global__ void __launch_bounds__(C::kThreads, 1)
     extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
     const uint32_t tiles_m = (p.m + C::kBM - 1) / C::kBM;
     const uint32_t tiles_n = (p.n + C::kBN - 1) / C::kBN;
-    const uint32_t slot = blockIdx.x / parts, part = blockIdx.x % parts;
+    const uint32_t lid  = xcd_remap(blockIdx.x, gridDim.x);
+    const uint32_t slot = lid / parts, part = lid % parts;
     uint32_t       tm, tn;
     tile_coords<C::kGroupM>(slot, tiles_m, tiles_n, tm, tn);
     const uint32_t nk  = (p.k + C::kBK - 1) / C::kBK;
     const uint32_t kt0 = part * nk / parts, kt1 = (part + 1) * nk / parts;
     gemm_tile<C, OUT, true>(p, tm * C::kBM, tn * C::kBN, vec_ok, lds, kt0, kt1 - kt0,
-                            ws + (size_t)blockIdx.x * Partial<C>::kInts);
+                            ws + (size_t)lid * Partial<C>::kInts);
 }
 
 template <class C, int OUT>

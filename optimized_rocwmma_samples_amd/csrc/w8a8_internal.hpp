@@ -68,6 +68,14 @@ bool       gemm_fast_path_ok(const GemmArgs& g);
 // fill at most half the CUs and ws_bytes >= gemm_nk_workspace_bytes(g).
 hipError_t launch_gemm_nk(const GemmArgs& g, void* ws, size_t ws_bytes, hipStream_t stream);
 size_t     gemm_nk_workspace_bytes(const GemmArgs& g);
+// Explicit stream-K over every tile (w8a8_gemm_streamk): `blocks` blocks (0:
+// one per CU, never more than the problem's k-tiles); ws: 16-byte aligned,
+// streamk_workspace_bytes.  Needs gemm_fast_path_ok and A, B under 2 GiB
+// (streamk_shape_ok).
+bool       streamk_shape_ok(const GemmArgs& g);
+size_t     streamk_workspace_bytes(uint32_t m, uint32_t n, uint32_t k, uint32_t blocks);
+uint32_t   streamk_blocks(uint32_t m, uint32_t n, uint32_t k, uint32_t blocks);
+hipError_t launch_gemm_streamk(const GemmArgs& g, uint32_t blocks, void* ws, hipStream_t stream);
 // Device address of the current GPU's W8A8_NOALLOC_SCRATCH_BYTES scratch
 // array (resolved once per device; gemm_i8.hip).
 hipError_t noalloc_scratch(void** ptr);

@@ -28,6 +28,7 @@ CLIS = {
     "rocwmma_gemm_quantized": (3, ["512", "512", "512"]),
     "w8a8_fused_sq_gemm": (3, ["512", "1024", "4096"]),
     "rocwmma_gemm_splitk": (3, ["16", "4096", "4096"]),
+    "rocwmma_streamk_gemm": (3, ["512", "512", "4096"]),
     "rocwmma_flatmm": (3, ["64", "4096", "4096"]),
     "rocwmma_grouped_gemm": (0, []),
     "rocwmma_topk_softmax": (3, ["1024", "64", "5"]),

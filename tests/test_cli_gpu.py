@@ -29,6 +29,8 @@ CASES = [
     ("w8a8_fused_sq_gemm", ["512", "4096", "4096"]),
     ("rocwmma_gemm_splitk", ["16", "4096", "4096"]),
     ("rocwmma_gemm_splitk", ["512", "512", "16384"]),
+    ("rocwmma_streamk_gemm", ["1024", "1024", "4096"]),
+    ("rocwmma_streamk_gemm", ["777", "1234", "4112", "--blocks=333"]),
     ("rocwmma_flatmm", ["64", "4096", "4096"]),
     ("rocwmma_flatmm", ["512", "4096", "4096"]),
     ("rocwmma_grouped_gemm", []),

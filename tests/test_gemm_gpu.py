@@ -67,6 +67,26 @@ def test_tile_configs_exact(w8a8, gpu, m, n, k):
     assert_f16_bitexact(host(c), O.dequant_f16(acc, sa, sb))
 
 
+# 256 x 256 launches of whole rounds plus a last round at most half full,
+# whose whole rounds are whole tile columns: the last round's columns run as
+# 128 x 256 tiles in a second launch (tile counts for 256 CUs).
+COLUMN_TAIL_SHAPES = [
+    (2048, 28672, 256),  # 8 x 112 tiles = 3 rounds + 128: columns 24576.. as 16 x 16 tiles
+    (2000, 17000, 272),  # 8 x 67 = 2 rounds + 24, ragged edges, a K tail: columns 16384..
+]
+
+
+@pytest.mark.parametrize("m,n,k", COLUMN_TAIL_SHAPES)
+def test_column_tail_exact(w8a8, gpu, m, n, k):
+    import torch
+    a, b, sa, sb = inputs(m, n, k, m + n + k)
+    ad, bd = dev(a, gpu), dev(b, gpu)
+    acc = O.gemm_i32(a, b)
+    assert_i32_equal(host(w8a8.gemm(ad, bd, out_dtype=torch.int32)), acc)
+    c = w8a8.gemm(ad, bd, dev(sa, gpu), dev(sb, gpu))
+    assert_f16_bitexact(host(c), O.dequant_f16(acc, sa, sb))
+
+
 # Launches of at least two 256 x 256 tiles per CU with K <= 4096 and an fp16
 # output run the persistent kernel: one block per CU walks its tiles, the
 # stage ring runs across tile boundaries and each tile's epilogue stores stay
