@@ -373,8 +373,11 @@ def bench_cfg3_smaller_m(torch, w8a8, dev, base, steps=10, sets=3):
 def bench_moe(torch, w8a8, dev, gen, iters=10):
     """Config 5: Mixtral-8x7B-shaped MoE FFN, 4096 tokens, hidden 4096, ffn
     14336, 8 experts, top-2.  One iteration = routing, sort, MoE SmoothQuant
-    into expert-sorted rows, gate_up expert GEMM, SiLU(gate)*up requant, down
-    expert GEMM, combine; ops = 2 * 8192 rows * (28672*4096 + 4096*14336)."""
+    into expert-sorted rows, gate_up expert GEMM with the SiLU(gate)*up
+    epilogue and the requantization (weights interleaved once beforehand),
+    down expert GEMM, combine; ops = 2 * 8192 rows * (28672*4096 + 4096*14336).
+    The same layer with the gate_up GEMM and the SiLU requantization as two
+    launches is timed alternately with it, the same way."""
     t, h, inter, e, k = 4096, 4096, 14336, 8, 2
     x = torch.randn((t, h), generator=gen, device=dev)
     cols = torch.randperm(h, generator=gen, device=dev)[: round(0.005 * h)]
@@ -384,6 +387,7 @@ def bench_moe(torch, w8a8, dev, gen, iters=10):
     s = torch.rand((e, h), generator=gen, device=dev) * 1.5 + 0.5
     wgu = torch.randint(-127, 128, (e, 2 * inter, h), generator=gen, device=dev, dtype=torch.int8)
     sgu = torch.rand((e, 2 * inter), generator=gen, device=dev) * 9e-3 + 1e-3
+    wgu_il, sgu_il = w8a8.moe_interleave_gate_up(wgu, sgu)
     wd = torch.randint(-127, 128, (e, h, inter), generator=gen, device=dev, dtype=torch.int8)
     sd = torch.rand((e, h), generator=gen, device=dev) * 9e-3 + 1e-3
     cap = int(w8a8.library().w8a8_moe_sort_capacity(t, k, e, 32))
@@ -395,11 +399,30 @@ def bench_moe(torch, w8a8, dev, gen, iters=10):
     y = torch.empty((cap, h), dtype=torch.float16, device=dev)
     out = torch.empty((t, h), dtype=torch.float16, device=dev)
     ws = torch.empty(w8a8.moe_gemm_workspace_size(e, cap, h, inter), dtype=torch.uint8, device=dev)
+    ws_silu = torch.empty(w8a8.moe_gate_up_silu_workspace_size(cap, inter), dtype=torch.uint8,
+                          device=dev)
     sort_ws = torch.empty(max(1, w8a8.moe_sort_workspace_size(t, k, e)), dtype=torch.uint8,
                           device=dev)
-    stages = ["route", "sort", "quant", "gate_up", "silu_quant", "down", "combine"]
+    stages = ["route", "sort", "quant", "gate_up_silu", "down", "combine"]
 
     def chain(ev=None):
+        mark = (lambda i: ev[i].record()) if ev is not None else (lambda i: None)
+        mark(0)
+        w, ids = w8a8.topk_softmax(logits, k)
+        mark(1)
+        srt = w8a8.moe_sort(ids, e, 32, workspace=sort_ws)
+        mark(2)
+        w8a8.moe_smoothquant(x, s, ids, dst_row=srt["dst_row"], rows=cap, out=qa, row_scale=ra)
+        mark(3)
+        w8a8.moe_gate_up_silu(qa, wgu_il, srt["start"], srt["count"], ra, sgu_il, q=q2,
+                              row_scale=r2, workspace=ws_silu)
+        mark(4)
+        w8a8.moe_gemm(q2, wd, srt["start"], srt["count"], r2, sd, out=y, workspace=ws)
+        mark(5)
+        w8a8.moe_combine(y, w, srt["dst_row"], out=out)
+        mark(6)
+
+    def chain_unfused(ev=None):  # the same layer with the gate_up GEMM and SiLU requant apart
         mark = (lambda i: ev[i].record()) if ev is not None else (lambda i: None)
         mark(0)
         w, ids = w8a8.topk_softmax(logits, k)
@@ -417,26 +440,40 @@ def bench_moe(torch, w8a8, dev, gen, iters=10):
         w8a8.moe_combine(y, w, srt["dst_row"], out=out)
         mark(7)
 
-    for _ in range(2):
+    # both forms alternate, after 0.3 s of them untimed (the clocks settle
+    # under this load), so neither is timed in a different power state
+    stages_u = ["route", "sort", "quant", "gate_up", "silu_quant", "down", "combine"]
+    t_end = time.perf_counter() + 0.3
+    while time.perf_counter() < t_end:
         chain()
-    torch.cuda.synchronize()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)]
-           for _ in range(iters)]
-    for i in range(iters):
-        chain(evs[i])
+        chain_unfused()
+        torch.cuda.synchronize()
+    evs, evu = [], []
+    for rnd in range(iters):
+        for fn, dst, nm in ((chain, evs, len(stages) + 1), (chain_unfused, evu, len(stages_u) + 1))[
+                ::(1 if rnd % 2 == 0 else -1)]:
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(nm)]
+            fn(ev)
+            dst.append(ev)
     torch.cuda.synchronize()
     per = {st: sum(ev[j].elapsed_time(ev[j + 1]) for ev in evs) / iters * 1e3
            for j, st in enumerate(stages)}
-    total_us = sum(evs[i][0].elapsed_time(evs[i][-1]) for i in range(iters)) / iters * 1e3
+    total_us = sum(ev[0].elapsed_time(ev[-1]) for ev in evs) / iters * 1e3
+    unf = {st: sum(ev[j].elapsed_time(ev[j + 1]) for ev in evu) / iters * 1e3
+           for j, st in enumerate(stages_u)}
+    unf_total = sum(ev[0].elapsed_time(ev[-1]) for ev in evu) / iters * 1e3
     rows = t * k
     ops_gu = 2.0 * rows * 2 * inter * h
     ops_d = 2.0 * rows * h * inter
     return {"workload": "cfg5 MoE FFN, Mixtral-8x7B shape: 4096 tokens, hidden 4096, ffn 14336, "
-                        "8 experts, top-2 (routing -> sort -> quant -> gate_up -> SiLU*up requant "
-                        "-> down -> combine)",
+                        "8 experts, top-2 (routing -> sort -> quant -> gate_up GEMM with the "
+                        "SiLU*up epilogue + requant -> down -> combine)",
             "us_per_layer": total_us, "TOPS": (ops_gu + ops_d) / (total_us * 1e-6) / 1e12,
             "stage_us": per,
-            "gate_up_TOPS": ops_gu / (per["gate_up"] * 1e-6) / 1e12,
+            "unfused_us_per_layer": unf_total,
+            "unfused_stage_us": unf,
+            "fused_saving_us": unf["gate_up"] + unf["silu_quant"] - per["gate_up_silu"],
+            "gate_up_silu_TOPS": ops_gu / (per["gate_up_silu"] * 1e-6) / 1e12,
             "down_TOPS": ops_d / (per["down"] * 1e-6) / 1e12,
             "frac_mfma": (ops_gu + ops_d) / (total_us * 1e-6) / PEAK_INT8_OPS}
 
@@ -475,8 +512,9 @@ def measured_peaks(torch, dev, cus):
     lib.w8a8_peak_mfma_ops.argtypes = [ctypes.c_uint32, ctypes.c_uint32]
     lib.w8a8_peak_mfma.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int, ctypes.c_void_p,
                                    ctypes.c_void_p]
-    lib.w8a8_peak_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
-                                   ctypes.c_uint32, ctypes.c_void_p]
+    lib.w8a8_peak_stream.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                     ctypes.c_uint32, ctypes.c_int, ctypes.c_void_p,
+                                     ctypes.c_void_p]
     lib.w8a8_peak_empty.argtypes = [ctypes.c_void_p]
 
     def check(rc, what):
@@ -513,14 +551,31 @@ def measured_peaks(torch, dev, cus):
     nbytes = 1 << 30
     src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(3)
     dst = torch.empty_like(src)
-    best = 0.0
-    for mult in (4, 8, 16):
-        sec = timed(lambda s, b=cus * mult: check(lib.w8a8_peak_copy(src.data_ptr(), dst.data_ptr(),
-                                                                      nbytes, b, s), "peak_copy"), 10)
-        best = max(best, 2 * nbytes / sec / 1e9)
-    out["copy_GBps"] = best
-    out["copy_note"] = "2^30 bytes read + 2^30 bytes written per launch, 16 B per lane access"
+    for mode, key, moved in ((0, "read_GBps", 1.0), (1, "copy_GBps", 2.0), (2, "stream21_GBps", 1.5)):
+        best = 0.0
+        for mult in (2, 4, 8):
+            sec = timed(lambda s, b=cus * mult, md=mode: check(
+                lib.w8a8_peak_stream(src.data_ptr(), dst.data_ptr(), nbytes, b, md,
+                                     sink.data_ptr(), s), "peak_stream"), 10)
+            best = max(best, moved * nbytes / sec / 1e9)
+        out[key] = best
+    out["stream_note"] = ("2^30 bytes read per launch; copy writes 2^30, stream21 writes 2^29 "
+                          "(the quantizer's 2:1 ratio); 16 B per lane access, 8 in flight")
     del src, dst
+    # the 2:1 stream at the cfg1 quantizer's size and launch pattern: 24 buffer
+    # pairs (MALL-cold) used in turn, 48 launches replayed from a graph
+    m1, n1 = 2048, 4096
+    pairs = [(torch.empty(2 * m1 * n1, dtype=torch.uint8, device=dev).fill_(1),
+              torch.empty(m1 * n1, dtype=torch.uint8, device=dev)) for _ in range(24)]
+    calls = [(lambda p=pairs[i % 24]: check(lib.w8a8_peak_stream(
+        p[0].data_ptr(), p[1].data_ptr(), 2 * m1 * n1, cus * 2, 2, sink.data_ptr(),
+        torch.cuda.current_stream(dev).cuda_stream), "peak_stream")) for i in range(48)]
+    us = graph_us(torch, calls)
+    out["stream21_cfg1_GBps"] = 3 * m1 * n1 / (us * 1e-6) / 1e9
+    out["stream21_cfg1_note"] = ("2:1 stream of cfg1's bytes (16.8 MB read, 8.4 MB written), "
+                                 "24 buffer pairs in turn, 48 graph-replayed launches: the "
+                                 "quantizer's cold cfg1 measurement with the arithmetic removed")
+    del pairs
     calls = [lambda: check(lib.w8a8_peak_empty(torch.cuda.current_stream(dev).cuda_stream),
                            "peak_empty")] * 48
     out["launch_floor_us"] = graph_us(torch, calls)
@@ -654,6 +709,8 @@ def main(argv=None) -> int:
 
     peaks = measured_peaks(torch, dev, cus)
     log(json.dumps(peaks))
+    for pp in per_proj:
+        pp["quant_frac_stream21_measured"] = pp["quant_GBps"] / peaks["stream21_GBps"]
     roofline["peak_measured"] = peaks["mfma_i8_random_TOPS"]
     roofline["frac_measured"] = gemm_tops / peaks["mfma_i8_random_TOPS"]
     roofline["peak_measured_note"] = ("int8 MFMA-only loop on random operands, same run "
@@ -662,8 +719,9 @@ def main(argv=None) -> int:
     extras = {}
     if not args.no_extras:
         extras["smoothquant_cfg1"] = bench_quantizer(torch, w8a8, dev, gen)
-        extras["smoothquant_cfg1"]["frac_copy_measured"] = (extras["smoothquant_cfg1"]["GBps"]
-                                                           / peaks["copy_GBps"])
+        q1 = extras["smoothquant_cfg1"]
+        q1["frac_stream21_cfg1_measured"] = q1["GBps"] / peaks["stream21_cfg1_GBps"]
+        q1["frac_stream21_measured"] = q1["GBps"] / peaks["stream21_GBps"]
         log(json.dumps(extras["smoothquant_cfg1"]))
         extras["smoothquant_sweep"] = bench_quantizer_sweep(torch, w8a8, dev, gen)
         log(json.dumps(extras["smoothquant_sweep"]))

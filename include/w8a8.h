@@ -420,6 +420,56 @@ int w8a8_moe_silu_mul_quant(const void* gate_up, uint32_t ld_gu, const float* sm
                             uint32_t ldq, float* row_scale, float quant_max, hipStream_t stream);
 
 /*
+ * Gate_up weights in the order w8a8_moe_gate_up_silu reads: w int8
+ * [experts, 2 * inter, ldw] (rows [0, inter) gate, [inter, 2 * inter) up, as
+ * w8a8_moe_gemm takes them) -> w_out int8 [experts, 2 * inter, k] whose rows
+ * come in blocks of 16: 8 gate rows, then the 8 up rows of the same outputs
+ * (out row r = gate row (r / 16) * 8 + r % 16 for r % 16 < 8, else up row
+ * (r / 16) * 8 + r % 16 - 8); scale_w [experts, 2 * inter] (optional) is
+ * permuted alike into scale_w_out.  A one-time weight preparation, like
+ * w8a8_pack_weights.  inter % 8 == 0; ldw = 0 means k.
+ */
+int w8a8_moe_interleave_gate_up(const int8_t* w, const float* scale_w, uint32_t experts,
+                                uint32_t inter, uint32_t k, uint32_t ldw, int8_t* w_out,
+                                float* scale_w_out, hipStream_t stream);
+
+/* Device workspace w8a8_moe_gate_up_silu needs (the fp16 activation, per-row
+ * maxima, K-split partials). */
+size_t w8a8_moe_gate_up_silu_workspace_size(uint32_t rows, uint32_t inter);
+
+/*
+ * The gate_up expert GEMM with SiLU(gate) * up fused in its epilogue, then
+ * the requantization for the down GEMM: the role of moe_gate_up_silu_kernel
+ * (rocwmma_fused_moe.cpp:96-158, SiLU "in register, no extra global memory
+ * round-trip"), computing the gated product that kernel describes (:20, :94)
+ * rather than the SiLU of every output it applies (:153-156).  Per sorted row
+ * r of expert e and output j < inter:
+ *   g, u = fp16 dequant of the GEMM (as w8a8_moe_gemm would write them)
+ *   h    = fp16(silu(g) * u)                  (fp32 product, one rounding)
+ *   q[r, j], row_scale[r] = SmoothQuant of float(h) * smooth_scale[e*inter + j]
+ * i.e. w8a8_moe_gemm + w8a8_moe_silu_mul_quant with the activation rounded
+ * to fp16 before it is smoothed, so q may differ by one step from the
+ * unfused chain.  The GEMM writes h at half the gate_up width plus, per row,
+ * the maxima of |float(h) * s| over its output tiles, so the requantization
+ * reads half the bytes the unfused one does and no row reduction is left.
+ * a int8 [rows, lda] expert-sorted (w8a8_moe_sort order); w_interleaved from
+ * w8a8_moe_interleave_gate_up ([experts, 2 * inter, k]); scale_a [rows],
+ * scale_w_interleaved [experts, 2 * inter] (or tensor scales as in
+ * w8a8_gemm); smooth_scale [experts, inter] or NULL; q int8 [rows, ldq]
+ * (ldq = 0 means inter), row_scale [rows]: only rows inside some expert's
+ * [start, start + count) are written.  workspace: 256-byte aligned,
+ * w8a8_moe_gate_up_silu_workspace_size bytes.  inter % 8 == 0, inter <=
+ * 32768, k % 16 == 0.
+ */
+int w8a8_moe_gate_up_silu(uint32_t experts, uint32_t rows, uint32_t inter, uint32_t k,
+                          const int8_t* a, uint32_t lda, const int8_t* w_interleaved,
+                          const float* scale_a, const float* scale_w_interleaved,
+                          float tensor_scale_a, float tensor_scale_b,
+                          const float* smooth_scale, const int32_t* expert_start,
+                          const int32_t* expert_count, int8_t* q, uint32_t ldq, float* row_scale,
+                          float quant_max, void* workspace, size_t ws_bytes, hipStream_t stream);
+
+/*
  * Weighted combine back to token order:
  *   out[t, j] = half(sum over slots s (ascending) of
  *                    fma(topk_weights[t, s], float(y[dst_row[t*topk + s], j]), acc))

@@ -39,6 +39,7 @@ __all__ = [
     "fused_sq_gemm", "W8A8Error", "PackedWeights", "pack_weights", "pack_weights_size",
     "gemm_packed", "gemm_packed_workspace_size", "fused_sq_gemm_packed", "grouped_gemm",
     "topk_softmax", "moe_sort", "moe_sort_workspace_size", "moe_gemm", "moe_gemm_workspace_size", "moe_silu_mul_quant",
+    "moe_interleave_gate_up", "moe_gate_up_silu", "moe_gate_up_silu_workspace_size",
     "moe_combine", "moe_ffn", "add_rmsnorm_smoothquant", "rmsnorm", "add_rmsnorm",
     "quantize_weights",
 ]
@@ -525,6 +526,51 @@ def moe_silu_mul_quant(gate_up, expert_start, expert_count, smooth_scale=None,
     return q, r
 
 
+def moe_interleave_gate_up(w_gate_up, scale_w=None):
+    """gate_up weights int8 [E, 2*inter, K] (+ scales [E, 2*inter]) -> the row
+    order moe_gate_up_silu reads (blocks of 8 gate rows then their 8 up rows)."""
+    torch = _torch()
+    _require_cuda(w_gate_up, scale_w)
+    e, two_i, k = w_gate_up.shape
+    wo = torch.empty((e, two_i, k), dtype=torch.int8, device=w_gate_up.device)
+    so = torch.empty((e, two_i), dtype=torch.float32, device=w_gate_up.device) \
+        if scale_w is not None else None
+    _lib.call("w8a8_moe_interleave_gate_up", _ptr(w_gate_up), _ptr(scale_w), e, two_i // 2, k,
+              w_gate_up.stride(1), _ptr(wo), _ptr(so), _stream(w_gate_up.device))
+    return wo, so
+
+
+def moe_gate_up_silu_workspace_size(rows: int, inter: int) -> int:
+    return int(library().w8a8_moe_gate_up_silu_workspace_size(rows, inter))
+
+
+def moe_gate_up_silu(a, w_interleaved, expert_start, expert_count, scale_a=None,
+                     scale_w_interleaved=None, smooth_scale=None, quant_max: float = 127.0,
+                     q=None, row_scale=None, workspace=None, tensor_scale_a: float = 1.0,
+                     tensor_scale_b: float = 1.0):
+    """Gate_up expert GEMM with SiLU(gate)*up in its epilogue, then the
+    requantization for the down GEMM: a int8 [rows, K] expert-sorted,
+    w_interleaved from moe_interleave_gate_up -> (q int8 [rows, inter], row_scale)."""
+    torch = _torch()
+    _require_cuda(a, w_interleaved, expert_start, expert_count, scale_a, scale_w_interleaved,
+                  smooth_scale)
+    rows, k = a.shape
+    e, two_i, _ = w_interleaved.shape
+    inter = two_i // 2
+    q = q if q is not None else torch.empty((rows, inter), dtype=torch.int8, device=a.device)
+    r = row_scale if row_scale is not None else torch.empty(rows, dtype=torch.float32,
+                                                            device=a.device)
+    if workspace is None:
+        workspace = torch.empty(moe_gate_up_silu_workspace_size(rows, inter), dtype=torch.uint8,
+                                device=a.device)
+    _lib.call("w8a8_moe_gate_up_silu", e, rows, inter, k, _ptr(a), a.stride(0),
+              _ptr(w_interleaved), _ptr(scale_a), _ptr(scale_w_interleaved),
+              float(tensor_scale_a), float(tensor_scale_b), _ptr(smooth_scale),
+              _ptr(expert_start), _ptr(expert_count), _ptr(q), q.stride(0), _ptr(r),
+              float(quant_max), _ptr(workspace), workspace.numel(), _stream(a.device))
+    return q, r
+
+
 def moe_combine(y, topk_weights, dst_row, out=None):
     """y fp16 [rows, N] (expert-sorted) -> out fp16 [T, N] = sum_k w * y[dst_row]."""
     torch = _torch()
@@ -538,14 +584,17 @@ def moe_combine(y, topk_weights, dst_row, out=None):
 
 
 def moe_ffn(x, logits, smooth_scale, w_gate_up, sb_gate_up, w_down, sb_down, topk: int,
-            smooth_scale_down=None, unit_size: int = 32):
+            smooth_scale_down=None, unit_size: int = 32, gate_up_interleaved=None):
     """Whole expert FFN on one GPU, nine launches, no host synchronization:
     top-k routing, stable expert sort, MoE SmoothQuant straight into the
     expert-sorted rows, gate_up expert GEMM, SiLU(gate)*up requantization,
-    down expert GEMM, weighted combine.  Returns (out fp16 [T, H], parts)."""
+    down expert GEMM, weighted combine.  Returns (out fp16 [T, H], parts).
+    gate_up_interleaved: (w, scale) from moe_interleave_gate_up -- then the
+    gate_up GEMM runs with the SiLU epilogue (moe_gate_up_silu) and
+    parts["gate_up"] is None."""
     torch = _torch()
     t, h = x.shape
-    e = w_gate_up.shape[0]
+    e = w_gate_up.shape[0] if w_gate_up is not None else gate_up_interleaved[0].shape[0]
     w, ids = topk_softmax(logits, topk)
     srt = moe_sort(ids, e, unit_size)
     rows = srt["sorted_ids"].numel()
@@ -554,8 +603,13 @@ def moe_ffn(x, logits, smooth_scale, w_gate_up, sb_gate_up, w_down, sb_down, top
     moe_smoothquant(x, smooth_scale, ids, dst_row=srt["dst_row"], rows=rows, out=qa, row_scale=ra)
     ws = torch.empty(moe_gemm_workspace_size(e, rows, h, w_down.shape[2]), dtype=torch.uint8,
                      device=x.device)
-    gu = moe_gemm(qa, w_gate_up, srt["start"], srt["count"], ra, sb_gate_up, workspace=ws)
-    q2, r2 = moe_silu_mul_quant(gu, srt["start"], srt["count"], smooth_scale_down)
+    if gate_up_interleaved is not None:
+        gu = None
+        q2, r2 = moe_gate_up_silu(qa, gate_up_interleaved[0], srt["start"], srt["count"], ra,
+                                  gate_up_interleaved[1], smooth_scale_down)
+    else:
+        gu = moe_gemm(qa, w_gate_up, srt["start"], srt["count"], ra, sb_gate_up, workspace=ws)
+        q2, r2 = moe_silu_mul_quant(gu, srt["start"], srt["count"], smooth_scale_down)
     y = moe_gemm(q2, w_down, srt["start"], srt["count"], r2, sb_down, workspace=ws)
     out = moe_combine(y, w, srt["dst_row"])
     return out, dict(weights=w, ids=ids, sort=srt, qa=qa, ra=ra, gate_up=gu, q2=q2, r2=r2, y=y)

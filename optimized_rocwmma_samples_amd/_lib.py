@@ -82,6 +82,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                              _ptr, _ptr, _f32, _f32, _ptr, _ptr, _i32, _ptr, _size, _ptr]),
     "w8a8_moe_silu_mul_quant": (_i32, [_ptr, _u32, _ptr, _ptr, _ptr, _u32, _u32, _u32, _ptr, _u32,
                                        _ptr, _f32, _ptr]),
+    "w8a8_moe_interleave_gate_up": (_i32, [_ptr, _ptr, _u32, _u32, _u32, _u32, _ptr, _ptr, _ptr]),
+    "w8a8_moe_gate_up_silu_workspace_size": (_size, [_u32, _u32]),
+    "w8a8_moe_gate_up_silu": (_i32, [_u32, _u32, _u32, _u32, _ptr, _u32, _ptr, _ptr, _ptr, _f32,
+                                     _f32, _ptr, _ptr, _ptr, _ptr, _u32, _ptr, _f32, _ptr, _size,
+                                     _ptr]),
     "w8a8_moe_combine": (_i32, [_ptr, _u32, _u32, _ptr, _ptr, _u32, _u32, _u32, _ptr, _u32,
                                 _ptr]),
 }

@@ -660,6 +660,79 @@ int w8a8_moe_silu_mul_quant(const void* gate_up, uint32_t ld_gu, const float* sm
                       fn);
 }
 
+int w8a8_moe_interleave_gate_up(const int8_t* w, const float* scale_w, uint32_t experts,
+                                uint32_t inter, uint32_t k, uint32_t ldw, int8_t* w_out,
+                                float* scale_w_out, hipStream_t stream)
+{
+    const char* fn = "w8a8_moe_interleave_gate_up";
+    if(!w || !w_out || (scale_w && !scale_w_out))
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: null pointer argument", fn);
+    if(experts == 0 || inter == 0 || k == 0)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: experts, inter, k must be > 0", fn);
+    if(inter % 8 != 0)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: inter=%u must be a multiple of 8", fn, inter);
+    if(ldw == 0) ldw = k;
+    if(ldw < k) return fail(W8A8_ERROR_INVALID_VALUE, "%s: ldw=%u smaller than k=%u", fn, ldw, k);
+    return hip_status(w8a8::launch_moe_interleave_gate_up(w, scale_w, experts, inter, k, ldw,
+                                                          w_out, scale_w_out, stream),
+                      fn);
+}
+
+size_t w8a8_moe_gate_up_silu_workspace_size(uint32_t rows, uint32_t inter)
+{
+    return w8a8::moe_gate_up_silu_workspace_bytes(rows, inter);
+}
+
+int w8a8_moe_gate_up_silu(uint32_t experts, uint32_t rows, uint32_t inter, uint32_t k,
+                          const int8_t* a, uint32_t lda, const int8_t* w_interleaved,
+                          const float* scale_a, const float* scale_w_interleaved,
+                          float tensor_scale_a, float tensor_scale_b,
+                          const float* smooth_scale, const int32_t* expert_start,
+                          const int32_t* expert_count, int8_t* q, uint32_t ldq, float* row_scale,
+                          float quant_max, void* workspace, size_t ws_bytes, hipStream_t stream)
+{
+    const char* fn = "w8a8_moe_gate_up_silu";
+    if(!a || !w_interleaved || !expert_start || !expert_count || !q || !row_scale || !workspace)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: null pointer argument", fn);
+    if(experts == 0 || inter == 0 || k == 0)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: experts, inter, k must be > 0", fn);
+    if(inter % 8 != 0 || inter > 32768)
+        return fail(W8A8_ERROR_NOT_SUPPORTED, "%s: needs inter %% 8 == 0 and inter <= 32768 (inter=%u)",
+                    fn, inter);
+    if(lda == 0) lda = k;
+    if(ldq == 0) ldq = inter;
+    if(lda < k || ldq < inter)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: lda=%u must be >= k=%u and ldq=%u >= inter=%u",
+                    fn, lda, k, ldq, inter);
+    if(!valid_qmax(quant_max))
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: quant_max must be in (0, 127]", fn);
+    if(reinterpret_cast<uintptr_t>(a) % 16 || reinterpret_cast<uintptr_t>(w_interleaved) % 16
+       || lda % 16 || k % 16 || reinterpret_cast<uintptr_t>(q) % 8 || ldq % 8
+       || (scale_w_interleaved && reinterpret_cast<uintptr_t>(scale_w_interleaved) % 16)
+       || (smooth_scale && reinterpret_cast<uintptr_t>(smooth_scale) % 16))
+        return fail(W8A8_ERROR_NOT_SUPPORTED,
+                    "%s: needs 16-byte aligned a, w, scale_w, smooth_scale, lda, k %% 16 == 0, "
+                    "8-byte aligned q and ldq %% 8 == 0",
+                    fn);
+    constexpr uint64_t kLimit = 0x7FFFFFFFull;
+    if((uint64_t)rows * lda > kLimit || 2ull * inter * k > kLimit || (uint64_t)rows * inter * 2 > kLimit
+       || (uint64_t)rows * ldq > kLimit || (uint64_t)experts * inter * 4 > kLimit)
+        return fail(W8A8_ERROR_NOT_SUPPORTED,
+                    "%s: a, one expert's weights, the activation, q or smooth_scale over 2 GiB", fn);
+    if(reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: workspace must be 256-byte aligned", fn);
+    const size_t need = w8a8::moe_gate_up_silu_workspace_bytes(rows, inter);
+    if(ws_bytes < need)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: workspace of %zu bytes, %zu needed", fn, ws_bytes,
+                    need);
+    if(rows == 0) return hip_status(hipSuccess, fn);
+    w8a8::MoeSiluArgs g{a,         w_interleaved, scale_a,      scale_w_interleaved, smooth_scale,
+                        expert_start, expert_count, rows,       experts,             inter,
+                        k,         lda,           tensor_scale_a, tensor_scale_b,     q,
+                        ldq,       row_scale,     quant_max,    workspace};
+    return hip_status(w8a8::launch_moe_gate_up_silu(g, stream), fn);
+}
+
 int w8a8_moe_combine(const void* y, uint32_t ldy, uint32_t rows_y, const float* topk_weights,
                      const int32_t* dst_row, uint32_t tokens, uint32_t topk, uint32_t n,
                      void* out, uint32_t ldo, hipStream_t stream)

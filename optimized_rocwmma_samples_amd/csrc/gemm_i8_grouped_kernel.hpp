@@ -155,7 +155,8 @@ __device__ __forceinline__ uint32_t moe_total_tiles(const MoeArgs& q)
 // Problem and tile origin of logical MoE tile `lid` (< total).
 template <class C, int OUT>
 __device__ __forceinline__ void moe_tile(const MoeArgs& q, uint32_t lid, KArgs& p, uint32_t& m0,
-                                         uint32_t& n0)
+                                         uint32_t& n0, uint32_t* expert = nullptr,
+                                         uint32_t* first_row = nullptr)
 {
     const uint32_t tiles_n = (q.n + C::kBN - 1) / C::kBN;
     auto tiles = [&](uint32_t e) { return (moe_rows_of(q, e) + C::kBM - 1) / C::kBM * tiles_n; };
@@ -175,11 +176,133 @@ __device__ __forceinline__ void moe_tile(const MoeArgs& q, uint32_t lid, KArgs& 
     p.ldc = q.ldc;
     p.tsa = q.tsa;
     p.tsb = q.tsb;
+    if(expert) *expert = e;
+    if(first_row) *first_row = row0;
     local_tile<C>(lid - first, p.m, p.n, m0, n0);
 }
 
-template <class C, int OUT>
-__global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_moe_kernel(MoeArgs q, int vec_ok)
+// ---------------------------------------------------------------------------
+// SiLU(gate) * up epilogue of the MoE gate_up GEMM (w8a8_moe_gate_up_silu).
+// The weights' rows come interleaved in blocks of 16: 8 gate rows, then the
+// 8 up rows of the same outputs (w8a8_moe_interleave_gate_up).  In the MFMA
+// layout a lane holds, for each 32-column MFMA tile j, four runs g of 4
+// columns, (g * 8 + half * 4 + e); with that interleave run g = 2 * gp is
+// gate and g = 2 * gp + 1 is up of the same 4 outputs
+//   o = n0 / 2 + wn * kWaveN / 2 + j * 16 + gp * 8 + half * 4 + e,
+// so silu(g) * u is formed in registers: g and u rounded to fp16 (the values
+// the unfused gate_up GEMM would write), a = silu_mul_epi(g, u) in fp32, h =
+// fp16(a).  h is written at half the gate_up width, and each wave writes,
+// per row, the max over its kWaveN / 2 outputs of |float(h) * s2[e, o]| to
+// pmax[n0 / kWaveN + wn][row] (group-major, so the 32 rows of an MFMA tile
+// are 128 contiguous bytes): the requantization then knows every row's scale
+// before it reads the row.  The SiLU kernels use wave tiles kWaveN = 128
+// wide, so each wave's h rows are 128-byte lines.
+// ---------------------------------------------------------------------------
+struct SiluOut {
+    uint16_t*    h;    // [rows, ldh] fp16 activation (columns [0, inter))
+    float*       pmax; // [groups, ldp] group-major, groups = ceil(2 * inter / kWaveN), ldp >= rows
+    const float* s2;   // [experts, inter] smooth scale of the down GEMM's input, or null
+    uint32_t     ldh, ldp, inter;
+};
+
+// One tile's epilogue for waves wave_base, wave_base + 1, ... of the tile;
+// h and pmax point at the expert's first row, s2 at its vector (or null).
+template <class C>
+__device__ __forceinline__ void epilogue_silu(const KArgs& p, uint32_t m0, uint32_t n0,
+                                              int8_t* lds, int wave_base,
+                                              const v16i (&acc)[C::kTilesM][C::kTilesN],
+                                              const EpiScales<C>& sc, uint16_t* h, float* pmax,
+                                              const float* s2, uint32_t ldh, uint32_t ldp,
+                                              uint32_t inter)
+{
+    constexpr int kOutCols   = C::kWaveN / 2;
+    constexpr int kRowBytes  = kOutCols * 2;
+    constexpr int kRowChunks = kRowBytes / 16;
+    constexpr int kRowsPerSt = kWave / kRowChunks;
+    static_assert(kRowChunks == 4 || kRowChunks == 8 || kRowChunks == 16, "row of 4-16 chunks");
+    using S = StageSwz<kRowChunks>;
+    const int      slot = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int      wave = wave_base + slot;
+    const int      lane = threadIdx.x % kWave;
+    const int      wm   = wave / C::kWavesN;
+    const int      wn   = wave % C::kWavesN;
+    const int      half = lane >> 5;
+    const uint32_t oc0  = n0 / 2 + wn * kOutCols;
+    // waves wholly past the last interleaved column (a partial last N tile)
+    // have no pmax entry and store nothing
+    const bool     live = n0 + wn * C::kWaveN < p.n;
+    float* const   pcol = pmax + (size_t)(n0 / C::kWaveN + wn) * ldp;
+
+    // s2 of this lane's outputs (1 without s2; 0 past inter, where g = u = 0)
+    float s2v[C::kTilesN][2][4];
+#pragma unroll
+    for(int j = 0; j < C::kTilesN; ++j)
+#pragma unroll
+        for(int gp = 0; gp < 2; ++gp) {
+            const uint32_t o = oc0 + j * 16 + gp * 8 + half * 4;
+            if(s2 != nullptr && o + 4 <= inter) {
+                const float4 v = *reinterpret_cast<const float4*>(s2 + o);
+                s2v[j][gp][0] = v.x, s2v[j][gp][1] = v.y, s2v[j][gp][2] = v.z, s2v[j][gp][3] = v.w;
+            } else {
+#pragma unroll
+                for(int e = 0; e < 4; ++e)
+                    s2v[j][gp][e] = o + e < inter ? (s2 != nullptr ? s2[o + e] : 1.f) : 0.f;
+            }
+        }
+
+    block_barrier(); // every wave's fragment reads and LDS loads are done: the ring is free
+    int8_t* stage = lds + slot * (C::kWaveM * kRowBytes);
+#pragma unroll
+    for(int i = 0; i < C::kTilesM; ++i) {
+        const int row = i * 32 + (lane & 31);
+        float     mx  = 0.f;
+#pragma unroll
+        for(int j = 0; j < C::kTilesN; ++j) {
+#pragma unroll
+            for(int gp = 0; gp < 2; ++gp) {
+                const float4 sg     = sc.sb[j][2 * gp];
+                const float4 su     = sc.sb[j][2 * gp + 1];
+                const float  sgv[4] = {sg.x, sg.y, sg.z, sg.w};
+                const float  suv[4] = {su.x, su.y, su.z, su.w};
+                uint32_t     hb[4];
+#pragma unroll
+                for(int e = 0; e < 4; ++e) {
+                    const float g = half_bits_to_float(float_to_half_bits_2step(
+                        ((float)acc[i][j][(2 * gp) * 4 + e] * sc.sa[i]) * sgv[e]));
+                    const float u = half_bits_to_float(float_to_half_bits_2step(
+                        ((float)acc[i][j][(2 * gp + 1) * 4 + e] * sc.sa[i]) * suv[e]));
+                    hb[e] = float_to_half_bits_2step(silu_mul_epi(g, u));
+                    mx    = fmaxf(mx, fabsf(half_bits_to_float(hb[e]) * s2v[j][gp][e]));
+                }
+                const int phys = S::chunk(j * 2 + gp, row);
+                v2i       pk;
+                pk.x = (int)(hb[0] | (hb[1] << 16));
+                pk.y = (int)(hb[2] | (hb[3] << 16));
+                *reinterpret_cast<v2i*>(stage + row * kRowBytes + phys * 16
+                                        + S::half(half, row) * 8) = pk;
+            }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave)); // the row's other half
+        const uint32_t m = m0 + wm * C::kWaveM + row;
+        if(half == 0 && live && m < p.m) pcol[m] = mx;
+    }
+    // a wave reads back only what it wrote itself (LDS returns a wave's
+    // accesses in order)
+    const int      chunk = lane % kRowChunks;
+    const uint32_t o     = oc0 + chunk * 8;
+#pragma unroll
+    for(int qq = 0; qq < C::kWaveM / kRowsPerSt; ++qq) {
+        const int      row  = qq * kRowsPerSt + lane / kRowChunks;
+        const int      phys = S::chunk(chunk, row);
+        const v4i      v    = S::unswap(*reinterpret_cast<const v4i*>(stage + row * kRowBytes + phys * 16), row);
+        const uint32_t m    = m0 + wm * C::kWaveM + row;
+        if(m < p.m && o < inter) *reinterpret_cast<v4i*>(h + (size_t)m * ldh + o) = v;
+    }
+}
+
+template <class C, int OUT, bool SILU = false>
+__global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_moe_kernel(MoeArgs q, int vec_ok,
+                                                                      SiluOut so)
 {
     extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
     const uint32_t  total = moe_total_tiles<C>(q);
@@ -187,9 +310,19 @@ __global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_moe_kernel(MoeArgs q, 
     const TailSplit sp    = tail_split(total, q.cus, nk, q.ws != nullptr);
     if(blockIdx.x < sp.base) {
         KArgs    p;
-        uint32_t m0, n0;
-        moe_tile<C, OUT>(q, xcd_remap(blockIdx.x, sp.base), p, m0, n0);
-        gemm_tile<C, OUT>(p, m0, n0, vec_ok, lds);
+        uint32_t m0, n0, e, row0;
+        moe_tile<C, OUT>(q, xcd_remap(blockIdx.x, sp.base), p, m0, n0, &e, &row0);
+        if constexpr(SILU) {
+            v16i         acc[C::kTilesM][C::kTilesN];
+            EpiScales<C> sc;
+            gemm_tile_acc<C, true>(p, m0, n0, vec_ok, lds, 0, nk, acc, sc);
+            epilogue_silu<C>(p, m0, n0, lds, 0, acc, sc, so.h + (size_t)row0 * so.ldh,
+                             so.pmax + row0,
+                             so.s2 ? so.s2 + (size_t)e * so.inter : nullptr, so.ldh, so.ldp,
+                             so.inter);
+        } else {
+            gemm_tile<C, OUT>(p, m0, n0, vec_ok, lds);
+        }
         return;
     }
     const uint32_t x = blockIdx.x - sp.base;
@@ -206,9 +339,9 @@ __global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_moe_kernel(MoeArgs q, 
 // Split tiles, kPieces blocks each: a block holds kFixupWaves of the tile's
 // waves, sums their accumulators over the parts in order and runs their part
 // of the tile epilogue.
-template <class C, int OUT>
+template <class C, int OUT, bool SILU = false>
 __global__ void __launch_bounds__(Partial<C>::kFixupWaves * kWave, 1)
-    gemm_i8_moe_fixup_kernel(MoeArgs q, int vec_ok)
+    gemm_i8_moe_fixup_kernel(MoeArgs q, int vec_ok, SiluOut so)
 {
     extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
     const uint32_t  total = moe_total_tiles<C>(q);
@@ -218,8 +351,8 @@ __global__ void __launch_bounds__(Partial<C>::kFixupWaves * kWave, 1)
     const int       wave_base = (int)(blockIdx.x % Partial<C>::kPieces) * Partial<C>::kFixupWaves;
     if(slot >= sp.left) return;
     KArgs    p;
-    uint32_t m0, n0;
-    moe_tile<C, OUT>(q, sp.base + slot, p, m0, n0);
+    uint32_t m0, n0, e, row0;
+    moe_tile<C, OUT>(q, sp.base + slot, p, m0, n0, &e, &row0);
     v16i acc[C::kTilesM][C::kTilesN];
 #pragma unroll
     for(int i = 0; i < C::kTilesM; ++i)
@@ -228,7 +361,17 @@ __global__ void __launch_bounds__(Partial<C>::kFixupWaves * kWave, 1)
     const uint32_t tid = wave_base * kWave + threadIdx.x;
     for(uint32_t part = 0; part < sp.parts; ++part)
         add_partial<C>(q.ws + (size_t)(slot * sp.parts + part) * Partial<C>::kInts, tid, acc);
-    tile_epilogue<C, OUT>(p, m0, n0, vec_ok, lds, acc, wave_base);
+    if constexpr(SILU) {
+        const int    wave = wave_base + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+        EpiScales<C> sc;
+        sc.load(p, m0, n0, wave / C::kWavesN, wave % C::kWavesN, threadIdx.x % kWave, vec_ok);
+        epilogue_silu<C>(p, m0, n0, lds, wave_base, acc, sc, so.h + (size_t)row0 * so.ldh,
+                         so.pmax + row0,
+                         so.s2 ? so.s2 + (size_t)e * so.inter : nullptr, so.ldh, so.ldp,
+                         so.inter);
+    } else {
+        tile_epilogue<C, OUT>(p, m0, n0, vec_ok, lds, acc, wave_base);
+    }
 }
 
 // One flag per (config, output type, kernel kind): the two output types of a
@@ -284,22 +427,46 @@ hipError_t launch_moe(const MoeArgs& q, int out_type, int vec_ok, hipStream_t st
     if(out_type == W8A8_OUT_I32) {
         raise_lds_once<C, W8A8_OUT_I32, 1>(reinterpret_cast<const void*>(gemm_i8_moe_kernel<C, W8A8_OUT_I32>));
         hipLaunchKernelGGL((gemm_i8_moe_kernel<C, W8A8_OUT_I32>), dim3((uint32_t)grid),
-                           dim3(C::kThreads), C::kLdsBytes, stream, q, vec_ok);
+                           dim3(C::kThreads), C::kLdsBytes, stream, q, vec_ok, SiluOut{});
         if(split) {
             hipLaunchKernelGGL((gemm_i8_moe_fixup_kernel<C, W8A8_OUT_I32>), dim3(fixup_blocks),
                                dim3(Partial<C>::kFixupWaves * kWave), Partial<C>::kFixupLds,
-                               stream, q, vec_ok);
+                               stream, q, vec_ok, SiluOut{});
         }
     } else {
         raise_lds_once<C, W8A8_OUT_F16, 1>(reinterpret_cast<const void*>(gemm_i8_moe_kernel<C, W8A8_OUT_F16>));
         hipLaunchKernelGGL((gemm_i8_moe_kernel<C, W8A8_OUT_F16>), dim3((uint32_t)grid),
-                           dim3(C::kThreads), C::kLdsBytes, stream, q, vec_ok);
+                           dim3(C::kThreads), C::kLdsBytes, stream, q, vec_ok, SiluOut{});
         if(split) {
             hipLaunchKernelGGL((gemm_i8_moe_fixup_kernel<C, W8A8_OUT_F16>), dim3(fixup_blocks),
                                dim3(Partial<C>::kFixupWaves * kWave), Partial<C>::kFixupLds,
-                               stream, q, vec_ok);
+                               stream, q, vec_ok, SiluOut{});
         }
     }
+    return hipGetLastError();
+}
+
+// The gate_up GEMM with the SiLU epilogue (q.n = 2 * inter interleaved
+// columns, fp16 scales path; the caller checked vec_ok and the alignment of
+// h, ldh and s2).
+template <class C>
+hipError_t launch_moe_silu(const MoeArgs& q, const SiluOut& so, int vec_ok, hipStream_t stream)
+{
+    const uint32_t tiles_n = (q.n + C::kBN - 1) / C::kBN;
+    const uint64_t bound   = ((uint64_t)(q.rows + C::kBM - 1) / C::kBM + q.experts) * tiles_n;
+    if(bound == 0) return hipSuccess;
+    const bool     split = q.ws != nullptr && q.cus >= 2;
+    const uint64_t grid  = bound + (split ? q.cus : 0);
+    const uint32_t fixup_blocks = q.cus / 2 * Partial<C>::kPieces;
+    if(grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
+    raise_lds_once<C, W8A8_OUT_F16, 2>(
+        reinterpret_cast<const void*>(gemm_i8_moe_kernel<C, W8A8_OUT_F16, true>));
+    hipLaunchKernelGGL((gemm_i8_moe_kernel<C, W8A8_OUT_F16, true>), dim3((uint32_t)grid),
+                       dim3(C::kThreads), C::kLdsBytes, stream, q, vec_ok, so);
+    if(split)
+        hipLaunchKernelGGL((gemm_i8_moe_fixup_kernel<C, W8A8_OUT_F16, true>), dim3(fixup_blocks),
+                           dim3(Partial<C>::kFixupWaves * kWave), Partial<C>::kFixupLds, stream,
+                           q, vec_ok, so);
     return hipGetLastError();
 }
 

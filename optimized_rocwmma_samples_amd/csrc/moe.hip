@@ -329,8 +329,10 @@ struct SiluRows {
     uint32_t        gu_bytes, q_bytes, s2_bytes; // buffer extents of the vector kernel
 };
 
-// Expert holding sorted row `row`, or -1 for padding / out-of-range rows.
-__device__ __forceinline__ int row_expert(const SiluRows& p, uint32_t row)
+// Expert holding sorted row `row`, or -1 for padding / out-of-range rows
+// (P: any argument block with expert_start, expert_count, experts).
+template <class P>
+__device__ __forceinline__ int row_expert(const P& p, uint32_t row)
 {
     int lo = 0, hi = (int)p.experts - 1, e = -1;
     while(lo <= hi) { // last expert with start <= row
@@ -344,33 +346,6 @@ __device__ __forceinline__ int row_expert(const SiluRows& p, uint32_t row)
     }
     if(e < 0 || (int64_t)row >= (int64_t)p.expert_start[e] + p.expert_count[e]) return -1;
     return e;
-}
-
-// (g / (1 + exp(-g))) * u in about a third of the instructions of expf and
-// the IEEE division (the requantization is VALU-bound with those):
-//   exp(-g) = 2^(ph + pl), ph + pl = -g * log2(e) with log2(e) in two parts
-//   and the product's rounding error recovered by an fma, so v_exp_f32 of ph
-//   times (1 + pl ln 2) is within about an ulp of exp(-g);
-//   g / d from v_rcp_f32 and one residual correction (the quotient is then
-//   the correctly rounded one except in rare near-halfway cases).
-// Where exp(-g) overflows (ph >= 128) the division gives -0, for g = +inf it
-// gives +inf; both are selected explicitly.
-__device__ __forceinline__ float silu_mul(float g, float u)
-{
-    constexpr float kLog2eHi = 1.44269502162933349609375f;   // float(log2 e)
-    constexpr float kLog2eLo = 1.925963033500011079e-8f;     // log2 e - kLog2eHi
-    constexpr float kLn2     = 0.693147180559945309f;
-    const float ph = -g * kLog2eHi;
-    const float pl = __builtin_fmaf(-g, kLog2eLo, __builtin_fmaf(-g, kLog2eHi, -ph));
-    float       e  = __builtin_amdgcn_exp2f(ph);
-    e              = __builtin_fmaf(e, pl * kLn2, e);
-    const float d  = 1.f + e;
-    const float r  = __builtin_amdgcn_rcpf(d);
-    const float q0 = g * r;
-    float       q  = __builtin_fmaf(__builtin_fmaf(-d, q0, g), r, q0);
-    q              = ph >= 128.f ? -0.f : q;
-    q              = g == __builtin_inff() ? g : q;
-    return q * u;
 }
 
 // Generic form (any inter, alignment and size): element loads and stores.
@@ -522,6 +497,166 @@ __global__ void __launch_bounds__(kSqThreads) silu_quant_vec_kernel(SiluRows p)
         __builtin_amdgcn_raw_buffer_store_b64(
             pk, rq, (valid && col[j] != kOob) ? row * p.ldq + col[j] : kOob, 0, 0);
     }
+}
+
+// ---------------------------------------------------------------------------
+// Requantization after the gate_up GEMM's SiLU epilogue (epilogue_silu,
+// gemm_i8_grouped_kernel.hpp): row r of the fp16 activation h comes with the
+// per-wave maxima pmax[0..groups, r] of |float(h) * s2|, so the row scale is
+// known before the row is read and each lane quantizes its chunks as they
+// arrive: q = quantizer(float(h) * s2) with r = max / qmax (the SmoothQuant
+// order, rocwmma_smoothquant.cpp:99-113).  Rows outside every expert's
+// [start, start + count) are skipped.  inter % 8 == 0, 16-byte aligned rows.
+// ---------------------------------------------------------------------------
+struct SiluRequant {
+    const uint16_t* h;
+    uint32_t        ldh;
+    const float*    pmax; // [groups, ldp] group-major
+    uint32_t        ldp, groups;
+    const float*    s2;   // [experts, inter] or null
+    const int32_t*  expert_start;
+    const int32_t*  expert_count;
+    uint32_t        experts, rows, inter;
+    int8_t*         q;
+    uint32_t        ldq;
+    float*          r;
+    float           qmax;
+    uint32_t        h_bytes, p_bytes, q_bytes, s2_bytes; // buffer extents (< 2 GiB)
+};
+
+// A block of kSqThreads threads takes kRqRows consecutive rows.  Phase 1:
+// the rows' maxima over all groups (thread t reads row t % kRqRows of groups
+// t / kRqRows, + kRqSlots, ...: kRqRows consecutive floats per group, one
+// segment per wave instruction), reduced through LDS, and the rows' experts.
+// Phase 2: each wave quantizes kRqRows / kSqWaves rows, kRqBatch 8-column
+// chunks per lane in flight (h and s2 loads issued before any store).
+constexpr int kRqRows  = 16;
+constexpr int kRqSlots = kSqThreads / kRqRows;
+constexpr int kRqBatch = 7;
+
+template <bool S2>
+__global__ void __launch_bounds__(kSqThreads) silu_requant_kernel(SiluRequant p)
+{
+    constexpr uint32_t kOob = gemm::kOob;
+    __shared__ float   red[kRqSlots][kRqRows];
+    __shared__ float   rowmax[kRqRows];
+    __shared__ int     rowexp[kRqRows];
+    const int          t    = threadIdx.x;
+    const int          wave = t / kWave;
+    const int          lane = t % kWave;
+    const uint32_t     r0   = blockIdx.x * kRqRows;
+
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.pmax), 0, (int)p.p_bytes, gemm::kBufferFlags);
+    {
+        const uint32_t row = r0 + t % kRqRows;
+        float          mx  = 0.f;
+        for(uint32_t g = t / kRqRows; g < p.groups; g += kRqSlots) {
+            const uint32_t o = row < p.rows ? (g * p.ldp + row) * 4 : kOob;
+            mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, o, 0, 0)));
+        }
+        red[t / kRqRows][t % kRqRows] = mx;
+        if(t < kRqRows) rowexp[t] = r0 + t < p.rows ? row_expert(p, r0 + t) : -1;
+    }
+    __syncthreads();
+    if(t < kRqRows) {
+        float mx = 0.f;
+#pragma unroll
+        for(int sl = 0; sl < kRqSlots; ++sl) mx = fmaxf(mx, red[sl][t]);
+        rowmax[t] = mx;
+    }
+    __syncthreads();
+
+    const uint32_t n = p.inter;
+    const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(p.h), 0, (int)p.h_bytes, gemm::kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.s2), 0, (int)p.s2_bytes, gemm::kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(p.q, 0, (int)p.q_bytes,
+                                                                        gemm::kBufferFlags);
+    const float qmax = p.qmax;
+    for(int rr = wave; rr < kRqRows; rr += kSqWaves) {
+        const uint32_t row   = r0 + rr;
+        const int      e     = rowexp[rr];
+        if(e < 0) continue; // wave-uniform: padding rows and rows past the end
+        const float    rsc   = rowmax[rr] / qmax;
+        const float    inv   = rsc > 0.f ? 1.f / rsc : 0.f;
+        if(lane == 0) p.r[row] = rsc;
+        for(uint32_t c0 = 0; c0 < n; c0 += kRqBatch * 8 * kWave) {
+            v4i      hv[kRqBatch], s0[kRqBatch], s1[kRqBatch];
+            uint32_t col[kRqBatch];
+#pragma unroll
+            for(int j = 0; j < kRqBatch; ++j) {
+                const uint32_t c = c0 + (j * kWave + lane) * 8;
+                col[j]           = c < n ? c : kOob;
+                hv[j] = __builtin_amdgcn_raw_buffer_load_b128(
+                    rh, col[j] != kOob ? (row * p.ldh + c) * 2 : kOob, 0, 0);
+                if constexpr(S2) {
+                    const uint32_t so = col[j] != kOob ? ((uint32_t)e * n + c) * 4 : kOob;
+                    s0[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, so, 0, 0);
+                    s1[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, so, 16, 0);
+                }
+            }
+#pragma unroll
+            for(int j = 0; j < kRqBatch; ++j) {
+                const uint32_t hw[4] = {(uint32_t)hv[j].x, (uint32_t)hv[j].y, (uint32_t)hv[j].z,
+                                        (uint32_t)hv[j].w};
+                float          sv[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+                if constexpr(S2) {
+                    const int w[8] = {s0[j].x, s0[j].y, s0[j].z, s0[j].w,
+                                      s1[j].x, s1[j].y, s1[j].z, s1[j].w};
+#pragma unroll
+                    for(int x = 0; x < 8; ++x) sv[x] = __int_as_float(w[x]);
+                }
+                float v[8];
+#pragma unroll
+                for(int x = 0; x < 4; ++x) {
+                    v[2 * x]     = half_bits_to_float(hw[x] & 0xFFFFu) * sv[2 * x];
+                    v[2 * x + 1] = half_bits_to_float(hw[x] >> 16) * sv[2 * x + 1];
+                }
+                v2i pk;
+                pk.x = (int)pack4_i8(quant_i8(v[0], inv, qmax), quant_i8(v[1], inv, qmax),
+                                     quant_i8(v[2], inv, qmax), quant_i8(v[3], inv, qmax));
+                pk.y = (int)pack4_i8(quant_i8(v[4], inv, qmax), quant_i8(v[5], inv, qmax),
+                                     quant_i8(v[6], inv, qmax), quant_i8(v[7], inv, qmax));
+                __builtin_amdgcn_raw_buffer_store_b64(
+                    pk, rq, col[j] != kOob ? row * p.ldq + col[j] : kOob, 0, 0);
+            }
+        }
+    }
+}
+
+hipError_t launch_requant(const SiluRequant& p, hipStream_t stream)
+{
+    const dim3 grid((p.rows + kRqRows - 1) / kRqRows);
+    if(p.s2 != nullptr)
+        hipLaunchKernelGGL(silu_requant_kernel<true>, grid, dim3(kSqThreads), 0, stream, p);
+    else
+        hipLaunchKernelGGL(silu_requant_kernel<false>, grid, dim3(kSqThreads), 0, stream, p);
+    return hipGetLastError();
+}
+
+// Gate_up weights interleaved for the SiLU epilogue: output row r of expert
+// e is input row (r / 16) * 8 + r % 16 for r % 16 < 8 (gate) and
+// inter + (r / 16) * 8 + r % 16 - 8 otherwise (up); one block per output row.
+__global__ void __launch_bounds__(256)
+    interleave_gate_up_kernel(const int8_t* __restrict__ w, const float* __restrict__ sw,
+                              uint32_t inter, uint32_t k, uint32_t ldw, int8_t* __restrict__ wo,
+                              float* __restrict__ swo, int vec)
+{
+    const uint32_t rows = 2 * inter;
+    const uint32_t e = blockIdx.x / rows, r = blockIdx.x % rows;
+    const uint32_t b = r / 16, x = r % 16;
+    const uint32_t src = x < 8 ? b * 8 + x : inter + b * 8 + (x - 8);
+    const int8_t*  in  = w + ((size_t)e * rows + src) * ldw;
+    int8_t*        out = wo + ((size_t)e * rows + r) * k;
+    if(vec) {
+        for(uint32_t c = threadIdx.x * 16; c < k; c += 256 * 16)
+            *reinterpret_cast<int4*>(out + c) = *reinterpret_cast<const int4*>(in + c);
+    } else {
+        for(uint32_t c = threadIdx.x; c < k; c += 256) out[c] = in[c];
+    }
+    if(threadIdx.x == 0 && sw != nullptr) swo[(size_t)e * rows + r] = sw[(size_t)e * rows + src];
 }
 
 template <int CPL, int WPR>
@@ -705,6 +840,20 @@ hipError_t launch_silu_mul_quant(const uint16_t* gu, uint32_t ld_gu, const float
     return launch_silu_rows<16, 4>(p, vec, stream); // inter <= 32768 (host-checked)
 }
 
+hipError_t launch_moe_interleave_gate_up(const int8_t* w, const float* sw, uint32_t experts,
+                                         uint32_t inter, uint32_t k, uint32_t ldw, int8_t* wo,
+                                         float* swo, hipStream_t stream)
+{
+    const uint64_t blocks = (uint64_t)experts * 2 * inter;
+    if(blocks == 0 || k == 0) return hipSuccess;
+    if(blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
+    const int vec = reinterpret_cast<uintptr_t>(w) % 16 == 0 && ldw % 16 == 0
+                    && reinterpret_cast<uintptr_t>(wo) % 16 == 0 && k % 16 == 0;
+    hipLaunchKernelGGL(interleave_gate_up_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream, w,
+                       sw, inter, k, ldw, wo, swo, vec);
+    return hipGetLastError();
+}
+
 hipError_t launch_moe_combine(const uint16_t* y, uint32_t ldy, uint32_t rows_y, const float* w,
                               const int32_t* dst_row, uint32_t tokens, uint32_t topk, uint32_t n,
                               uint16_t* out, uint32_t ldo, hipStream_t stream)
@@ -799,6 +948,74 @@ hipError_t launch_moe_gemm(const MoeGemmArgs& a, hipStream_t stream)
     if(moe_tile_rows_128(a.rows, a.experts))
         return gemm::launch_moe<GemmGroupedMid>(q, a.out_type, vec_ok, stream);
     return gemm::launch_moe<GemmGrouped>(q, a.out_type, vec_ok, stream);
+}
+
+// The SiLU epilogue's tiles: wave tiles 128 columns wide (64 outputs, one
+// 128-byte line of h per row and wave), otherwise as GemmGrouped /
+// GemmGroupedMid.
+using GemmSilu    = gemm::Cfg<256, 256, 128, 2, 4, 2, 4>;
+using GemmSiluMid = gemm::Cfg<128, 256, 128, 3, 4, 2, 4>;
+static_assert(GemmSilu::kWaveN == GemmSiluMid::kWaveN, "one pmax layout for both tiles");
+static_assert(gemm::Partial<GemmSilu>::kBytes == gemm::Partial<GemmGrouped>::kBytes
+                  && gemm::Partial<GemmSiluMid>::kBytes == gemm::Partial<GemmGroupedMid>::kBytes,
+              "the SiLU tiles' partials fit moe_gemm_workspace_bytes");
+constexpr uint32_t kSiluGroupCols = GemmSilu::kWaveN; // interleaved columns per pmax entry
+
+static size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+
+size_t moe_gate_up_silu_workspace_bytes(uint32_t rows, uint32_t inter)
+{
+    const size_t groups = (2ull * inter + kSiluGroupCols - 1) / kSiluGroupCols;
+    return align256((size_t)rows * inter * 2) + align256((size_t)rows * groups * 4)
+           + moe_gemm_workspace_bytes();
+}
+
+hipError_t launch_moe_gate_up_silu(const MoeSiluArgs& a, hipStream_t stream)
+{
+    if(a.rows == 0) return hipSuccess;
+    const uint32_t groups = (2 * a.inter + kSiluGroupCols - 1) / kSiluGroupCols;
+    int8_t*        ws     = static_cast<int8_t*>(a.ws);
+    uint16_t*      h      = reinterpret_cast<uint16_t*>(ws);
+    float*         pmax   = reinterpret_cast<float*>(ws + align256((size_t)a.rows * a.inter * 2));
+    int32_t*       part   = reinterpret_cast<int32_t*>(
+        ws + align256((size_t)a.rows * a.inter * 2) + align256((size_t)a.rows * groups * 4));
+
+    gemm::MoeArgs q;
+    q.a            = a.a;
+    q.w            = a.w;
+    q.c            = nullptr; // the SiLU epilogue writes h and pmax instead
+    q.sa           = a.scale_a;
+    q.sw           = a.scale_w;
+    q.expert_start = a.expert_start;
+    q.expert_count = a.expert_count;
+    q.rows         = a.rows;
+    q.experts      = a.experts;
+    q.n            = 2 * a.inter;
+    q.k            = a.k;
+    q.lda          = a.lda;
+    q.ldw          = a.k;
+    q.ldc          = 0;
+    q.w_stride     = 2ull * a.inter * a.k;
+    q.tsa          = a.tsa;
+    q.tsb          = a.tsb;
+    q.ws           = part;
+    q.cus          = device_cus();
+    // pmax group-major: row stride ldp = rows
+    const gemm::SiluOut so{h, pmax, a.s2, a.inter, a.rows, a.inter};
+    const int vec_ok = a.scale_w == nullptr || reinterpret_cast<uintptr_t>(a.scale_w) % 16 == 0;
+    hipError_t e = moe_tile_rows_128(a.rows, a.experts)
+                       ? gemm::launch_moe_silu<GemmSiluMid>(q, so, vec_ok, stream)
+                       : gemm::launch_moe_silu<GemmSilu>(q, so, vec_ok, stream);
+    if(e != hipSuccess) return e;
+
+    const uint64_t h_bytes  = (uint64_t)a.rows * a.inter * 2;
+    const uint64_t p_bytes  = (uint64_t)a.rows * groups * 4;
+    const uint64_t q_bytes  = (uint64_t)(a.rows - 1) * a.ldq + a.inter;
+    const uint64_t s2_bytes = (uint64_t)a.experts * a.inter * 4;
+    const SiluRequant r{h, a.inter, pmax, a.rows, groups, a.s2, a.expert_start, a.expert_count,
+                        a.experts, a.rows, a.inter, a.q, a.ldq, a.r, a.qmax, (uint32_t)h_bytes,
+                        (uint32_t)p_bytes, (uint32_t)q_bytes, (uint32_t)s2_bytes};
+    return launch_requant(r, stream);
 }
 
 } // namespace w8a8

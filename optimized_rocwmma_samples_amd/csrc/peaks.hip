@@ -55,21 +55,38 @@ __global__ void __launch_bounds__(256) peak_mfma_i8_kernel(int iters, int random
     if(lane == 0) sink[blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64] = s;
 }
 
-// Grid-stride copy of `n16` 16-byte chunks, kUnroll loads in flight per lane.
-constexpr int kUnroll = 4;
-__global__ void __launch_bounds__(256) peak_copy_kernel(const v4i* __restrict__ src,
-                                                        v4i* __restrict__ dst, size_t n16)
+// Grid-stride stream over `n16` 16-byte source chunks, kUnroll loads in
+// flight per lane (the best of a sweep over 2-16 loads, 256-1024 threads and
+// 1-16 blocks per CU on MI355X).  MODE 0 reads only; MODE 1 copies each chunk;
+// MODE 2 writes 8 bytes per 16 read (the quantizer's fp16 -> int8 ratio).
+// Stores are non-temporal (the faster form in the same sweep).
+constexpr int kUnroll        = 8;
+constexpr int kStreamThreads = 512;
+typedef int v2i __attribute__((ext_vector_type(2)));
+
+template <int MODE>
+__global__ void __launch_bounds__(kStreamThreads) peak_stream_kernel(const v4i* __restrict__ src,
+                                                                     void* __restrict__ dst,
+                                                                     size_t n16, int* sink)
 {
-    const size_t stride = (size_t)gridDim.x * blockDim.x;
-    size_t       i      = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * kStreamThreads;
+    size_t       i      = (size_t)blockIdx.x * kStreamThreads + threadIdx.x;
+    v4i          acc    = {0, 0, 0, 0};
+    auto put = [&](size_t j, const v4i& v) {
+        if constexpr(MODE == 1) __builtin_nontemporal_store(v, static_cast<v4i*>(dst) + j);
+        if constexpr(MODE == 2)
+            __builtin_nontemporal_store(v2i{v.x ^ v.y, v.z ^ v.w}, static_cast<v2i*>(dst) + j);
+        if constexpr(MODE == 0) acc ^= v;
+    };
     for(; i + (kUnroll - 1) * stride < n16; i += kUnroll * stride) {
         v4i v[kUnroll];
 #pragma unroll
-        for(int u = 0; u < kUnroll; ++u) v[u] = __builtin_nontemporal_load(src + i + u * stride);
+        for(int u = 0; u < kUnroll; ++u) v[u] = src[i + u * stride];
 #pragma unroll
-        for(int u = 0; u < kUnroll; ++u) __builtin_nontemporal_store(v[u], dst + i + u * stride);
+        for(int u = 0; u < kUnroll; ++u) put(i + u * stride, v[u]);
     }
-    for(; i < n16; i += stride) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+    for(; i < n16; i += stride) put(i, src[i]);
+    if(MODE == 0 && acc.x == 0x13579BDF && acc.y == acc.z) sink[0] = acc.w; // keeps the loads live
 }
 
 __global__ void peak_empty_kernel() {}
@@ -95,15 +112,26 @@ int w8a8_peak_mfma(uint32_t blocks, uint32_t iters, int random, int* sink, hipSt
     return (int)hipGetLastError();
 }
 
-// Copy `bytes` (a multiple of 16; src, dst 16-byte aligned) with `blocks`
-// blocks of 256 threads.
-int w8a8_peak_copy(const void* src, void* dst, size_t bytes, uint32_t blocks, hipStream_t stream)
+// Stream `bytes` of src (a multiple of 16; src, dst 16-byte aligned) with
+// `blocks` blocks: mode 0 read only (dst unused, sink: one int), 1 copy to
+// dst (`bytes` written), 2 write bytes / 2 to dst.
+int w8a8_peak_stream(const void* src, void* dst, size_t bytes, uint32_t blocks, int mode,
+                     int* sink, hipStream_t stream)
 {
-    if(!src || !dst || bytes % 16 || blocks == 0 || reinterpret_cast<uintptr_t>(src) % 16
-       || reinterpret_cast<uintptr_t>(dst) % 16)
+    if(!src || bytes % 16 || blocks == 0 || reinterpret_cast<uintptr_t>(src) % 16
+       || (mode != 0 && (!dst || reinterpret_cast<uintptr_t>(dst) % 16)) || (mode == 0 && !sink)
+       || mode < 0 || mode > 2)
         return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(peak_copy_kernel, dim3(blocks), dim3(256), 0, stream,
-                       static_cast<const v4i*>(src), static_cast<v4i*>(dst), bytes / 16);
+    const v4i* s = static_cast<const v4i*>(src);
+    if(mode == 0)
+        hipLaunchKernelGGL(peak_stream_kernel<0>, dim3(blocks), dim3(kStreamThreads), 0, stream, s,
+                           dst, bytes / 16, sink);
+    else if(mode == 1)
+        hipLaunchKernelGGL(peak_stream_kernel<1>, dim3(blocks), dim3(kStreamThreads), 0, stream, s,
+                           dst, bytes / 16, sink);
+    else
+        hipLaunchKernelGGL(peak_stream_kernel<2>, dim3(blocks), dim3(kStreamThreads), 0, stream, s,
+                           dst, bytes / 16, sink);
     return (int)hipGetLastError();
 }
 

@@ -111,6 +111,46 @@ __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d)
            | ((uint32_t)d << 24);
 }
 
+// (g / (1 + exp(-g))) * u in about a third of the instructions of expf and
+// the IEEE division (the requantization is VALU-bound with those):
+//   exp(-g) = 2^(ph + pl), ph + pl = -g * log2(e) with log2(e) in two parts
+//   and the product's rounding error recovered by an fma, so v_exp_f32 of ph
+//   times (1 + pl ln 2) is within about an ulp of exp(-g);
+//   g / d from v_rcp_f32 and one residual correction (the quotient is then
+//   the correctly rounded one except in rare near-halfway cases).
+// Where exp(-g) overflows (ph >= 128) the division gives -0, for g = +inf it
+// gives +inf; both are selected explicitly.
+__device__ __forceinline__ float silu_mul(float g, float u)
+{
+    constexpr float kLog2eHi = 1.44269502162933349609375f;   // float(log2 e)
+    constexpr float kLog2eLo = 1.925963033500011079e-8f;     // log2 e - kLog2eHi
+    constexpr float kLn2     = 0.693147180559945309f;
+    const float ph = -g * kLog2eHi;
+    const float pl = __builtin_fmaf(-g, kLog2eLo, __builtin_fmaf(-g, kLog2eHi, -ph));
+    float       e  = __builtin_amdgcn_exp2f(ph);
+    e              = __builtin_fmaf(e, pl * kLn2, e);
+    const float d  = 1.f + e;
+    const float r  = __builtin_amdgcn_rcpf(d);
+    const float q0 = g * r;
+    float       q  = __builtin_fmaf(__builtin_fmaf(-d, q0, g), r, q0);
+    q              = ph >= 128.f ? -0.f : q;
+    q              = g == __builtin_inff() ? g : q;
+    return q * u;
+}
+
+// silu(g) * u for the gate_up GEMM's SiLU epilogue, where it runs inside the
+// compute-bound GEMM: exp(-g) as one v_exp_f32 of -g * log2(e) and the
+// quotient from v_rcp_f32, with no correction steps (a few ulps of fp32,
+// ahead of a rounding to fp16).  As g -> -inf exp(-g) overflows and the
+// product gives -0 (g = -inf selected explicitly); g = +inf gives +inf * u.
+__device__ __forceinline__ float silu_mul_epi(float g, float u)
+{
+    constexpr float kLog2e = 1.44269502162933349609375f;
+    const float     r      = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-g * kLog2e));
+    const float     s      = g == -__builtin_inff() ? -0.f : g * r;
+    return s * u;
+}
+
 // s_waitcnt vmcnt(N) with expcnt/lgkmcnt left at their maxima (gfx9 encoding:
 // vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
 template <int N>

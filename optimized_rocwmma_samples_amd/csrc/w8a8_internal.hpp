@@ -192,4 +192,30 @@ hipError_t launch_moe_gemm(const MoeGemmArgs& a, hipStream_t stream);
 // along K (one int32 tile partial per CU of the current device).
 size_t moe_gemm_workspace_bytes();
 
+// The gate_up expert GEMM with the SiLU(gate) * up epilogue, then the
+// requantization of the fp16 activation (w8a8_moe_gate_up_silu).  w: the
+// interleaved gate_up weights [experts, 2 * inter, k]; ws: 256-byte aligned,
+// moe_gate_up_silu_workspace_bytes (activation, row maxima, split partials).
+struct MoeSiluArgs {
+    const int8_t*  a;
+    const int8_t*  w;
+    const float*   scale_a;
+    const float*   scale_w; // [experts, 2 * inter], interleaved like w
+    const float*   s2;      // [experts, inter] or null
+    const int32_t* expert_start;
+    const int32_t* expert_count;
+    uint32_t       rows, experts, inter, k, lda;
+    float          tsa, tsb;
+    int8_t*        q;
+    uint32_t       ldq;
+    float*         r;
+    float          qmax;
+    void*          ws;
+};
+size_t     moe_gate_up_silu_workspace_bytes(uint32_t rows, uint32_t inter);
+hipError_t launch_moe_gate_up_silu(const MoeSiluArgs& a, hipStream_t stream);
+hipError_t launch_moe_interleave_gate_up(const int8_t* w, const float* sw, uint32_t experts,
+                                         uint32_t inter, uint32_t k, uint32_t ldw, int8_t* wo,
+                                         float* swo, hipStream_t stream);
+
 } // namespace w8a8

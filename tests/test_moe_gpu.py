@@ -452,3 +452,103 @@ def test_config5_full_size_sampled(w8a8, gpu):
     tok = np.r_[0, t - 1, np.arange(1, t - 1, 97)]
     out_exp = O.moe_combine(y, host(parts["weights"]), dst)
     assert np.array_equal(host(out)[tok].view(np.uint16), out_exp[tok].view(np.uint16))
+
+
+def _interleave_perm(inter):
+    """Row order of moe_interleave_gate_up: blocks of 8 gate rows, then their 8 up rows."""
+    r = np.arange(2 * inter)
+    b, x = r // 16, r % 16
+    return np.where(x < 8, b * 8 + x, inter + b * 8 + x - 8)
+
+
+@pytest.mark.parametrize("e,inter,k", [(3, 40, 48), (2, 64, 50)])
+def test_moe_interleave_gate_up_exact(w8a8, gpu, e, inter, k):
+    w = G.int8(inter + k, G.TID_B, (e, 2 * inter, k))
+    sw = G.uniform(inter + k, G.TID_SB, (e, 2 * inter), 1e-3, 1e-2)
+    wo, so = w8a8.moe_interleave_gate_up(dev(w, gpu), dev(sw, gpu))
+    perm = _interleave_perm(inter)
+    assert np.array_equal(host(wo), w[:, perm, :])
+    assert np.array_equal(host(so), sw[:, perm])
+    # the permutation itself: each output row block holds gate j..j+7 then up j..j+7
+    assert list(perm[:16]) == list(range(8)) + list(range(inter, inter + 8))
+
+
+def _silu_h16(gu):
+    """fp16(silu(g) * u) in fp32 from fp16 gate_up rows (numpy exp)."""
+    inter = gu.shape[1] // 2
+    g = gu[:, :inter].astype(np.float32)
+    u = gu[:, inter:].astype(np.float32)
+    with np.errstate(over="ignore"):
+        a = (g / (np.float32(1) + np.exp(-g))) * u
+    return a.astype(np.float16)
+
+
+# (tokens, topk, experts, hidden, inter, sort unit, smooth scale): the second
+# case has K = 4096, so a partial last round of tiles is split along K and the
+# fixup kernel runs the SiLU epilogue; the last has 128-row tiles
+SILU_CASES = [(256, 2, 8, 512, 384, 32, True), (512, 2, 4, 4096, 512, 32, True),
+              (128, 1, 5, 256, 136, 1, False), (2000, 6, 64, 256, 128, 16, True)]
+
+
+@pytest.mark.parametrize("t,k,e,h,inter,unit,with_s2", SILU_CASES)
+def test_moe_gate_up_silu(w8a8, gpu, t, k, e, h, inter, unit, with_s2):
+    import torch
+    seed = t + h + inter
+    ids, count, start, a, wgu, sa, sgu = _sorted_problem(t, k, e, h, 2 * inter, unit, seed)
+    rows = a.shape[0]
+    s2 = G.uniform(seed, G.TID_S, (e, inter), 0.5, 2.0) if with_s2 else None
+    w_il, s_il = w8a8.moe_interleave_gate_up(dev(wgu, gpu), dev(sgu, gpu))
+    q = torch.full((rows, inter), 99, dtype=torch.int8, device=gpu)
+    r = torch.full((rows,), -1.0, dtype=torch.float32, device=gpu)
+    w8a8.moe_gate_up_silu(dev(a, gpu), w_il, dev(start, gpu), dev(count, gpu), dev(sa, gpu), s_il,
+                          dev(s2, gpu) if with_s2 else None, q=q, row_scale=r)
+    qg, rg = host(q), host(r)
+    off1 = exact = total = 0
+    for x in range(e):
+        r0, r1 = start[x], start[x] + count[x]
+        if r1 > r0:
+            gu = O.dequant_f16(O.gemm_i32(a[r0:r1], wgu[x]), sa[r0:r1], sgu[x])
+            sx = s2[x] if with_s2 else np.ones(inter, np.float32)
+            # the fused semantics: SmoothQuant of the fp16 activation
+            qe, re = O.smoothquant(_silu_h16(gu), sx)
+            d = np.abs(qg[r0:r1].astype(np.int32) - qe)
+            assert d.max() <= 1
+            off1 += int((d != 0).sum())
+            exact += int((rg[r0:r1].view(np.int32) == re.view(np.int32)).sum())
+            total += r1 - r0
+            # against the unfused chain (fp32 activation): one step, r within
+            # the activation's fp16 rounding
+            qo, ro = O.silu_mul_quant(gu, s2[x] if with_s2 else None)
+            assert np.abs(qg[r0:r1].astype(np.int32) - qo).max() <= 1
+            assert np.all(np.abs(rg[r0:r1] - ro) <= 1e-3 * np.abs(ro) + 1e-30)
+        if r1 < start[x + 1]:  # padding rows untouched
+            assert (qg[r1:start[x + 1]] == 99).all() and (rg[r1:start[x + 1]] == -1).all()
+    # silu's exp differs from numpy's by an ulp or so: the fp16 activation, and
+    # through it q or r, may differ in rare near-ties
+    assert off1 <= max(2, int(1e-3 * total * inter)), f"{off1} off-by-one values"
+    assert exact >= total - max(2, total // 100), f"{total - exact} row scales differ"
+
+
+def test_moe_ffn_chain_fused(w8a8, gpu):
+    t, h, inter, e, k = 256, 512, 384, 8, 2
+    x, logits, s, wgu, sgu, wd, sd = _chain_inputs(t, h, inter, e, 43)
+    il = w8a8.moe_interleave_gate_up(dev(wgu, gpu), dev(sgu, gpu))
+    out, parts = w8a8.moe_ffn(dev(x, gpu), dev(logits, gpu), dev(s, gpu), None, None,
+                              dev(wd, gpu), dev(sd, gpu), k, gate_up_interleaved=il)
+    assert parts["gate_up"] is None
+    io = O.topk_softmax(logits, k)[1]
+    count, start, padded, sorted_ids, dst = O.moe_sort(io, e, 32)
+    rows = sorted_ids.size
+    qa, ra = O.moe_smoothquant(x, s, io, dst_row=dst, rows=rows)
+    q2, r2, y = host(parts["q2"]), host(parts["r2"]), host(parts["y"])
+    for x_ in range(e):
+        r0, r1 = start[x_], start[x_] + count[x_]
+        if r1 == r0:
+            continue
+        gu = O.dequant_f16(O.gemm_i32(qa[r0:r1], wgu[x_]), ra[r0:r1], sgu[x_])
+        q2o, _ = O.silu_mul_quant(gu)
+        assert np.abs(q2[r0:r1].astype(np.int32) - q2o).max() <= 1
+        y_exp = O.dequant_f16(O.gemm_i32(q2[r0:r1], wd[x_]), r2[r0:r1], sd[x_])
+        assert_f16_bitexact(y[r0:r1], y_exp)
+    out_exp = O.moe_combine(y, host(parts["weights"]), dst)
+    assert np.array_equal(host(out).view(np.uint16), out_exp.view(np.uint16))
