@@ -102,6 +102,10 @@ def graph_us(torch, calls, repeat=1):
     replayed once to warm up, then one replay timed between two events.  The
     host's launch cost does not enter: short kernels are timed back to back,
     as the reference samples time their launch loops (README.md:1568-1569)."""
+    # the side stream does not wait for the default stream by itself: without
+    # this, the warm-up calls could read inputs still being generated, and
+    # write outputs into memory that a pending kernel still reads
+    torch.cuda.synchronize()
     st = torch.cuda.Stream()
     with torch.cuda.stream(st):
         for c in calls[:3]:
