@@ -22,17 +22,20 @@ namespace {
 using gemm::KArgs;
 
 // Production tile configuration, and the smaller tiles of launches that
-// would leave most CUs idle with it (pick_tile_cfg).
-using GemmMain  = gemm::Cfg<256, 256, 128, 2, 2, 4, 4>;
+// would leave most CUs idle with it (pick_tile_cfg).  All on the
+// 16 x 16 x 64 MFMA (gemm::Cfg): against the 32 x 32 x 32 form, GEMM-only,
+// cold weights, cfg3 projections: M = 8192 1448 -> 1389 µs, M = 2048 411 ->
+// 398 µs, M = 512 144 -> 132 µs (sum of the four).
+using GemmMain  = gemm::Cfg<256, 256, 128, 2, 2, 4, 4, 16>;
 // 3 LDS stages: these launches have few tiles per CU and read their panels
 // from HBM, where a third k-tile in flight hides the latency (cold weights,
 // M = 512: 128 x 128 o_proj 32 -> 22 µs, down 100 -> 66 µs; M = 2048,
 // 128 x 256: o_proj 47 -> 40 µs, down 146 -> 116 µs).
-using GemmMidM  = gemm::Cfg<128, 256, 128, 3, 2, 4, 4>; // 8 waves of 64 x 64, 144 KiB LDS
-using GemmSmall = gemm::Cfg<128, 128, 128, 3, 2, 4, 4>; // 8 waves of 64 x 32, 96 KiB LDS
+using GemmMidM  = gemm::Cfg<128, 256, 128, 3, 2, 4, 4, 16>; // 8 waves of 64 x 64, 144 KiB LDS
+using GemmSmall = gemm::Cfg<128, 128, 128, 3, 2, 4, 4, 16>; // 8 waves of 64 x 32, 96 KiB LDS
 // m <= 64 over row-major weights (tiles_beat_decode): 4 waves of 64 x 32,
 // 4 stages (96 KiB LDS), one tile row.
-using GemmDecTile = gemm::Cfg<64, 128, 128, 4, 1, 4, 1>;
+using GemmDecTile = gemm::Cfg<64, 128, 128, 4, 1, 4, 1, 16>;
 // Packed-weight tile configurations (m > kDecodeMaxM): 256 x 256 blocks, and
 // 128 / 64-row blocks for launches that would leave most CUs idle with them
 // (pick_packed_cfg).

@@ -209,12 +209,14 @@ struct SiluOut {
 // h and pmax point at the expert's first row, s2 at its vector (or null).
 template <class C>
 __device__ __forceinline__ void epilogue_silu(const KArgs& p, uint32_t m0, uint32_t n0,
-                                              int8_t* lds, int wave_base,
-                                              const v16i (&acc)[C::kTilesM][C::kTilesN],
+                                              int8_t* lds, int wave_base, const Acc<C>& acc,
                                               const EpiScales<C>& sc, uint16_t* h, float* pmax,
                                               const float* s2, uint32_t ldh, uint32_t ldp,
                                               uint32_t inter)
 {
+    // gate and up of one output sit in quads 2 gp and 2 gp + 1 of the same
+    // lane only in the 32 x 32 MFMA layout (8-row interleave)
+    static_assert(C::kMfma == 32, "SiLU epilogue: 32 x 32 MFMA layout");
     constexpr int kOutCols   = C::kWaveN / 2;
     constexpr int kRowBytes  = kOutCols * 2;
     constexpr int kRowChunks = kRowBytes / 16;
@@ -260,17 +262,17 @@ __device__ __forceinline__ void epilogue_silu(const KArgs& p, uint32_t m0, uint3
         for(int j = 0; j < C::kTilesN; ++j) {
 #pragma unroll
             for(int gp = 0; gp < 2; ++gp) {
-                const float4 sg     = sc.sb[j][2 * gp];
-                const float4 su     = sc.sb[j][2 * gp + 1];
+                const float4 sg     = sc.sb[j * 4 + 2 * gp];
+                const float4 su     = sc.sb[j * 4 + 2 * gp + 1];
                 const float  sgv[4] = {sg.x, sg.y, sg.z, sg.w};
                 const float  suv[4] = {su.x, su.y, su.z, su.w};
                 uint32_t     hb[4];
 #pragma unroll
                 for(int e = 0; e < 4; ++e) {
                     const float g = half_bits_to_float(float_to_half_bits_2step(
-                        ((float)acc[i][j][(2 * gp) * 4 + e] * sc.sa[i]) * sgv[e]));
+                        ((float)acc.r[i][j][(2 * gp) * 4 + e] * sc.sa[i]) * sgv[e]));
                     const float u = half_bits_to_float(float_to_half_bits_2step(
-                        ((float)acc[i][j][(2 * gp + 1) * 4 + e] * sc.sa[i]) * suv[e]));
+                        ((float)acc.r[i][j][(2 * gp + 1) * 4 + e] * sc.sa[i]) * suv[e]));
                     hb[e] = float_to_half_bits_2step(silu_mul_epi(g, u));
                     mx    = fmaxf(mx, fabsf(half_bits_to_float(hb[e]) * s2v[j][gp][e]));
                 }
@@ -313,7 +315,7 @@ __global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_moe_kernel(MoeArgs q, 
         uint32_t m0, n0, e, row0;
         moe_tile<C, OUT>(q, xcd_remap(blockIdx.x, sp.base), p, m0, n0, &e, &row0);
         if constexpr(SILU) {
-            v16i         acc[C::kTilesM][C::kTilesN];
+            Acc<C>       acc;
             EpiScales<C> sc;
             gemm_tile_acc<C, true>(p, m0, n0, vec_ok, lds, 0, nk, acc, sc);
             epilogue_silu<C>(p, m0, n0, lds, 0, acc, sc, so.h + (size_t)row0 * so.ldh,
@@ -353,11 +355,8 @@ __global__ void __launch_bounds__(Partial<C>::kFixupWaves * kWave, 1)
     KArgs    p;
     uint32_t m0, n0, e, row0;
     moe_tile<C, OUT>(q, sp.base + slot, p, m0, n0, &e, &row0);
-    v16i acc[C::kTilesM][C::kTilesN];
-#pragma unroll
-    for(int i = 0; i < C::kTilesM; ++i)
-#pragma unroll
-        for(int j = 0; j < C::kTilesN; ++j) acc[i][j] = v16i{0};
+    Acc<C> acc;
+    acc.zero();
     const uint32_t tid = wave_base * kWave + threadIdx.x;
     for(uint32_t part = 0; part < sp.parts; ++part)
         add_partial<C>(q.ws + (size_t)(slot * sp.parts + part) * Partial<C>::kInts, tid, acc);

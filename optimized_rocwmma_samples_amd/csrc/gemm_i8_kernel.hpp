@@ -8,10 +8,12 @@
 // A is [M,K] row-major, B is [N,K] K-contiguous (both operands K-major).
 //
 // Tile hierarchy (Cfg): block BM x BN x BK, WAVES_M x WAVES_N waves, each wave
-// owning a (BM/WAVES_M) x (BN/WAVES_N) tile of 32x32 v_mfma_i32_32x32x32_i8.
+// owning a (BM/WAVES_M) x (BN/WAVES_N) tile of 16 x 16 v_mfma_i32_16x16x64_i8
+// blocks (or 32 x 32 v_mfma_i32_32x32x32_i8 ones, Cfg's MFMA_ parameter).
 // The MFMA is issued with srcA = B fragment (rows n) and srcB = A fragment
 // (rows m): D[i=n][j=m], so each lane owns one m and runs of 4 consecutive n
-// and the epilogue writes 4 fp16 (8 B) or 4 int32 (16 B) per store.
+// (Acc<C>'s quads) and the epilogue writes 4 fp16 (8 B) or 4 int32 (16 B)
+// per store.
 //
 // Data movement
 //   * global -> LDS with global_load_lds_dwordx4 (no VGPR staging): one wave
@@ -22,8 +24,8 @@
 //     The 16 lanes of each ds_read_b128 quarter-wave (16 consecutive rows, same
 //     logical chunk) then hit 16 distinct 16-byte bank groups: conflict-free.
 //   * STAGES-deep ring: tiles t+1..t+STAGES-1 are in flight while t computes.
-//     One barrier per BK-deep tile, placed before the last 32-deep MFMA group
-//     so LDS fragment reads always overlap MFMA work.
+//     One barrier per BK-deep tile, placed before the last MFMA k-group so
+//     LDS fragment reads always overlap MFMA work (FragPipe).
 //   * Loads are raw buffer loads into LDS: per-lane offsets are fixed, the
 //     tile's k offset is the uniform soffset, and out-of-range rows / k-chunks
 //     use an offset past the buffer, which reads as zeros; edges need no
@@ -42,12 +44,21 @@
 #include "w8a8_device.hpp"
 
 #include <mutex>
+#include <type_traits>
 
 namespace w8a8 {
 
 namespace gemm {
 
-template <int BM_, int BN_, int BK_, int STAGES_, int WAVES_M_, int WAVES_N_, int GROUP_M_ = 8>
+// MFMA_: the matrix instruction of the tile body, 32 for v_mfma_i32_32x32x32_i8
+// or 16 for v_mfma_i32_16x16x64_i8.  Both retire the same int8 ops per cycle
+// and read the same LDS bytes per op for a given wave tile; on MI355X under
+// the power limit the 16 x 16 x 64 form sustains ~14% more ops on random
+// operands (3.60 against 3.16 POP/s in a loop fed from LDS like the tile
+// body; plausibly because it reads and writes half the accumulator bytes per
+// op).
+template <int BM_, int BN_, int BK_, int STAGES_, int WAVES_M_, int WAVES_N_, int GROUP_M_ = 8,
+          int MFMA_ = 32>
 struct Cfg {
     static constexpr int kBM      = BM_;
     static constexpr int kBN      = BN_;
@@ -60,8 +71,9 @@ struct Cfg {
     static constexpr int kThreads = kWaves * kWave;
     static constexpr int kWaveM   = kBM / kWavesM;
     static constexpr int kWaveN   = kBN / kWavesN;
-    static constexpr int kTilesM  = kWaveM / 32;
-    static constexpr int kTilesN  = kWaveN / 32;
+    static constexpr int kMfma    = MFMA_;
+    static constexpr int kTilesM  = kWaveM / kMfma;      // MFMA blocks per wave tile
+    static constexpr int kTilesN  = kWaveN / kMfma;
     static constexpr int kChunks  = kBK / 16;           // 16-byte chunks per LDS row
     static constexpr int kSwzShift = kChunks == 8 ? 1 : (kChunks == 4 ? 2 : 3);
     static constexpr int kRowsPerLoad = kWave / kChunks; // rows one wave-load fills
@@ -72,13 +84,16 @@ struct Cfg {
     static constexpr int kLoadsA  = kABytes / 1024 / kWaves; // wave-loads per wave per stage
     static constexpr int kLoadsB  = kBBytes / 1024 / kWaves;
     static constexpr int kLoads   = kLoadsA + kLoadsB;
-    static constexpr int kSubK    = kBK / 32;            // 32-deep MFMA groups per tile
+    static constexpr int kMfmaK   = kMfma == 32 ? 32 : 64; // depth of one MFMA
+    static constexpr int kSubK    = kBK / kMfmaK;        // MFMA k-groups per tile
 
     static_assert(kChunks == 2 || kChunks == 4 || kChunks == 8, "BK in {32, 64, 128}");
     static_assert(kSubK % 2 == 0 || kSubK == 1, "fragment ping-pong needs an even group count");
     static_assert(kLoadsA * kWaves * 1024 == kABytes && kLoadsB * kWaves * 1024 == kBBytes,
                   "tile bytes must split evenly into 1 KiB wave-loads");
-    static_assert(kWaveM % 32 == 0 && kWaveN % 32 == 0, "wave tile made of 32x32 MFMA tiles");
+    static_assert(kMfma == 32 || kMfma == 16, "32x32x32 or 16x16x64 MFMA");
+    static_assert(kBK % kMfmaK == 0, "whole MFMA k-groups per tile");
+    static_assert(kWaveM % 32 == 0 && kWaveN % 32 == 0, "wave tile of whole 32-row passes");
     static_assert(kStages >= 2, "at least double buffering");
     static_assert(kLoads * (kStages - 1) < 64, "vmcnt counter range");
     static_assert(kLdsBytes <= 160 * 1024, "gfx950 LDS per workgroup");
@@ -143,9 +158,9 @@ __device__ __forceinline__ void block_barrier()
     asm volatile("" ::: "memory");
 }
 
-// One 32-deep MFMA group: MFMAs and the DS reads of the next fragments
-// alternate, then the remaining MFMAs follow.  The first MFMA stays ahead of
-// the reads so it waits only on fragments read one group earlier.
+// One MFMA k-group (32 x 32 x 32 form): MFMAs and the DS reads of the next
+// fragments alternate, then the remaining MFMAs follow.  The first MFMA stays
+// ahead of the reads so it waits only on fragments read one group earlier.
 template <int NMFMA, int NDS, int ID>
 __device__ __forceinline__ void interleave_mfma_ds()
 {
@@ -184,6 +199,189 @@ __device__ __forceinline__ void interleave_mfma_vmem_ds()
     interleave_step<0, kSteps, NVMEM, NDS, ID>();
 }
 
+// One 16 x 16 x 64 k-group (FragPipe): per A row, its NB MFMAs, then the
+// read of that row's next A fragment (and of one next B fragment in the
+// first NB rows) and its share of NVMEM global -> LDS loads.
+template <int I, int ROWS, int NB, int NVMEM, int ID>
+__device__ __forceinline__ void interleave_rows16()
+{
+    if constexpr(I < ROWS) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, NB, ID);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, I < NB ? 2 : 1, ID);
+        constexpr int nv = (I + 1) * NVMEM / ROWS - I * NVMEM / ROWS;
+        if constexpr(nv > 0) __builtin_amdgcn_sched_group_barrier(kSchedVmemRd, nv, ID);
+        interleave_rows16<I + 1, ROWS, NB, NVMEM, ID>();
+    }
+}
+
+// The int32 accumulators of one wave tile, in the lane layout of the tile's
+// MFMA (srcA = B fragment, srcB = A fragment, so D[n][m]).  Epilogues see
+// them as quads: 4 outputs of one row m at 4 consecutive columns n, quad
+// (qm, qn) at wave-tile row row(qm) and first column col(qn):
+//   MFMA 32: r[i][j] is the 32 x 32 block (i, j); quad (qm, qn) is
+//     r[qm][qn / 4][4 (qn % 4) ...], m = 32 qm + lane % 32,
+//     n = 32 (qn / 4) + 8 (qn % 4) + 4 (lane / 32);
+//   MFMA 16: r[i][j] is the 16 x 16 block (i, j) and quad (i, j) itself,
+//     m = 16 qm + lane % 16, n = 16 qn + 4 (lane / 16).
+// Quads are numbered q = qm * kQuadsN + qn (the K-split partial layout).
+template <class C>
+struct Acc {
+    static constexpr bool kBig    = C::kMfma == 32;
+    static constexpr int  kQuadsM = C::kTilesM;
+    static constexpr int  kQuadsN = kBig ? C::kTilesN * 4 : C::kTilesN;
+    static constexpr int  kQuads  = kQuadsM * kQuadsN;
+    using Block                   = std::conditional_t<kBig, v16i, v4i>;
+    Block r[C::kTilesM][C::kTilesN];
+
+    __device__ static __forceinline__ int row(int qm, int lane)
+    {
+        return kBig ? qm * 32 + (lane & 31) : qm * 16 + (lane & 15);
+    }
+    __device__ static __forceinline__ int col(int qn, int lane)
+    {
+        return kBig ? (qn >> 2) * 32 + (qn & 3) * 8 + (lane >> 5) * 4 : qn * 16 + (lane >> 4) * 4;
+    }
+    __device__ __forceinline__ void zero()
+    {
+#pragma unroll
+        for(int i = 0; i < C::kTilesM; ++i)
+#pragma unroll
+            for(int j = 0; j < C::kTilesN; ++j) r[i][j] = Block{0};
+    }
+    __device__ __forceinline__ v4i quad(int qm, int qn) const
+    {
+        if constexpr(kBig) {
+            const v16i& b = r[qm][qn >> 2];
+            const int   o = (qn & 3) * 4;
+            return v4i{b[o], b[o + 1], b[o + 2], b[o + 3]};
+        } else {
+            return r[qm][qn];
+        }
+    }
+    __device__ __forceinline__ void add(int qm, int qn, const v4i& v)
+    {
+        if constexpr(kBig) {
+            v16i&     b = r[qm][qn >> 2];
+            const int o = (qn & 3) * 4;
+            b[o] += v.x, b[o + 1] += v.y, b[o + 2] += v.z, b[o + 3] += v.w;
+        } else {
+            r[qm][qn] += v;
+        }
+    }
+    // r += the products of one k-group's fragments
+    __device__ __forceinline__ void mfma(const v4i (&af)[C::kTilesM], const v4i (&bf)[C::kTilesN])
+    {
+#pragma unroll
+        for(int i = 0; i < C::kTilesM; ++i)
+#pragma unroll
+            for(int j = 0; j < C::kTilesN; ++j) {
+                if constexpr(kBig)
+                    r[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], r[i][j], 0, 0, 0);
+                else
+                    r[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[j], af[i], r[i][j], 0, 0, 0);
+            }
+    }
+};
+
+// LDS -> register fragments of one k-group.  Fragment t of A covers wave-tile
+// rows [t kMfma, (t + 1) kMfma): lane l reads row t kMfma + l % kMfma, 16
+// bytes at k-chunk (kMfmaK / 16) g + l / kMfma of the k-tile, i.e. the
+// chunk it was swizzled to (same rule as the loads).  B alike.  Both
+// operands use the same lane -> k mapping, so the sum over k is the full dot
+// product whatever order the MFMA reduces it in.  The row's swizzle bits lie
+// below bit 4, so they come from the lane alone.
+template <class C>
+struct FragReader {
+    using FragA = v4i[C::kTilesM];
+    using FragB = v4i[C::kTilesN];
+    int offa, offb;       // byte offsets of fragment 0 within a stage
+    int cofs[C::kSubK];   // byte offset of each k-group's chunk
+
+    __device__ __forceinline__ FragReader(int wm, int wn, int lane)
+    {
+        const int frow = lane % C::kMfma;
+        const int fswz = (frow >> C::kSwzShift) & (C::kChunks - 1);
+        offa           = (wm * C::kWaveM + frow) * C::kBK;
+        offb           = C::kABytes + (wn * C::kWaveN + frow) * C::kBK;
+        constexpr int kPerG = C::kMfmaK / 16; // 16-byte k-chunks per lane group and k-group
+#pragma unroll
+        for(int g = 0; g < C::kSubK; ++g)
+            cofs[g] = ((kPerG * g + lane / C::kMfma) ^ fswz) * 16;
+    }
+    __device__ __forceinline__ v4i a(const int8_t* sbase, int g, int t) const
+    {
+        return *reinterpret_cast<const v4i*>(sbase + offa + t * C::kMfma * C::kBK + cofs[g]);
+    }
+    __device__ __forceinline__ v4i b(const int8_t* sbase, int g, int t) const
+    {
+        return *reinterpret_cast<const v4i*>(sbase + offb + t * C::kMfma * C::kBK + cofs[g]);
+    }
+    __device__ __forceinline__ void load(const int8_t* sbase, int g, FragA& af, FragB& bf) const
+    {
+#pragma unroll
+        for(int t = 0; t < C::kTilesM; ++t) af[t] = a(sbase, g, t);
+#pragma unroll
+        for(int t = 0; t < C::kTilesN; ++t) bf[t] = b(sbase, g, t);
+    }
+};
+
+// The k-loop's fragment registers, and one k-group of MFMAs with the reads of
+// the next k-group's fragments interleaved.  Slot s = k-group parity (even
+// kSubK, so k-group g of every k-tile uses slot g & 1).
+//   MFMA 32: two full fragment sets; a group reads the next into the other.
+//   MFMA 16: one A set: the next group's A fragment t is read into fragment
+//     t's registers right after row t's MFMAs have issued, (kTilesM - 1)
+//     kTilesN MFMAs before its first use; B ping-pongs, its next fragments
+//     read during the first rows.  Fragments take 64 VGPRs instead of 96,
+//     which keeps the 128 x 64 wave tile's loop within 256 VGPRs.
+// NVMEM: global -> LDS loads issued just before, spread over the group.
+template <class C>
+struct FragPipe {
+    static constexpr bool kBig = C::kMfma == 32;
+    static constexpr int  kMfmaN = C::kTilesM * C::kTilesN;
+    static constexpr int  kDs    = C::kTilesM + C::kTilesN;
+    static_assert(kBig || C::kTilesN <= C::kTilesM, "B reads spread over the first rows");
+    FragReader<C> fr;
+    v4i           fa[kBig ? 2 : 1][C::kTilesM];
+    v4i           fb[2][C::kTilesN];
+
+    __device__ __forceinline__ FragPipe(int wm, int wn, int lane) : fr(wm, wn, lane) {}
+
+    __device__ __forceinline__ void first(const int8_t* sbase) { fr.load(sbase, 0, fa[0], fb[0]); }
+
+    template <int NVMEM>
+    __device__ __forceinline__ void step(Acc<C>& acc, int s, const int8_t* sbase_n, int g_n)
+    {
+        if constexpr(kBig) {
+            fr.load(sbase_n, g_n, fa[s ^ 1], fb[s ^ 1]);
+            acc.mfma(fa[s], fb[s]);
+            if constexpr(NVMEM > 0)
+                interleave_mfma_vmem_ds<kMfmaN, NVMEM, kDs, 1>();
+            else
+                interleave_mfma_ds<kMfmaN, kDs, 0>();
+        } else {
+#pragma unroll
+            for(int i = 0; i < C::kTilesM; ++i) {
+#pragma unroll
+                for(int j = 0; j < C::kTilesN; ++j)
+                    acc.r[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb[s][j], fa[0][i],
+                                                                         acc.r[i][j], 0, 0, 0);
+                fa[0][i] = fr.a(sbase_n, g_n, i);
+                if(i < C::kTilesN) fb[s ^ 1][i] = fr.b(sbase_n, g_n, i);
+            }
+            interleave_rows16<0, C::kTilesM, C::kTilesN, NVMEM, (NVMEM > 0 ? 1 : 0)>();
+        }
+    }
+    // a k-group with no fragments to read next: MFMAs only, with the NVMEM
+    // global -> LDS loads issued just before spread over them
+    template <int NVMEM = 0>
+    __device__ __forceinline__ void last(Acc<C>& acc, int s)
+    {
+        acc.mfma(fa[kBig ? s : 0], fb[s]);
+        if constexpr(NVMEM > 0) interleave_mfma_vmem_ds<kMfmaN, NVMEM, 0, 1>();
+    }
+};
+
 // Store 4 consecutive-n outputs of one lane.
 template <int OUT>
 __device__ __forceinline__ void store4(const KArgs& p, uint32_t m, uint32_t n, const int* v,
@@ -221,68 +419,64 @@ __device__ __forceinline__ void store4(const KArgs& p, uint32_t m, uint32_t n, c
     }
 }
 
-// Dequant scales of one lane's outputs in a wave tile: sa for each 32-row
-// MFMA tile (row m = lane % 32), sb for each run of 4 columns.  Tensor-scale
-// mode (no scale vectors) folds tsa * tsb into sa and sets sb to 1, which is
-// exact, so every output is (acc * sa) * sb.  On tiles that lie inside the
-// matrix the loads are unconditional: they all go out back to back and the
-// epilogue waits for them once (per-group guarded loads each waited for
-// their own result and serialized eight memory latencies).
+// Dequant scales of one lane's outputs in a wave tile (quad layout of
+// Acc<C>): sa[qm] for the lane's row in each quad row, sb[qn] for each run
+// of 4 columns.  Tensor-scale mode (no scale vectors) folds tsa * tsb into sa
+// and sets sb to 1, which is exact, so every output is (acc * sa) * sb.  On
+// tiles that lie inside the matrix the loads are unconditional: they all go
+// out back to back and the epilogue waits for them once (per-group guarded
+// loads each waited for their own result and serialized eight memory
+// latencies).
 template <class C>
 struct EpiScales {
-    float  sa[C::kTilesM];
-    float4 sb[C::kTilesN][4];
+    using A = Acc<C>;
+    float  sa[A::kQuadsM];
+    float4 sb[A::kQuadsN];
 
     __device__ __forceinline__ void load(const KArgs& p, uint32_t m0, uint32_t n0, int wm, int wn,
                                          int lane, int vec_ok)
     {
-        const uint32_t mb = m0 + wm * C::kWaveM + (lane & 31);
-        const uint32_t nb = n0 + wn * C::kWaveN + (lane >> 5) * 4;
+        const uint32_t mb = m0 + wm * C::kWaveM;
+        const uint32_t nb = n0 + wn * C::kWaveN;
         if(p.sa == nullptr && p.sb == nullptr) {
             const float ab = p.tsa * p.tsb;
 #pragma unroll
-            for(int i = 0; i < C::kTilesM; ++i) sa[i] = ab;
+            for(int i = 0; i < A::kQuadsM; ++i) sa[i] = ab;
 #pragma unroll
-            for(int j = 0; j < C::kTilesN; ++j)
-#pragma unroll
-                for(int g = 0; g < 4; ++g) sb[j][g] = make_float4(1.f, 1.f, 1.f, 1.f);
+            for(int j = 0; j < A::kQuadsN; ++j) sb[j] = make_float4(1.f, 1.f, 1.f, 1.f);
             return;
         }
         if(p.sa == nullptr) {
 #pragma unroll
-            for(int i = 0; i < C::kTilesM; ++i) sa[i] = p.tsa;
+            for(int i = 0; i < A::kQuadsM; ++i) sa[i] = p.tsa;
         } else if(m0 + C::kBM <= p.m) {
 #pragma unroll
-            for(int i = 0; i < C::kTilesM; ++i) sa[i] = p.sa[mb + i * 32];
+            for(int i = 0; i < A::kQuadsM; ++i) sa[i] = p.sa[mb + A::row(i, lane)];
         } else {
 #pragma unroll
-            for(int i = 0; i < C::kTilesM; ++i)
-                sa[i] = mb + i * 32 < p.m ? p.sa[mb + i * 32] : p.tsa;
+            for(int i = 0; i < A::kQuadsM; ++i) {
+                const uint32_t m = mb + A::row(i, lane);
+                sa[i]            = m < p.m ? p.sa[m] : p.tsa;
+            }
         }
         if(p.sb == nullptr) {
 #pragma unroll
-            for(int j = 0; j < C::kTilesN; ++j)
-#pragma unroll
-                for(int g = 0; g < 4; ++g) sb[j][g] = make_float4(p.tsb, p.tsb, p.tsb, p.tsb);
+            for(int j = 0; j < A::kQuadsN; ++j) sb[j] = make_float4(p.tsb, p.tsb, p.tsb, p.tsb);
         } else if(vec_ok && n0 + C::kBN <= p.n) {
 #pragma unroll
-            for(int j = 0; j < C::kTilesN; ++j)
-#pragma unroll
-                for(int g = 0; g < 4; ++g)
-                    sb[j][g] = *reinterpret_cast<const float4*>(p.sb + nb + j * 32 + g * 8);
+            for(int j = 0; j < A::kQuadsN; ++j)
+                sb[j] = *reinterpret_cast<const float4*>(p.sb + nb + A::col(j, lane));
         } else {
 #pragma unroll
-            for(int j = 0; j < C::kTilesN; ++j)
-#pragma unroll
-                for(int g = 0; g < 4; ++g) {
-                    const uint32_t n = nb + j * 32 + g * 8;
-                    float4         v = make_float4(p.tsb, p.tsb, p.tsb, p.tsb);
-                    if(n + 0 < p.n) v.x = p.sb[n + 0];
-                    if(n + 1 < p.n) v.y = p.sb[n + 1];
-                    if(n + 2 < p.n) v.z = p.sb[n + 2];
-                    if(n + 3 < p.n) v.w = p.sb[n + 3];
-                    sb[j][g] = v;
-                }
+            for(int j = 0; j < A::kQuadsN; ++j) {
+                const uint32_t n = nb + A::col(j, lane);
+                float4         v = make_float4(p.tsb, p.tsb, p.tsb, p.tsb);
+                if(n + 0 < p.n) v.x = p.sb[n + 0];
+                if(n + 1 < p.n) v.y = p.sb[n + 1];
+                if(n + 2 < p.n) v.z = p.sb[n + 2];
+                if(n + 3 < p.n) v.w = p.sb[n + 3];
+                sb[j] = v;
+            }
         }
     }
 };
@@ -319,8 +513,7 @@ struct StageSwz {
 template <class C>
 __device__ __forceinline__ void epilogue_f16_lds(const KArgs& p, uint32_t m0, uint32_t n0,
                                                  int vec_ok, int8_t* lds, int slot, int lane,
-                                                 int wm, int wn,
-                                                 const v16i (&acc)[C::kTilesM][C::kTilesN],
+                                                 int wm, int wn, const Acc<C>& acc,
                                                  const EpiScales<C>& sc)
 {
     constexpr int kRowBytes  = C::kWaveN * 2;
@@ -333,28 +526,29 @@ __device__ __forceinline__ void epilogue_f16_lds(const KArgs& p, uint32_t m0, ui
     // every wave's fragment reads and LDS loads are done: the ring is free
     block_barrier();
     int8_t* stage = lds + slot * (C::kWaveM * kRowBytes);
+    using A       = Acc<C>;
 #pragma unroll
-    for(int i = 0; i < C::kTilesM; ++i) {
-        const int row = i * 32 + (lane & 31);
+    for(int i = 0; i < A::kQuadsM; ++i) {
+        const int row = A::row(i, lane);
 #pragma unroll
-        for(int j = 0; j < C::kTilesN; ++j) {
+        for(int j = 0; j < A::kQuadsN; ++j) {
+            const int    col    = A::col(j, lane);
+            const v4i    v      = acc.quad(i, j);
+            const float4 sb     = sc.sb[j];
+            const int    vv[4]  = {v.x, v.y, v.z, v.w};
+            const float  sbv[4] = {sb.x, sb.y, sb.z, sb.w};
+            uint32_t     h[4];
+            // two roundings (fp32 product, then fp16), as the reference's
+            // float epilogue does: never one fused mixed-precision multiply
 #pragma unroll
-            for(int g = 0; g < 4; ++g) {
-                const float4 sb     = sc.sb[j][g];
-                const float  sbv[4] = {sb.x, sb.y, sb.z, sb.w};
-                uint32_t     h[4];
-                // two roundings (fp32 product, then fp16), as the reference's
-                // float epilogue does: never one fused mixed-precision multiply
-#pragma unroll
-                for(int e = 0; e < 4; ++e)
-                    h[e] = float_to_half_bits_2step(((float)acc[i][j][g * 4 + e] * sc.sa[i]) * sbv[e]);
-                const int phys = S::chunk(j * 4 + g, row);
-                v2i       pk;
-                pk.x = (int)(h[0] | (h[1] << 16));
-                pk.y = (int)(h[2] | (h[3] << 16));
-                *reinterpret_cast<v2i*>(stage + row * kRowBytes + phys * 16
-                                        + S::half(lane >> 5, row) * 8) = pk;
-            }
+            for(int e = 0; e < 4; ++e)
+                h[e] = float_to_half_bits_2step(((float)vv[e] * sc.sa[i]) * sbv[e]);
+            const int phys = S::chunk(col >> 3, row);
+            v2i       pk;
+            pk.x = (int)(h[0] | (h[1] << 16));
+            pk.y = (int)(h[2] | (h[3] << 16));
+            *reinterpret_cast<v2i*>(stage + row * kRowBytes + phys * 16
+                                    + S::half((col >> 2) & 1, row) * 8) = pk;
         }
     }
     // a wave reads back only what it wrote itself: LDS returns each wave's
@@ -381,12 +575,12 @@ __device__ __forceinline__ void epilogue_f16_lds(const KArgs& p, uint32_t m0, ui
     }
 }
 
-// int32 accumulators of one tile as a K-split partial: register block
-// q = (i * kTilesN + j) * 4 + g (4 ints) of thread t at ints
-// (q * kThreads + t) * 4, so every store and load of a block is contiguous.
+// int32 accumulators of one tile as a K-split partial: quad q of thread t
+// (Acc<C> numbering, 4 ints) at ints (q * kThreads + t) * 4, so every store
+// and load of a quad is contiguous.
 template <class C>
 struct Partial {
-    static constexpr int    kBlocks = C::kTilesM * C::kTilesN * 4;
+    static constexpr int    kBlocks = Acc<C>::kQuads;
     static constexpr size_t kInts   = (size_t)kBlocks * C::kThreads * 4;
     static constexpr size_t kBytes  = kInts * 4;
     // fixup blocks of kFixupWaves waves: the tile's epilogue in kPieces blocks
@@ -402,33 +596,30 @@ constexpr uint32_t kMaxParts     = 8;
 constexpr uint32_t kMinKtPerPart = 16;
 
 template <class C>
-__device__ __forceinline__ void store_partial(int32_t* part,
-                                              const v16i (&acc)[C::kTilesM][C::kTilesN])
+__device__ __forceinline__ void store_partial(int32_t* part, const Acc<C>& acc)
 {
+    using A = Acc<C>;
 #pragma unroll
-    for(int i = 0; i < C::kTilesM; ++i)
+    for(int i = 0; i < A::kQuadsM; ++i)
 #pragma unroll
-        for(int j = 0; j < C::kTilesN; ++j)
-#pragma unroll
-            for(int g = 0; g < 4; ++g) {
-                const int q = (i * C::kTilesN + j) * 4 + g;
-                v4i       v = {acc[i][j][g * 4 + 0], acc[i][j][g * 4 + 1], acc[i][j][g * 4 + 2],
-                               acc[i][j][g * 4 + 3]};
-                *reinterpret_cast<v4i*>(part + ((size_t)q * C::kThreads + threadIdx.x) * 4) = v;
-            }
+        for(int j = 0; j < A::kQuadsN; ++j) {
+            const int q = i * A::kQuadsN + j;
+            *reinterpret_cast<v4i*>(part + ((size_t)q * C::kThreads + threadIdx.x) * 4)
+                = acc.quad(i, j);
+        }
 }
 
 // acc += one partial, for thread `tid` of the tile's layout.  The loads go out
 // in batches of kBatch into a register array before any add, so a thread
 // keeps kBatch loads in flight.
 template <class C>
-__device__ __forceinline__ void add_partial(const int32_t* part, uint32_t tid,
-                                            v16i (&acc)[C::kTilesM][C::kTilesN])
+__device__ __forceinline__ void add_partial(const int32_t* part, uint32_t tid, Acc<C>& acc)
 {
-    constexpr int kBatch = Partial<C>::kBlocks < 16 ? Partial<C>::kBlocks : 16;
-    static_assert(Partial<C>::kBlocks % kBatch == 0, "whole batches");
+    using A              = Acc<C>;
+    constexpr int kBatch = A::kQuads < 16 ? A::kQuads : 16;
+    static_assert(A::kQuads % kBatch == 0, "whole batches");
 #pragma unroll
-    for(int b = 0; b < Partial<C>::kBlocks; b += kBatch) {
+    for(int b = 0; b < A::kQuads; b += kBatch) {
         v4i v[kBatch];
 #pragma unroll
         for(int x = 0; x < kBatch; ++x)
@@ -436,21 +627,16 @@ __device__ __forceinline__ void add_partial(const int32_t* part, uint32_t tid,
                 part + ((size_t)(b + x) * C::kThreads + tid) * 4));
         __builtin_amdgcn_sched_barrier(0); // every load of the batch issued before the adds
 #pragma unroll
-        for(int x = 0; x < kBatch; ++x) {
-            const int q = b + x, i = q / (4 * C::kTilesN), j = (q / 4) % C::kTilesN, g = q % 4;
-            acc[i][j][g * 4 + 0] += v[x].x;
-            acc[i][j][g * 4 + 1] += v[x].y;
-            acc[i][j][g * 4 + 2] += v[x].z;
-            acc[i][j][g * 4 + 3] += v[x].w;
-        }
+        for(int x = 0; x < kBatch; ++x)
+            acc.add((b + x) / A::kQuadsN, (b + x) % A::kQuadsN, v[x]);
     }
 }
 
 template <class C, int OUT>
 __device__ __forceinline__ void tile_epilogue_sc(const KArgs& p, uint32_t m0, uint32_t n0,
                                                  int vec_ok, int8_t* lds,
-                                                 const v16i (&acc)[C::kTilesM][C::kTilesN],
-                                                 int wave_base, const EpiScales<C>& sc);
+                                                 const Acc<C>& acc, int wave_base,
+                                                 const EpiScales<C>& sc);
 
 // The int32 accumulators of one BM x BN output tile at (m0, n0) of problem
 // p over k-tiles [kt0, kt0 + nk) (nk >= 1), computed by the whole block;
@@ -460,8 +646,7 @@ __device__ __forceinline__ void tile_epilogue_sc(const KArgs& p, uint32_t m0, ui
 template <class C, bool SCALES>
 __device__ __forceinline__ void gemm_tile_acc(const KArgs& p, uint32_t m0, uint32_t n0,
                                               int vec_ok, int8_t* lds, uint32_t kt0,
-                                              uint32_t nk, v16i (&acc)[C::kTilesM][C::kTilesN],
-                                              EpiScales<C>& sc)
+                                              uint32_t nk, Acc<C>& acc, EpiScales<C>& sc)
 {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); // wave-uniform
     const int lane = threadIdx.x % kWave;
@@ -517,47 +702,9 @@ __device__ __forceinline__ void gemm_tile_acc(const KArgs& p, uint32_t m0, uint3
         }
     };
 
-    // ---- LDS -> register fragment offsets ----------------------------------
-    // Fragment row = lane % 32 of a 32-row tile; k-chunk = 2*g + lane / 32 for
-    // MFMA group g.  Both operands use the same lane -> k mapping, so the sum
-    // over k is the full dot product whatever order the MFMA reduces it in.
-    const int frow = lane & 31;
-    const int fswz = (frow >> C::kSwzShift) & (C::kChunks - 1);
-    int       offa[C::kTilesM], offb[C::kTilesN];
-#pragma unroll
-    for(int t = 0; t < C::kTilesM; ++t) offa[t] = (wm * C::kWaveM + t * 32 + frow) * C::kBK;
-#pragma unroll
-    for(int t = 0; t < C::kTilesN; ++t)
-        offb[t] = C::kABytes + (wn * C::kWaveN + t * 32 + frow) * C::kBK;
-    int cofs[C::kSubK];
-#pragma unroll
-    for(int g = 0; g < C::kSubK; ++g) cofs[g] = ((2 * g + (lane >> 5)) ^ fswz) * 16;
-
-#pragma unroll
-    for(int i = 0; i < C::kTilesM; ++i)
-#pragma unroll
-        for(int j = 0; j < C::kTilesN; ++j) acc[i][j] = v16i{0};
-
-    using FragA = v4i[C::kTilesM];
-    using FragB = v4i[C::kTilesN];
-    auto load_frags = [&](const int8_t* sbase, int g, FragA& af, FragB& bf) {
-#pragma unroll
-        for(int t = 0; t < C::kTilesM; ++t)
-            af[t] = *reinterpret_cast<const v4i*>(sbase + offa[t] + cofs[g]);
-#pragma unroll
-        for(int t = 0; t < C::kTilesN; ++t)
-            bf[t] = *reinterpret_cast<const v4i*>(sbase + offb[t] + cofs[g]);
-    };
-    auto mfma_tile = [&](const FragA& af, const FragB& bf) {
-#pragma unroll
-        for(int i = 0; i < C::kTilesM; ++i)
-#pragma unroll
-            for(int j = 0; j < C::kTilesN; ++j)
-                acc[i][j]
-                    = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], acc[i][j], 0, 0, 0);
-    };
-    constexpr int kMfma = C::kTilesM * C::kTilesN;
-    constexpr int kDs   = C::kTilesM + C::kTilesN;
+    // ---- LDS -> register fragments (FragPipe) --------------------------------
+    FragPipe<C> fp(wm, wn, lane);
+    acc.zero();
 
     // ---- prologue: fill every stage of the ring ----------------------------
     // Tiles past K are still issued (every lane then reads kOob: zeros, no
@@ -567,44 +714,32 @@ __device__ __forceinline__ void gemm_tile_acc(const KArgs& p, uint32_t m0, uint3
     for(int s = 0; s < C::kStages; ++s) issue_stage(s, s);
     wait_vmcnt<C::kLoads * (C::kStages - 1)>(); // tile 0 landed
     block_barrier();
-
-    FragA fa[2];
-    FragB fb[2];
-    load_frags(lds, 0, fa[0], fb[0]);
+    fp.first(lds);
 
     // ---- main loop (the last tile is peeled: one path for the waitcnt pass) -
-    // Per tile kt: MFMA groups 0..S-2 read the next group's fragments as they
+    // Per tile kt: k-groups 0..S-2 read the next group's fragments as they
     // go; then [all reads of stage kt done, tile kt+1 landed] barrier; the
     // last group refills stage kt with tile kt+S and reads tile kt+1 group 0.
     for(uint32_t kt = 0; kt + 1 < nk; ++kt) {
         const int8_t* sbase = lds + (kt % C::kStages) * C::kStageBytes;
 #pragma unroll
-        for(int g = 0; g + 1 < C::kSubK; ++g) {
-            load_frags(sbase, g + 1, fa[(g + 1) & 1], fb[(g + 1) & 1]);
-            mfma_tile(fa[g & 1], fb[g & 1]);
-            interleave_mfma_ds<kMfma, kDs, 0>();
-        }
+        for(int g = 0; g + 1 < C::kSubK; ++g) fp.template step<0>(acc, g & 1, sbase, g + 1);
         constexpr int gl = C::kSubK - 1;
         __builtin_amdgcn_sched_barrier(0);
         wait_lgkmcnt0(); // this wave's reads of stage kt are done before it is refilled
         wait_vmcnt<C::kLoads * (C::kStages - 2)>(); // tile kt+1 landed
         block_barrier();
         issue_stage(kt % C::kStages, kt + C::kStages);
-        load_frags(lds + ((kt + 1) % C::kStages) * C::kStageBytes, 0, fa[(gl + 1) & 1],
-                   fb[(gl + 1) & 1]);
-        mfma_tile(fa[gl & 1], fb[gl & 1]);
-        interleave_mfma_vmem_ds<kMfma, C::kLoads, kDs, 1>();
+        fp.template step<C::kLoads>(acc, gl & 1, lds + ((kt + 1) % C::kStages) * C::kStageBytes,
+                                    0);
     }
     // the fp16 epilogue's scales load while the last tile's MFMAs run
     if constexpr(SCALES) sc.load(p, m0, n0, wm, wn, lane, vec_ok);
     {
         const int8_t* sbase = lds + ((nk - 1) % C::kStages) * C::kStageBytes;
 #pragma unroll
-        for(int g = 0; g + 1 < C::kSubK; ++g) {
-            load_frags(sbase, g + 1, fa[(g + 1) & 1], fb[(g + 1) & 1]);
-            mfma_tile(fa[g & 1], fb[g & 1]);
-        }
-        mfma_tile(fa[(C::kSubK - 1) & 1], fb[(C::kSubK - 1) & 1]);
+        for(int g = 0; g + 1 < C::kSubK; ++g) fp.template step<0>(acc, g & 1, sbase, g + 1);
+        fp.last(acc, (C::kSubK - 1) & 1);
     }
     wait_vmcnt<0>(); // no global->LDS write may outlive the workgroup's LDS
 }
@@ -619,7 +754,7 @@ __device__ __forceinline__ void gemm_tile(const KArgs& p, uint32_t m0, uint32_t 
                                           int8_t* lds, uint32_t kt0 = 0, uint32_t nkt = 0,
                                           int32_t* part = nullptr)
 {
-    v16i         acc[C::kTilesM][C::kTilesN];
+    Acc<C>       acc;
     EpiScales<C> sc;
     if constexpr(PART) {
         gemm_tile_acc<C, false>(p, m0, n0, vec_ok, lds, kt0, nkt, acc, sc);
@@ -631,15 +766,14 @@ __device__ __forceinline__ void gemm_tile(const KArgs& p, uint32_t m0, uint32_t 
     }
 }
 
-// acc[i][j][r]: m = m0 + wm*kWaveM + i*32 + lane%32,
-//               n = n0 + wn*kWaveN + j*32 + (r/4)*8 + (lane/32)*4 + r%4.
+// Quad (qm, qn) of a wave's Acc<C> holds outputs m = m0 + wm*kWaveM +
+// row(qm), n = n0 + wn*kWaveN + col(qn) + 0..3.
 // A block may hold only waves wave_base, wave_base + 1, ... of the tile (the
 // split-tile fixup); each wave stages through LDS slice threadIdx.x / 64.
 // sc: the fp16 path's scales, loaded by the caller (unused for int32 output).
 template <class C, int OUT>
 __device__ __forceinline__ void tile_epilogue_sc(const KArgs& p, uint32_t m0, uint32_t n0,
-                                                 int vec_ok, int8_t* lds,
-                                                 const v16i (&acc)[C::kTilesM][C::kTilesN],
+                                                 int vec_ok, int8_t* lds, const Acc<C>& acc,
                                                  int wave_base, const EpiScales<C>& sc)
 {
     const int   slot  = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -653,31 +787,18 @@ __device__ __forceinline__ void tile_epilogue_sc(const KArgs& p, uint32_t m0, ui
         epilogue_f16_lds<C>(p, m0, n0, vec_ok, lds, slot, lane, wm, wn, acc, sc);
         return;
     }
+    // int32 output: straight from the registers
+    using A = Acc<C>;
 #pragma unroll
-    for(int i = 0; i < C::kTilesM; ++i) {
-        const uint32_t m  = m0 + wm * C::kWaveM + i * 32 + (lane & 31);
-        float          sa = p.tsa;
-        if(OUT == W8A8_OUT_F16 && p.sa != nullptr && m < p.m) sa = p.sa[m];
+    for(int i = 0; i < A::kQuadsM; ++i) {
+        const uint32_t m = m0 + wm * C::kWaveM + A::row(i, lane);
 #pragma unroll
-        for(int j = 0; j < C::kTilesN; ++j) {
-#pragma unroll
-            for(int g = 0; g < 4; ++g) {
-                const uint32_t n  = n0 + wn * C::kWaveN + j * 32 + g * 8 + (lane >> 5) * 4;
-                float4         sb = make_float4(p.tsb, p.tsb, p.tsb, p.tsb);
-                if(OUT == W8A8_OUT_F16 && p.sb != nullptr) {
-                    if(vec_ok && n + 4 <= p.n)
-                        sb = *reinterpret_cast<const float4*>(p.sb + n);
-                    else {
-                        if(n + 0 < p.n) sb.x = p.sb[n + 0];
-                        if(n + 1 < p.n) sb.y = p.sb[n + 1];
-                        if(n + 2 < p.n) sb.z = p.sb[n + 2];
-                        if(n + 3 < p.n) sb.w = p.sb[n + 3];
-                    }
-                }
-                const int v[4] = {acc[i][j][g * 4 + 0], acc[i][j][g * 4 + 1],
-                                  acc[i][j][g * 4 + 2], acc[i][j][g * 4 + 3]};
-                store4<OUT>(p, m, n, v, sa, sb, ab, mode1, vec_ok != 0);
-            }
+        for(int j = 0; j < A::kQuadsN; ++j) {
+            const uint32_t n    = n0 + wn * C::kWaveN + A::col(j, lane);
+            const v4i      q    = acc.quad(i, j);
+            const int      v[4] = {q.x, q.y, q.z, q.w};
+            store4<OUT>(p, m, n, v, p.tsa, make_float4(p.tsb, p.tsb, p.tsb, p.tsb), ab, mode1,
+                        vec_ok != 0);
         }
     }
 }
@@ -686,8 +807,7 @@ __device__ __forceinline__ void tile_epilogue_sc(const KArgs& p, uint32_t m0, ui
 // grouped and MoE fixups): one batch of scale loads, then the epilogue.
 template <class C, int OUT>
 __device__ __forceinline__ void tile_epilogue(const KArgs& p, uint32_t m0, uint32_t n0,
-                                              int vec_ok, int8_t* lds,
-                                              const v16i (&acc)[C::kTilesM][C::kTilesN],
+                                              int vec_ok, int8_t* lds, const Acc<C>& acc,
                                               int wave_base = 0)
 {
     EpiScales<C> sc;
@@ -747,11 +867,8 @@ __global__ void __launch_bounds__(Partial<C>::kFixupWaves * kWave, 1)
     const int      wave_base = (int)(blockIdx.x % Partial<C>::kPieces) * Partial<C>::kFixupWaves;
     uint32_t       tm, tn;
     tile_coords<C::kGroupM>(slot, tiles_m, tiles_n, tm, tn);
-    v16i acc[C::kTilesM][C::kTilesN];
-#pragma unroll
-    for(int i = 0; i < C::kTilesM; ++i)
-#pragma unroll
-        for(int j = 0; j < C::kTilesN; ++j) acc[i][j] = v16i{0};
+    Acc<C> acc;
+    acc.zero();
     const uint32_t tid = wave_base * kWave + threadIdx.x;
     for(uint32_t part = 0; part < parts; ++part)
         add_partial<C>(ws + (size_t)(slot * parts + part) * Partial<C>::kInts, tid, acc);

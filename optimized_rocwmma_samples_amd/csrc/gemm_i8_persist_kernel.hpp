@@ -37,9 +37,11 @@ struct Persist {
     static constexpr int kRowBytes    = C::kWaveN * 2;           // one staged fp16 row
     static constexpr int kRowChunks   = kRowBytes / 16;
     static constexpr int kRowsPerSt   = kWave / kRowChunks;       // rows per wave store
-    static constexpr int kPassRows    = 32;                       // one MFMA tile row
+    static constexpr int kPassRows    = 32;                       // rows staged per pass
+    static constexpr int kPasses      = C::kWaveM / kPassRows;
+    static constexpr int kQmPerPass   = kPassRows / C::kMfma;     // quad rows per pass
     static constexpr int kStPerPass   = kPassRows / kRowsPerSt;
-    static constexpr int kStores      = C::kTilesM * kStPerPass;  // per wave per tile
+    static constexpr int kStores      = kPasses * kStPerPass;     // per wave per tile
     static constexpr int kSliceBytes  = kPassRows * kRowBytes;    // per wave
     static constexpr int kLdsBytes    = C::kLdsBytes + C::kWaves * kSliceBytes;
     static_assert(kRowChunks == 4 || kRowChunks == 8 || kRowChunks == 16, "row of 4-16 chunks");
@@ -59,35 +61,37 @@ struct Persist {
 template <class C>
 __device__ __forceinline__ void epilogue_f16_persist(const KArgs& p, __amdgpu_buffer_rsrc_t rc,
                                                      uint32_t m0, uint32_t n0, int8_t* slice,
-                                                     int lane, int wm, int wn,
-                                                     const v16i (&acc)[C::kTilesM][C::kTilesN],
+                                                     int lane, int wm, int wn, const Acc<C>& acc,
                                                      const EpiScales<C>& sc, int nt)
 {
     using P               = Persist<C>;
     using S               = StageSwz<P::kRowChunks>;
+    using A               = Acc<C>;
     const int      chunk  = lane % P::kRowChunks;
     const uint32_t n      = n0 + wn * C::kWaveN + chunk * 8;
     const bool     n_in   = n < p.n;
 #pragma unroll
-    for(int i = 0; i < C::kTilesM; ++i) {
-        const int row = lane & 31;
+    for(int pass = 0; pass < P::kPasses; ++pass) {
 #pragma unroll
-        for(int j = 0; j < C::kTilesN; ++j) {
+        for(int i = pass * P::kQmPerPass; i < (pass + 1) * P::kQmPerPass; ++i) {
+            const int row = A::row(i, lane) - pass * P::kPassRows; // row within the slice
 #pragma unroll
-            for(int g = 0; g < 4; ++g) {
-                const float4 sb     = sc.sb[j][g];
+            for(int j = 0; j < A::kQuadsN; ++j) {
+                const int    col    = A::col(j, lane);
+                const v4i    v      = acc.quad(i, j);
+                const float4 sb     = sc.sb[j];
+                const int    vv[4]  = {v.x, v.y, v.z, v.w};
                 const float  sbv[4] = {sb.x, sb.y, sb.z, sb.w};
                 uint32_t     h[4];
 #pragma unroll
                 for(int e = 0; e < 4; ++e)
-                    h[e] = float_to_half_bits_2step(((float)acc[i][j][g * 4 + e] * sc.sa[i])
-                                                    * sbv[e]);
-                const int phys = S::chunk(j * 4 + g, row);
+                    h[e] = float_to_half_bits_2step(((float)vv[e] * sc.sa[i]) * sbv[e]);
+                const int phys = S::chunk(col >> 3, row);
                 v2i       pk;
                 pk.x = (int)(h[0] | (h[1] << 16));
                 pk.y = (int)(h[2] | (h[3] << 16));
                 *reinterpret_cast<v2i*>(slice + row * P::kRowBytes + phys * 16
-                                        + S::half(lane >> 5, row) * 8) = pk;
+                                        + S::half((col >> 2) & 1, row) * 8) = pk;
             }
         }
         // read back row-contiguous (a wave's LDS accesses complete in order,
@@ -97,7 +101,7 @@ __device__ __forceinline__ void epilogue_f16_persist(const KArgs& p, __amdgpu_bu
             const int      r    = q * P::kRowsPerSt + lane / P::kRowChunks;
             const int      phys = S::chunk(chunk, r);
             const v4i      v    = S::unswap(*reinterpret_cast<const v4i*>(slice + r * P::kRowBytes + phys * 16), r);
-            const uint32_t m    = m0 + wm * C::kWaveM + i * 32 + r;
+            const uint32_t m    = m0 + wm * C::kWaveM + pass * P::kPassRows + r;
             const uint32_t off  = (m < p.m && n_in) ? (m * p.ldc + n) * 2 : kOob;
             if(nt)
                 __builtin_amdgcn_raw_buffer_store_b128(v, rc, off, 0, kCpolNonTemporal);
@@ -206,39 +210,8 @@ __global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_persist_kernel(KArgs p
     };
 
     // ---- LDS -> register fragments (as in gemm_tile) -------------------------
-    const int frow = lane & 31;
-    const int fswz = (frow >> C::kSwzShift) & (C::kChunks - 1);
-    int       offa[C::kTilesM], offb[C::kTilesN];
-#pragma unroll
-    for(int t = 0; t < C::kTilesM; ++t) offa[t] = (wm * C::kWaveM + t * 32 + frow) * C::kBK;
-#pragma unroll
-    for(int t = 0; t < C::kTilesN; ++t)
-        offb[t] = C::kABytes + (wn * C::kWaveN + t * 32 + frow) * C::kBK;
-    int cofs[C::kSubK];
-#pragma unroll
-    for(int g = 0; g < C::kSubK; ++g) cofs[g] = ((2 * g + (lane >> 5)) ^ fswz) * 16;
-
-    using FragA = v4i[C::kTilesM];
-    using FragB = v4i[C::kTilesN];
-    auto load_frags = [&](const int8_t* sbase, int g, FragA& af, FragB& bf) {
-#pragma unroll
-        for(int t = 0; t < C::kTilesM; ++t)
-            af[t] = *reinterpret_cast<const v4i*>(sbase + offa[t] + cofs[g]);
-#pragma unroll
-        for(int t = 0; t < C::kTilesN; ++t)
-            bf[t] = *reinterpret_cast<const v4i*>(sbase + offb[t] + cofs[g]);
-    };
-    v16i acc[C::kTilesM][C::kTilesN];
-    auto mfma_tile = [&](const FragA& af, const FragB& bf) {
-#pragma unroll
-        for(int i = 0; i < C::kTilesM; ++i)
-#pragma unroll
-            for(int j = 0; j < C::kTilesN; ++j)
-                acc[i][j]
-                    = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], acc[i][j], 0, 0, 0);
-    };
-    constexpr int kMfma = C::kTilesM * C::kTilesN;
-    constexpr int kDs   = C::kTilesM + C::kTilesN;
+    FragPipe<C> fp(wm, wn, lane);
+    Acc<C>      acc;
 
     int8_t* slice = lds + C::kLdsBytes + wave * P::kSliceBytes;
 
@@ -248,9 +221,7 @@ __global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_persist_kernel(KArgs p
     wait_vmcnt<C::kLoads * (C::kStages - 1)>();
     block_barrier();
 
-    FragA fa[2];
-    FragB fb[2];
-    load_frags(lds, 0, fa[0], fb[0]);
+    fp.first(lds);
 
     // ---- tiles ----------------------------------------------------------------
     // Every k-step: MFMA groups 0..S-2 read the next group's fragments; then
@@ -259,15 +230,14 @@ __global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_persist_kernel(KArgs p
     // tile's), and the last group reads the next k-step's group 0.
     uint32_t step = 0;
     // one k-step; after_epi: the previous tile's epilogue stores are the
-    // youngest memory operations and may stay in flight at the wait
-    auto kstep = [&](bool after_epi) {
+    // youngest memory operations and may stay in flight at the wait.
+    // last: the tile's last k-step, whose final k-group reads no fragments;
+    // the next k-step's first ones are read after the epilogue, so they do
+    // not occupy registers through it.
+    auto kstep = [&](bool after_epi, auto last) {
         const int8_t* sbase = lds + (step % C::kStages) * C::kStageBytes;
 #pragma unroll
-        for(int g = 0; g + 1 < C::kSubK; ++g) {
-            load_frags(sbase, g + 1, fa[(g + 1) & 1], fb[(g + 1) & 1]);
-            mfma_tile(fa[g & 1], fb[g & 1]);
-            interleave_mfma_ds<kMfma, kDs, 0>();
-        }
+        for(int g = 0; g + 1 < C::kSubK; ++g) fp.template step<0>(acc, g & 1, sbase, g + 1);
         constexpr int gl = C::kSubK - 1;
         __builtin_amdgcn_sched_barrier(0);
         wait_lgkmcnt0();
@@ -277,27 +247,32 @@ __global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_persist_kernel(KArgs p
             wait_vmcnt<C::kLoads * (C::kStages - 2)>();
         block_barrier();
         issue_next(step % C::kStages);
-        load_frags(lds + ((step + 1) % C::kStages) * C::kStageBytes, 0, fa[(gl + 1) & 1],
-                   fb[(gl + 1) & 1]);
-        mfma_tile(fa[gl & 1], fb[gl & 1]);
-        interleave_mfma_vmem_ds<kMfma, C::kLoads, kDs, 1>();
+        if constexpr(decltype(last)::value)
+            fp.template last<C::kLoads>(acc, gl & 1);
+        else
+            fp.template step<C::kLoads>(acc, gl & 1,
+                                        lds + ((step + 1) % C::kStages) * C::kStageBytes, 0);
         ++step;
     };
     for(uint32_t j = 0; j < count; ++j) {
         uint32_t m0, n0;
         tile_of(j, m0, n0);
-#pragma unroll
-        for(int i = 0; i < C::kTilesM; ++i)
-#pragma unroll
-            for(int jj = 0; jj < C::kTilesN; ++jj) acc[i][jj] = v16i{0};
-        for(uint32_t kt = 0; kt + 1 < nk; ++kt) kstep(kt == 0 && j > 0);
-        // last k-step peeled: the epilogue's scales load while it runs
+        acc.zero();
+        for(uint32_t kt = 0; kt + 1 < nk; ++kt) kstep(kt == 0 && j > 0, std::false_type{});
+        // last k-step peeled: the epilogue's scales load while it runs.  The
+        // lane id is made opaque per tile so that the epilogue's per-lane
+        // addresses are computed here, not hoisted out of the tile loop and
+        // held in registers across the k-loop
+        int elane = lane;
+        asm volatile("" : "+v"(elane));
         EpiScales<C> sc;
-        sc.load(p, m0, n0, wm, wn, lane, vec_ok);
-        kstep(nk == 1 && j > 0);
+        sc.load(p, m0, n0, wm, wn, elane, vec_ok);
+        kstep(nk == 1 && j > 0, std::true_type{});
         __builtin_amdgcn_sched_barrier(0);
-        epilogue_f16_persist<C>(p, rc, m0, n0, slice, lane, wm, wn, acc, sc, nt);
+        epilogue_f16_persist<C>(p, rc, m0, n0, slice, elane, wm, wn, acc, sc, nt);
         __builtin_amdgcn_sched_barrier(0);
+        // the next k-step (landed at the last barrier, not refilled since)
+        fp.first(lds + (step % C::kStages) * C::kStageBytes);
     }
     wait_vmcnt<0>(); // no global->LDS write may outlive the workgroup's LDS
 }

@@ -84,37 +84,34 @@ size_t sk_workspace_bytes(const SkPlan& s)
 constexpr int kCpolDevice = 16;
 
 template <class C>
-__device__ __forceinline__ void store_partial_dev(int32_t* part,
-                                                  const v16i (&acc)[C::kTilesM][C::kTilesN])
+__device__ __forceinline__ void store_partial_dev(int32_t* part, const Acc<C>& acc)
 {
+    using A = Acc<C>;
     const __amdgpu_buffer_rsrc_t r
         = __builtin_amdgcn_make_buffer_rsrc(part, 0, (int)Partial<C>::kBytes, kBufferFlags);
 #pragma unroll
-    for(int i = 0; i < C::kTilesM; ++i)
+    for(int i = 0; i < A::kQuadsM; ++i)
 #pragma unroll
-        for(int j = 0; j < C::kTilesN; ++j)
-#pragma unroll
-            for(int g = 0; g < 4; ++g) {
-                const int q = (i * C::kTilesN + j) * 4 + g;
-                v4i       v = {acc[i][j][g * 4 + 0], acc[i][j][g * 4 + 1], acc[i][j][g * 4 + 2],
-                               acc[i][j][g * 4 + 3]};
-                __builtin_amdgcn_raw_buffer_store_b128(
-                    v, r, (uint32_t)(q * C::kThreads + threadIdx.x) * 16, 0, kCpolDevice);
-            }
+        for(int j = 0; j < A::kQuadsN; ++j) {
+            const int q = i * A::kQuadsN + j;
+            __builtin_amdgcn_raw_buffer_store_b128(acc.quad(i, j), r,
+                                                   (uint32_t)(q * C::kThreads + threadIdx.x) * 16,
+                                                   0, kCpolDevice);
+        }
 }
 
 // acc += one partial (store_partial layout), read with device scope in
 // batches that keep every load of a batch in flight before the adds.
 template <class C>
-__device__ __forceinline__ void add_partial_dev(const int32_t* part,
-                                                v16i (&acc)[C::kTilesM][C::kTilesN])
+__device__ __forceinline__ void add_partial_dev(const int32_t* part, Acc<C>& acc)
 {
-    constexpr int kBatch = Partial<C>::kBlocks < 8 ? Partial<C>::kBlocks : 8;
-    static_assert(Partial<C>::kBlocks % kBatch == 0, "whole batches");
+    using A              = Acc<C>;
+    constexpr int kBatch = A::kQuads < 8 ? A::kQuads : 8;
+    static_assert(A::kQuads % kBatch == 0, "whole batches");
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<int32_t*>(part), 0, (int)Partial<C>::kBytes, kBufferFlags);
 #pragma unroll
-    for(int b = 0; b < Partial<C>::kBlocks; b += kBatch) {
+    for(int b = 0; b < A::kQuads; b += kBatch) {
         v4i v[kBatch];
 #pragma unroll
         for(int x = 0; x < kBatch; ++x)
@@ -123,13 +120,7 @@ __device__ __forceinline__ void add_partial_dev(const int32_t* part,
                                                  0, kCpolDevice));
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for(int x = 0; x < kBatch; ++x) {
-            const int q = b + x, i = q / (4 * C::kTilesN), j = (q / 4) % C::kTilesN, g = q % 4;
-            acc[i][j][g * 4 + 0] += v[x].x;
-            acc[i][j][g * 4 + 1] += v[x].y;
-            acc[i][j][g * 4 + 2] += v[x].z;
-            acc[i][j][g * 4 + 3] += v[x].w;
-        }
+        for(int x = 0; x < kBatch; ++x) acc.add((b + x) / A::kQuadsN, (b + x) % A::kQuadsN, v[x]);
     }
 }
 
@@ -164,7 +155,7 @@ __global__ void __launch_bounds__(C::kThreads, 1)
         uint32_t tm, tn;
         tile_coords<C::kGroupM>(t0 + t, tiles_m, tiles_n, tm, tn);
         const uint32_t m0 = tm * C::kBM, n0 = tn * C::kBN;
-        v16i           acc[C::kTilesM][C::kTilesN];
+        Acc<C>         acc;
         EpiScales<C>   unused;
         gemm_tile_acc<C, false>(p, m0, n0, vec_ok, lds, k0, k1 - k0, acc, unused);
         if(k0 != 0 || k1 != sk.nk) {

@@ -725,10 +725,10 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-using GemmGrouped = gemm::Cfg<256, 256, 128, 2, 2, 4, 4>;
+using GemmGrouped = gemm::Cfg<256, 256, 128, 2, 2, 4, 4, 16>;
 // MoE GEMM over experts of a few hundred rows: 128-row tiles waste less of
 // each expert's last tile row (moe_tile_rows_128).
-using GemmGroupedMid = gemm::Cfg<128, 256, 128, 3, 2, 4, 4>;
+using GemmGroupedMid = gemm::Cfg<128, 256, 128, 3, 2, 4, 4, 16>;
 
 // 128-row tiles when the fraction of tile rows an expert of average size
 // fills, times their per-op rate relative to 256-row tiles (about 0.8,
@@ -867,7 +867,7 @@ hipError_t launch_moe_combine(const uint16_t* y, uint32_t ldy, uint32_t rows_y, 
     return hipGetLastError();
 }
 
-using GemmGroupedSmall = gemm::Cfg<128, 128, 128, 3, 2, 4, 4>;
+using GemmGroupedSmall = gemm::Cfg<128, 128, 128, 3, 2, 4, 4, 16>;
 
 namespace {
 uint32_t device_cus()
@@ -952,7 +952,8 @@ hipError_t launch_moe_gemm(const MoeGemmArgs& a, hipStream_t stream)
 
 // The SiLU epilogue's tiles: wave tiles 128 columns wide (64 outputs, one
 // 128-byte line of h per row and wave), otherwise as GemmGrouped /
-// GemmGroupedMid.
+// GemmGroupedMid, on the 32 x 32 x 32 MFMA: the gate/up interleave in blocks
+// of 8 rows puts a gate and its up value in one lane only in that layout.
 using GemmSilu    = gemm::Cfg<256, 256, 128, 2, 4, 2, 4>;
 using GemmSiluMid = gemm::Cfg<128, 256, 128, 3, 4, 2, 4>;
 static_assert(GemmSilu::kWaveN == GemmSiluMid::kWaveN, "one pmax layout for both tiles");

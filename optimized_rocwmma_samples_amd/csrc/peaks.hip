@@ -19,10 +19,13 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 constexpr int kChains = 8; // independent accumulators per wave (covers the MFMA latency)
 
 // Each wave: kChains accumulators, `iters` rounds of kChains MFMAs.  The
-// operands are pseudo-random bytes (random: a hash of the lane) or zeros, and
-// are perturbed every round from the accumulators' low bits so the compiler
-// cannot hoist the products; the accumulators are folded into `sink` at the
-// end (one int per wave) so nothing is dead.
+// operands are pseudo-random bytes (random: a hash of the lane) or zeros; an
+// empty asm statement that claims to rewrite them once per round keeps the
+// compiler from hoisting or folding the products, and the accumulators are
+// folded into `sink` at the end (one int per wave) so nothing is dead.  The
+// operands stay the same from round to round: on MI355X, four operand sets
+// rotated through a GEMM-like 4 x 2 fragment order run at the same rate
+// (3.43 against 3.44 POP/s), so changing operands cost nothing measurable.
 __global__ void __launch_bounds__(256) peak_mfma_i8_kernel(int iters, int random, int* sink)
 {
     const uint32_t lane = threadIdx.x % 64;
