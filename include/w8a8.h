@@ -423,11 +423,11 @@ int w8a8_moe_silu_mul_quant(const void* gate_up, uint32_t ld_gu, const float* sm
  * Gate_up weights in the order w8a8_moe_gate_up_silu reads: w int8
  * [experts, 2 * inter, ldw] (rows [0, inter) gate, [inter, 2 * inter) up, as
  * w8a8_moe_gemm takes them) -> w_out int8 [experts, 2 * inter, k] whose rows
- * come in blocks of 16: 8 gate rows, then the 8 up rows of the same outputs
- * (out row r = gate row (r / 16) * 8 + r % 16 for r % 16 < 8, else up row
- * (r / 16) * 8 + r % 16 - 8); scale_w [experts, 2 * inter] (optional) is
+ * come in blocks of 32: 16 gate rows, then the 16 up rows of the same outputs
+ * (out row r = gate row (r / 32) * 16 + r % 32 for r % 32 < 16, else up row
+ * (r / 32) * 16 + r % 32 - 16); scale_w [experts, 2 * inter] (optional) is
  * permuted alike into scale_w_out.  A one-time weight preparation, like
- * w8a8_pack_weights.  inter % 8 == 0; ldw = 0 means k.
+ * w8a8_pack_weights.  inter % 16 == 0; ldw = 0 means k.
  */
 int w8a8_moe_interleave_gate_up(const int8_t* w, const float* scale_w, uint32_t experts,
                                 uint32_t inter, uint32_t k, uint32_t ldw, int8_t* w_out,
@@ -458,7 +458,7 @@ size_t w8a8_moe_gate_up_silu_workspace_size(uint32_t rows, uint32_t inter);
  * w8a8_gemm); smooth_scale [experts, inter] or NULL; q int8 [rows, ldq]
  * (ldq = 0 means inter), row_scale [rows]: only rows inside some expert's
  * [start, start + count) are written.  workspace: 256-byte aligned,
- * w8a8_moe_gate_up_silu_workspace_size bytes.  inter % 8 == 0, inter <=
+ * w8a8_moe_gate_up_silu_workspace_size bytes.  inter % 16 == 0, inter <=
  * 32768, k % 16 == 0.
  */
 int w8a8_moe_gate_up_silu(uint32_t experts, uint32_t rows, uint32_t inter, uint32_t k,

@@ -528,7 +528,7 @@ def moe_silu_mul_quant(gate_up, expert_start, expert_count, smooth_scale=None,
 
 def moe_interleave_gate_up(w_gate_up, scale_w=None):
     """gate_up weights int8 [E, 2*inter, K] (+ scales [E, 2*inter]) -> the row
-    order moe_gate_up_silu reads (blocks of 8 gate rows then their 8 up rows)."""
+    order moe_gate_up_silu reads (blocks of 16 gate rows then their 16 up rows)."""
     torch = _torch()
     _require_cuda(w_gate_up, scale_w)
     e, two_i, k = w_gate_up.shape

@@ -669,8 +669,8 @@ int w8a8_moe_interleave_gate_up(const int8_t* w, const float* scale_w, uint32_t 
         return fail(W8A8_ERROR_INVALID_VALUE, "%s: null pointer argument", fn);
     if(experts == 0 || inter == 0 || k == 0)
         return fail(W8A8_ERROR_INVALID_VALUE, "%s: experts, inter, k must be > 0", fn);
-    if(inter % 8 != 0)
-        return fail(W8A8_ERROR_INVALID_VALUE, "%s: inter=%u must be a multiple of 8", fn, inter);
+    if(inter % 16 != 0)
+        return fail(W8A8_ERROR_INVALID_VALUE, "%s: inter=%u must be a multiple of 16", fn, inter);
     if(ldw == 0) ldw = k;
     if(ldw < k) return fail(W8A8_ERROR_INVALID_VALUE, "%s: ldw=%u smaller than k=%u", fn, ldw, k);
     return hip_status(w8a8::launch_moe_interleave_gate_up(w, scale_w, experts, inter, k, ldw,
@@ -696,9 +696,9 @@ int w8a8_moe_gate_up_silu(uint32_t experts, uint32_t rows, uint32_t inter, uint3
         return fail(W8A8_ERROR_INVALID_VALUE, "%s: null pointer argument", fn);
     if(experts == 0 || inter == 0 || k == 0)
         return fail(W8A8_ERROR_INVALID_VALUE, "%s: experts, inter, k must be > 0", fn);
-    if(inter % 8 != 0 || inter > 32768)
-        return fail(W8A8_ERROR_NOT_SUPPORTED, "%s: needs inter %% 8 == 0 and inter <= 32768 (inter=%u)",
-                    fn, inter);
+    if(inter % 16 != 0 || inter > 32768)
+        return fail(W8A8_ERROR_NOT_SUPPORTED,
+                    "%s: needs inter %% 16 == 0 and inter <= 32768 (inter=%u)", fn, inter);
     if(lda == 0) lda = k;
     if(ldq == 0) ldq = inter;
     if(lda < k || ldq < inter)

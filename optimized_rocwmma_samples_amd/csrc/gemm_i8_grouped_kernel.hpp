@@ -207,6 +207,10 @@ struct SiluOut {
 
 // One tile's epilogue for waves wave_base, wave_base + 1, ... of the tile;
 // h and pmax point at the expert's first row, s2 at its vector (or null).
+// The weights come interleaved in blocks of 32 rows, 16 gate rows then the
+// 16 up rows of the same outputs, so in the 16 x 16 MFMA layout (Acc<C>)
+// quad 2 p of a lane holds the gates and quad 2 p + 1 the ups of its outputs
+// 16 p + 4 (lane / 16) + 0..3 of the wave's kWaveN / 2.
 template <class C>
 __device__ __forceinline__ void epilogue_silu(const KArgs& p, uint32_t m0, uint32_t n0,
                                               int8_t* lds, int wave_base, const Acc<C>& acc,
@@ -214,21 +218,22 @@ __device__ __forceinline__ void epilogue_silu(const KArgs& p, uint32_t m0, uint3
                                               const float* s2, uint32_t ldh, uint32_t ldp,
                                               uint32_t inter)
 {
-    // gate and up of one output sit in quads 2 gp and 2 gp + 1 of the same
-    // lane only in the 32 x 32 MFMA layout (8-row interleave)
-    static_assert(C::kMfma == 32, "SiLU epilogue: 32 x 32 MFMA layout");
+    static_assert(C::kMfma == 16, "SiLU epilogue: 16 x 16 MFMA layout");
+    using A                  = Acc<C>;
+    constexpr int kPairs     = A::kQuadsN / 2;
     constexpr int kOutCols   = C::kWaveN / 2;
     constexpr int kRowBytes  = kOutCols * 2;
     constexpr int kRowChunks = kRowBytes / 16;
     constexpr int kRowsPerSt = kWave / kRowChunks;
     static_assert(kRowChunks == 4 || kRowChunks == 8 || kRowChunks == 16, "row of 4-16 chunks");
+    static_assert(C::kWaveN % 32 == 0, "whole 32-row interleave blocks per wave");
     using S = StageSwz<kRowChunks>;
     const int      slot = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int      wave = wave_base + slot;
     const int      lane = threadIdx.x % kWave;
     const int      wm   = wave / C::kWavesN;
     const int      wn   = wave % C::kWavesN;
-    const int      half = lane >> 5;
+    const int      lgrp = lane >> 4; // 4-column group of the lane's quads
     const uint32_t oc0  = n0 / 2 + wn * kOutCols;
     // waves wholly past the last interleaved column (a partial last N tile)
     // have no pmax entry and store nothing
@@ -236,57 +241,59 @@ __device__ __forceinline__ void epilogue_silu(const KArgs& p, uint32_t m0, uint3
     float* const   pcol = pmax + (size_t)(n0 / C::kWaveN + wn) * ldp;
 
     // s2 of this lane's outputs (1 without s2; 0 past inter, where g = u = 0)
-    float s2v[C::kTilesN][2][4];
+    float s2v[kPairs][4];
 #pragma unroll
-    for(int j = 0; j < C::kTilesN; ++j)
+    for(int q = 0; q < kPairs; ++q) {
+        const uint32_t o = oc0 + q * 16 + lgrp * 4;
+        if(s2 != nullptr && o + 4 <= inter) {
+            const float4 v = *reinterpret_cast<const float4*>(s2 + o);
+            s2v[q][0] = v.x, s2v[q][1] = v.y, s2v[q][2] = v.z, s2v[q][3] = v.w;
+        } else {
 #pragma unroll
-        for(int gp = 0; gp < 2; ++gp) {
-            const uint32_t o = oc0 + j * 16 + gp * 8 + half * 4;
-            if(s2 != nullptr && o + 4 <= inter) {
-                const float4 v = *reinterpret_cast<const float4*>(s2 + o);
-                s2v[j][gp][0] = v.x, s2v[j][gp][1] = v.y, s2v[j][gp][2] = v.z, s2v[j][gp][3] = v.w;
-            } else {
-#pragma unroll
-                for(int e = 0; e < 4; ++e)
-                    s2v[j][gp][e] = o + e < inter ? (s2 != nullptr ? s2[o + e] : 1.f) : 0.f;
-            }
+            for(int e = 0; e < 4; ++e)
+                s2v[q][e] = o + e < inter ? (s2 != nullptr ? s2[o + e] : 1.f) : 0.f;
         }
+    }
 
     block_barrier(); // every wave's fragment reads and LDS loads are done: the ring is free
     int8_t* stage = lds + slot * (C::kWaveM * kRowBytes);
 #pragma unroll
-    for(int i = 0; i < C::kTilesM; ++i) {
-        const int row = i * 32 + (lane & 31);
+    for(int i = 0; i < A::kQuadsM; ++i) {
+        const int row = A::row(i, lane);
         float     mx  = 0.f;
 #pragma unroll
-        for(int j = 0; j < C::kTilesN; ++j) {
+        for(int q = 0; q < kPairs; ++q) {
+            const v4i    gq     = acc.quad(i, 2 * q);
+            const v4i    uq     = acc.quad(i, 2 * q + 1);
+            const float4 sg     = sc.sb[2 * q];
+            const float4 su     = sc.sb[2 * q + 1];
+            const int    gv[4]  = {gq.x, gq.y, gq.z, gq.w};
+            const int    uv[4]  = {uq.x, uq.y, uq.z, uq.w};
+            const float  sgv[4] = {sg.x, sg.y, sg.z, sg.w};
+            const float  suv[4] = {su.x, su.y, su.z, su.w};
+            uint32_t     hb[4];
 #pragma unroll
-            for(int gp = 0; gp < 2; ++gp) {
-                const float4 sg     = sc.sb[j * 4 + 2 * gp];
-                const float4 su     = sc.sb[j * 4 + 2 * gp + 1];
-                const float  sgv[4] = {sg.x, sg.y, sg.z, sg.w};
-                const float  suv[4] = {su.x, su.y, su.z, su.w};
-                uint32_t     hb[4];
-#pragma unroll
-                for(int e = 0; e < 4; ++e) {
-                    const float g = half_bits_to_float(float_to_half_bits_2step(
-                        ((float)acc.r[i][j][(2 * gp) * 4 + e] * sc.sa[i]) * sgv[e]));
-                    const float u = half_bits_to_float(float_to_half_bits_2step(
-                        ((float)acc.r[i][j][(2 * gp + 1) * 4 + e] * sc.sa[i]) * suv[e]));
-                    hb[e] = float_to_half_bits_2step(silu_mul_epi(g, u));
-                    mx    = fmaxf(mx, fabsf(half_bits_to_float(hb[e]) * s2v[j][gp][e]));
-                }
-                const int phys = S::chunk(j * 2 + gp, row);
-                v2i       pk;
-                pk.x = (int)(hb[0] | (hb[1] << 16));
-                pk.y = (int)(hb[2] | (hb[3] << 16));
-                *reinterpret_cast<v2i*>(stage + row * kRowBytes + phys * 16
-                                        + S::half(half, row) * 8) = pk;
+            for(int e = 0; e < 4; ++e) {
+                const float g = half_bits_to_float(
+                    float_to_half_bits_2step(((float)gv[e] * sc.sa[i]) * sgv[e]));
+                const float u = half_bits_to_float(
+                    float_to_half_bits_2step(((float)uv[e] * sc.sa[i]) * suv[e]));
+                hb[e] = float_to_half_bits_2step(silu_mul_epi(g, u));
+                mx    = fmaxf(mx, fabsf(half_bits_to_float(hb[e]) * s2v[q][e]));
             }
+            const int oc   = q * 16 + lgrp * 4; // output column within the wave
+            const int phys = S::chunk(oc >> 3, row);
+            v2i       pk;
+            pk.x = (int)(hb[0] | (hb[1] << 16));
+            pk.y = (int)(hb[2] | (hb[3] << 16));
+            *reinterpret_cast<v2i*>(stage + row * kRowBytes + phys * 16
+                                    + S::half((oc >> 2) & 1, row) * 8) = pk;
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave)); // the row's other half
+        // the row's other three column groups
+        mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
         const uint32_t m = m0 + wm * C::kWaveM + row;
-        if(half == 0 && live && m < p.m) pcol[m] = mx;
+        if(lgrp == 0 && live && m < p.m) pcol[m] = mx;
     }
     // a wave reads back only what it wrote itself (LDS returns a wave's
     // accesses in order)

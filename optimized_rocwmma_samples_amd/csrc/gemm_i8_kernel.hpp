@@ -199,18 +199,18 @@ __device__ __forceinline__ void interleave_mfma_vmem_ds()
     interleave_step<0, kSteps, NVMEM, NDS, ID>();
 }
 
-// One 16 x 16 x 64 k-group (FragPipe): per A row, its NB MFMAs, then the
-// read of that row's next A fragment (and of one next B fragment in the
-// first NB rows) and its share of NVMEM global -> LDS loads.
-template <int I, int ROWS, int NB, int NVMEM, int ID>
+// One 16 x 16 x 64 k-group (FragPipe): per outer fragment, its INNER MFMAs,
+// then the read of its next fragment (and of one next inner fragment in the
+// first INNER of them) and its share of NVMEM global -> LDS loads.
+template <int I, int OUTER, int INNER, int NVMEM, int ID>
 __device__ __forceinline__ void interleave_rows16()
 {
-    if constexpr(I < ROWS) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, NB, ID);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, I < NB ? 2 : 1, ID);
-        constexpr int nv = (I + 1) * NVMEM / ROWS - I * NVMEM / ROWS;
+    if constexpr(I < OUTER) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, INNER, ID);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, I < INNER ? 2 : 1, ID);
+        constexpr int nv = (I + 1) * NVMEM / OUTER - I * NVMEM / OUTER;
         if constexpr(nv > 0) __builtin_amdgcn_sched_group_barrier(kSchedVmemRd, nv, ID);
-        interleave_rows16<I + 1, ROWS, NB, NVMEM, ID>();
+        interleave_rows16<I + 1, OUTER, INNER, NVMEM, ID>();
     }
 }
 
@@ -329,25 +329,64 @@ struct FragReader {
 // the next k-group's fragments interleaved.  Slot s = k-group parity (even
 // kSubK, so k-group g of every k-tile uses slot g & 1).
 //   MFMA 32: two full fragment sets; a group reads the next into the other.
-//   MFMA 16: one A set: the next group's A fragment t is read into fragment
-//     t's registers right after row t's MFMAs have issued, (kTilesM - 1)
-//     kTilesN MFMAs before its first use; B ping-pongs, its next fragments
-//     read during the first rows.  Fragments take 64 VGPRs instead of 96,
-//     which keeps the 128 x 64 wave tile's loop within 256 VGPRs.
+//   MFMA 16: the operand with more fragments per wave tile is the outer one
+//     (A unless the wave tile is wider than tall): one register set, the next
+//     group's outer fragment t read into fragment t's registers right after
+//     its MFMAs have issued, (outer - 1) x inner MFMAs before its first use;
+//     the inner fragments ping-pong, next inner fragment t read after outer
+//     fragment t (the earliest slots, so they have the most time to land
+//     before the next group starts).  A 128 x 64 wave tile holds 64 fragment
+//     VGPRs instead of 96, which keeps its loop within 256 VGPRs.
 // NVMEM: global -> LDS loads issued just before, spread over the group.
 template <class C>
 struct FragPipe {
-    static constexpr bool kBig = C::kMfma == 32;
-    static constexpr int  kMfmaN = C::kTilesM * C::kTilesN;
-    static constexpr int  kDs    = C::kTilesM + C::kTilesN;
-    static_assert(kBig || C::kTilesN <= C::kTilesM, "B reads spread over the first rows");
+    static constexpr bool kBig       = C::kMfma == 32;
+    static constexpr bool kRowsOuter = C::kTilesM >= C::kTilesN;
+    static constexpr int  kOuter     = kRowsOuter ? C::kTilesM : C::kTilesN;
+    static constexpr int  kInner     = kRowsOuter ? C::kTilesN : C::kTilesM;
+    static constexpr int  kMfmaN     = C::kTilesM * C::kTilesN;
+    static constexpr int  kDs        = C::kTilesM + C::kTilesN;
     FragReader<C> fr;
-    v4i           fa[kBig ? 2 : 1][C::kTilesM];
-    v4i           fb[2][C::kTilesN];
+    // MFMA 32 registers
+    v4i fa[kBig ? 2 : 1][kBig ? C::kTilesM : 1];
+    v4i fb[kBig ? 2 : 1][kBig ? C::kTilesN : 1];
+    // MFMA 16 registers
+    v4i fo[kBig ? 1 : kOuter];
+    v4i fi[kBig ? 1 : 2][kBig ? 1 : kInner];
 
     __device__ __forceinline__ FragPipe(int wm, int wn, int lane) : fr(wm, wn, lane) {}
 
-    __device__ __forceinline__ void first(const int8_t* sbase) { fr.load(sbase, 0, fa[0], fb[0]); }
+    __device__ __forceinline__ v4i outer(const int8_t* sbase, int g, int t) const
+    {
+        return kRowsOuter ? fr.a(sbase, g, t) : fr.b(sbase, g, t);
+    }
+    __device__ __forceinline__ v4i inner(const int8_t* sbase, int g, int t) const
+    {
+        return kRowsOuter ? fr.b(sbase, g, t) : fr.a(sbase, g, t);
+    }
+    // the 16 x 16 x 64 MFMAs of outer fragment o with inner set s
+    __device__ __forceinline__ void mfma_outer(Acc<C>& acc, int s, int o)
+    {
+#pragma unroll
+        for(int x = 0; x < kInner; ++x) {
+            const int i = kRowsOuter ? o : x, j = kRowsOuter ? x : o;
+            const v4i& a = kRowsOuter ? fo[o] : fi[s][x];
+            const v4i& b = kRowsOuter ? fi[s][x] : fo[o];
+            acc.r[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b, a, acc.r[i][j], 0, 0, 0);
+        }
+    }
+
+    __device__ __forceinline__ void first(const int8_t* sbase)
+    {
+        if constexpr(kBig) {
+            fr.load(sbase, 0, fa[0], fb[0]);
+        } else {
+#pragma unroll
+            for(int t = 0; t < kOuter; ++t) fo[t] = outer(sbase, 0, t);
+#pragma unroll
+            for(int t = 0; t < kInner; ++t) fi[0][t] = inner(sbase, 0, t);
+        }
+    }
 
     template <int NVMEM>
     __device__ __forceinline__ void step(Acc<C>& acc, int s, const int8_t* sbase_n, int g_n)
@@ -361,15 +400,12 @@ struct FragPipe {
                 interleave_mfma_ds<kMfmaN, kDs, 0>();
         } else {
 #pragma unroll
-            for(int i = 0; i < C::kTilesM; ++i) {
-#pragma unroll
-                for(int j = 0; j < C::kTilesN; ++j)
-                    acc.r[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb[s][j], fa[0][i],
-                                                                         acc.r[i][j], 0, 0, 0);
-                fa[0][i] = fr.a(sbase_n, g_n, i);
-                if(i < C::kTilesN) fb[s ^ 1][i] = fr.b(sbase_n, g_n, i);
+            for(int o = 0; o < kOuter; ++o) {
+                mfma_outer(acc, s, o);
+                fo[o] = outer(sbase_n, g_n, o);
+                if(o < kInner) fi[s ^ 1][o] = inner(sbase_n, g_n, o);
             }
-            interleave_rows16<0, C::kTilesM, C::kTilesN, NVMEM, (NVMEM > 0 ? 1 : 0)>();
+            interleave_rows16<0, kOuter, kInner, NVMEM, (NVMEM > 0 ? 1 : 0)>();
         }
     }
     // a k-group with no fragments to read next: MFMAs only, with the NVMEM
@@ -377,7 +413,12 @@ struct FragPipe {
     template <int NVMEM = 0>
     __device__ __forceinline__ void last(Acc<C>& acc, int s)
     {
-        acc.mfma(fa[kBig ? s : 0], fb[s]);
+        if constexpr(kBig) {
+            acc.mfma(fa[s], fb[s]);
+        } else {
+#pragma unroll
+            for(int o = 0; o < kOuter; ++o) mfma_outer(acc, s, o);
+        }
         if constexpr(NVMEM > 0) interleave_mfma_vmem_ds<kMfmaN, NVMEM, 0, 1>();
     }
 };

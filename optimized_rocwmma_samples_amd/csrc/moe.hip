@@ -637,8 +637,9 @@ hipError_t launch_requant(const SiluRequant& p, hipStream_t stream)
 }
 
 // Gate_up weights interleaved for the SiLU epilogue: output row r of expert
-// e is input row (r / 16) * 8 + r % 16 for r % 16 < 8 (gate) and
-// inter + (r / 16) * 8 + r % 16 - 8 otherwise (up); one block per output row.
+// e is input row (r / 32) * 16 + r % 32 for r % 32 < 16 (gate) and
+// inter + (r / 32) * 16 + r % 32 - 16 otherwise (up); one block per output
+// row (inter % 16 == 0, host-checked).
 __global__ void __launch_bounds__(256)
     interleave_gate_up_kernel(const int8_t* __restrict__ w, const float* __restrict__ sw,
                               uint32_t inter, uint32_t k, uint32_t ldw, int8_t* __restrict__ wo,
@@ -646,8 +647,8 @@ __global__ void __launch_bounds__(256)
 {
     const uint32_t rows = 2 * inter;
     const uint32_t e = blockIdx.x / rows, r = blockIdx.x % rows;
-    const uint32_t b = r / 16, x = r % 16;
-    const uint32_t src = x < 8 ? b * 8 + x : inter + b * 8 + (x - 8);
+    const uint32_t b = r / 32, x = r % 32;
+    const uint32_t src = x < 16 ? b * 16 + x : inter + b * 16 + (x - 16);
     const int8_t*  in  = w + ((size_t)e * rows + src) * ldw;
     int8_t*        out = wo + ((size_t)e * rows + r) * k;
     if(vec) {
@@ -952,10 +953,10 @@ hipError_t launch_moe_gemm(const MoeGemmArgs& a, hipStream_t stream)
 
 // The SiLU epilogue's tiles: wave tiles 128 columns wide (64 outputs, one
 // 128-byte line of h per row and wave), otherwise as GemmGrouped /
-// GemmGroupedMid, on the 32 x 32 x 32 MFMA: the gate/up interleave in blocks
-// of 8 rows puts a gate and its up value in one lane only in that layout.
-using GemmSilu    = gemm::Cfg<256, 256, 128, 2, 4, 2, 4>;
-using GemmSiluMid = gemm::Cfg<128, 256, 128, 3, 4, 2, 4>;
+// GemmGroupedMid (16 x 16 x 64 MFMA, whose lane layout the 32-row gate/up
+// interleave matches).
+using GemmSilu    = gemm::Cfg<256, 256, 128, 2, 4, 2, 4, 16>;
+using GemmSiluMid = gemm::Cfg<128, 256, 128, 3, 4, 2, 4, 16>;
 static_assert(GemmSilu::kWaveN == GemmSiluMid::kWaveN, "one pmax layout for both tiles");
 static_assert(gemm::Partial<GemmSilu>::kBytes == gemm::Partial<GemmGrouped>::kBytes
                   && gemm::Partial<GemmSiluMid>::kBytes == gemm::Partial<GemmGroupedMid>::kBytes,

@@ -307,6 +307,21 @@ def test_moe_silu_and_combine_validation(w8a8):
     assert _status("w8a8_moe_combine", *bad)[0] == W.ERROR_INVALID_VALUE
 
 
+def test_moe_gate_up_silu_validation(w8a8):
+    # the 32-row gate/up interleave needs whole 16-output blocks
+    rc, msg = _status("w8a8_moe_interleave_gate_up", FAKE, None, 2, 40, 64, 0, FAKE, None, None)
+    assert rc == W.ERROR_INVALID_VALUE and "multiple of 16" in msg
+    ok = [2, 256, 48, 64, FAKE, 0, FAKE, FAKE, FAKE, 1.0, 1.0, None, FAKE, FAKE, FAKE, 0, FAKE,
+          127.0, FAKE, 1 << 20, None]
+    bad = list(ok); bad[2] = 40
+    rc, msg = _status("w8a8_moe_gate_up_silu", *bad)
+    assert rc == W.ERROR_NOT_SUPPORTED and "inter % 16" in msg
+    bad = list(ok); bad[2] = 32784
+    assert _status("w8a8_moe_gate_up_silu", *bad)[0] == W.ERROR_NOT_SUPPORTED
+    bad = list(ok); bad[17] = 0.0
+    assert _status("w8a8_moe_gate_up_silu", *bad)[0] == W.ERROR_INVALID_VALUE
+
+
 def test_python_layer_raises_w8a8error(w8a8):
     with pytest.raises(W.W8A8Error) as ei:
         _lib.call("w8a8_smoothquant", None, None, None, None, 1, 1, 127.0, 0, 0, None)

@@ -455,13 +455,13 @@ def test_config5_full_size_sampled(w8a8, gpu):
 
 
 def _interleave_perm(inter):
-    """Row order of moe_interleave_gate_up: blocks of 8 gate rows, then their 8 up rows."""
+    """Row order of moe_interleave_gate_up: blocks of 16 gate rows, then their 16 up rows."""
     r = np.arange(2 * inter)
-    b, x = r // 16, r % 16
-    return np.where(x < 8, b * 8 + x, inter + b * 8 + x - 8)
+    b, x = r // 32, r % 32
+    return np.where(x < 16, b * 16 + x, inter + b * 16 + x - 16)
 
 
-@pytest.mark.parametrize("e,inter,k", [(3, 40, 48), (2, 64, 50)])
+@pytest.mark.parametrize("e,inter,k", [(3, 48, 48), (2, 64, 50)])
 def test_moe_interleave_gate_up_exact(w8a8, gpu, e, inter, k):
     w = G.int8(inter + k, G.TID_B, (e, 2 * inter, k))
     sw = G.uniform(inter + k, G.TID_SB, (e, 2 * inter), 1e-3, 1e-2)
@@ -469,8 +469,8 @@ def test_moe_interleave_gate_up_exact(w8a8, gpu, e, inter, k):
     perm = _interleave_perm(inter)
     assert np.array_equal(host(wo), w[:, perm, :])
     assert np.array_equal(host(so), sw[:, perm])
-    # the permutation itself: each output row block holds gate j..j+7 then up j..j+7
-    assert list(perm[:16]) == list(range(8)) + list(range(inter, inter + 8))
+    # the permutation itself: each output row block holds gate j..j+15 then up j..j+15
+    assert list(perm[:32]) == list(range(16)) + list(range(inter, inter + 16))
 
 
 def _silu_h16(gu):
@@ -487,7 +487,7 @@ def _silu_h16(gu):
 # case has K = 4096, so a partial last round of tiles is split along K and the
 # fixup kernel runs the SiLU epilogue; the last has 128-row tiles
 SILU_CASES = [(256, 2, 8, 512, 384, 32, True), (512, 2, 4, 4096, 512, 32, True),
-              (128, 1, 5, 256, 136, 1, False), (2000, 6, 64, 256, 128, 16, True)]
+              (128, 1, 5, 256, 144, 1, False), (2000, 6, 64, 256, 128, 16, True)]
 
 
 @pytest.mark.parametrize("t,k,e,h,inter,unit,with_s2", SILU_CASES)
