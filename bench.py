@@ -326,7 +326,12 @@ def bench_cfg3_smaller_m(torch, w8a8, dev, base, steps=10, sets=3):
     the dense GEMM's K-split workspace preallocated (the launches whose tiles
     fill at most half of the CUs use it).  Inputs are the first M rows of the
     headline's (datagen) activations; `sets` copies of its weights are used in
-    turn so each step streams its weights from HBM (3 x 216 MB)."""
+    turn so each step streams its weights from HBM (3 x 216 MB).  A step is 8
+    launches of 3-70 us, so launching them one by one from Python costs about
+    as much host time as the GPU spends: the steps are timed replayed from a
+    captured HIP graph (`TOPS`, GPU throughput; one replay's outputs are
+    checked bitwise against the eager step) and launched eagerly
+    (`eager_TOPS`)."""
     def sub(p, m, copy):
         return dict(x=p["x"][:m], s=p["s"], w=p["w"].clone() if copy else p["w"], sb=p["sb"],
                     q=torch.empty((m, p["k"]), dtype=torch.int8, device=dev),
@@ -359,7 +364,7 @@ def bench_cfg3_smaller_m(torch, w8a8, dev, base, steps=10, sets=3):
             step(i)
         t1.record()
         torch.cuda.synchronize()
-        ms = t0.elapsed_time(t1) / steps
+        eager_ms = t0.elapsed_time(t1) / steps
         evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(LLAMA3_8B) + 1)]
                for _ in range(steps)]
         for i in range(steps):
@@ -367,8 +372,20 @@ def bench_cfg3_smaller_m(torch, w8a8, dev, base, steps=10, sets=3):
         torch.cuda.synchronize()
         per = {name: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / steps * 1e3
                for j, (name, _, _) in enumerate(LLAMA3_8B)}
+        # the same steps replayed from a graph, then the last one's outputs
+        # against an eager run of that step
+        ms = graph_us(torch, [(lambda i=i: step(i)) for i in range(steps)]) / 1e3
+        last = projs[(steps - 1) % sets]
+        replayed = [p["c"].clone() for p in last]
+        step(steps - 1)
+        torch.cuda.synchronize()
+        same = all(torch.equal(a.view(torch.int16), p["c"].view(torch.int16))
+                   for a, p in zip(replayed, last))
         out.append({"M": m, "ms_per_step": ms, "TOPS": ops / (ms * 1e-3) / 1e12,
                     "frac_mfma": ops / (ms * 1e-3) / PEAK_INT8_OPS,
+                    "graph_matches_eager": same,
+                    "eager_ms_per_step": eager_ms,
+                    "eager_TOPS": ops / (eager_ms * 1e-3) / 1e12,
                     "fused_us_per_projection": per, "workspace_bytes": ws_bytes})
         del projs, ws
     return out
@@ -699,7 +716,7 @@ def main(argv=None) -> int:
                                    "+ WRITE_SIZE x1.0, calibrated on a 2^30-byte copy; "
                                    "FETCH_SIZE includes MALL hits)") if traffic else None,
                 "kernel": " + ".join(
-                    f"{'gemm_i8_persist_kernel<Cfg<256,256,128,2,2,4,4>>' if kd == 'persist' else 'gemm_i8_tile_kernel<Cfg<256,256,128,2,2,4,4>, F16>'} ({', '.join(nm for (nm, _, _), k2 in zip(LLAMA3_8B, kinds) if k2 == kd)})"
+                    f"{'gemm_i8_persist_kernel<Cfg<256,256,128,2,2,4,4,16>>' if kd == 'persist' else 'gemm_i8_tile_kernel<Cfg<256,256,128,2,2,4,4,16>, F16>'} ({', '.join(nm for (nm, _, _), k2 in zip(LLAMA3_8B, kinds) if k2 == kd)})"
                     for kd in dict.fromkeys(kinds)),
                 "traffic_note": "per-projection entries of the persistent kernel are its average "
                                 "over the projections it runs (one block per CU each)",
