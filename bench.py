@@ -556,19 +556,23 @@ def measured_peaks(torch, dev, cus):
 
     out = {}
     blocks, iters = cus, 4096
-    sink = torch.empty(blocks * 4, dtype=torch.int32, device=dev)
+    sink = torch.empty(blocks * 8, dtype=torch.int32, device=dev)
     ops = lib.w8a8_peak_mfma_ops(blocks, iters)
-    for name, rnd in (("random", 1), ("zeros", 0)):
+    # mode bit 0: random operands, bit 1: the 16x16x64 form (the GEMM's)
+    for key, mode in (("mfma_i8_random_TOPS", 1), ("mfma_i8_zeros_TOPS", 0),
+                      ("mfma16_i8_random_TOPS", 3), ("mfma16_i8_zeros_TOPS", 2)):
         t_end = time.perf_counter() + 0.2  # let the clocks settle under this load
         while time.perf_counter() < t_end:
-            check(lib.w8a8_peak_mfma(blocks, iters, rnd, sink.data_ptr(),
+            check(lib.w8a8_peak_mfma(blocks, iters, mode, sink.data_ptr(),
                                      torch.cuda.current_stream(dev).cuda_stream), "peak_mfma")
             torch.cuda.synchronize()
-        sec = timed(lambda s, r=rnd: check(lib.w8a8_peak_mfma(blocks, iters, r, sink.data_ptr(), s),
-                                            "peak_mfma"), 10)
-        out[f"mfma_i8_{name}_TOPS"] = ops / sec / 1e12
-    out["mfma_note"] = (f"v_mfma_i32_32x32x32_i8 only, {blocks} blocks x 4 waves x 8 independent "
-                        f"accumulators, {iters} rounds; operands held in registers")
+        sec = timed(lambda s, md=mode: check(lib.w8a8_peak_mfma(blocks, iters, md, sink.data_ptr(),
+                                                                s), "peak_mfma"), 10)
+        out[key] = ops / sec / 1e12
+    out["mfma_note"] = (f"MFMA-only loops of the same ops, {blocks} blocks: 4 waves x 8 "
+                        f"accumulators x {iters} rounds of v_mfma_i32_32x32x32_i8, or 8 waves "
+                        f"(the GEMM's two per SIMD) x 16 accumulators x {iters // 2} rounds of "
+                        "v_mfma_i32_16x16x64_i8; operands held in registers")
     nbytes = 1 << 30
     src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(3)
     dst = torch.empty_like(src)
@@ -732,10 +736,13 @@ def main(argv=None) -> int:
     log(json.dumps(peaks))
     for pp in per_proj:
         pp["quant_frac_stream21_measured"] = pp["quant_GBps"] / peaks["stream21_GBps"]
-    roofline["peak_measured"] = peaks["mfma_i8_random_TOPS"]
-    roofline["frac_measured"] = gemm_tops / peaks["mfma_i8_random_TOPS"]
-    roofline["peak_measured_note"] = ("int8 MFMA-only loop on random operands, same run "
-                                      "(measured_peaks)")
+    roofline["peak_measured"] = peaks["mfma16_i8_random_TOPS"]
+    roofline["frac_measured"] = gemm_tops / peaks["mfma16_i8_random_TOPS"]
+    roofline["peak_measured_note"] = ("MFMA-only loop of the GEMM's instruction "
+                                      "(v_mfma_i32_16x16x64_i8) on random operands, same run "
+                                      "(measured_peaks); the 32x32x32 form's loop: "
+                                      "frac_measured_mfma32")
+    roofline["frac_measured_mfma32"] = gemm_tops / peaks["mfma_i8_random_TOPS"]
 
     extras = {}
     if not args.no_extras:

@@ -1,8 +1,9 @@
 // peaks.hip -- measured ceilings of one MI355X, built as libw8a8_peaks.so and
 // timed by bench.py beside the path's kernels (not part of the W8A8 C ABI):
-//   * an int8 MFMA-only loop: v_mfma_i32_32x32x32_i8 back to back on operands
-//     held in registers, nothing else in the loop -- the matrix-core rate the
-//     chip sustains at the clock it holds under that load;
+//   * int8 MFMA-only loops: v_mfma_i32_32x32x32_i8 or v_mfma_i32_16x16x64_i8
+//     back to back on operands held in registers, nothing else in the loop --
+//     the matrix-core rate the chip sustains at the clock it holds under that
+//     load;
 //   * a streaming copy: 16 bytes per lane per access, several accesses in
 //     flight per lane -- the HBM rate a plain read + write stream reaches;
 //   * an empty kernel -- the launch floor of back-to-back launches (timed by
@@ -58,6 +59,42 @@ __global__ void __launch_bounds__(256) peak_mfma_i8_kernel(int iters, int random
     if(lane == 0) sink[blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64] = s;
 }
 
+// The same loop on v_mfma_i32_16x16x64_i8, in blocks of 8 waves (two per
+// SIMD, as the GEMM runs): one wave per SIMD cannot issue this form back to
+// back (about 2.9 of 4.6 POP/s on zeros, 16 or 32 accumulators alike).  Each
+// wave keeps 2 kChains accumulators of 16 x 16, so a round of a block is
+// twice the 32 x 32 loop's ops; the host halves the rounds.
+constexpr int kThreads16 = 512;
+__global__ void __launch_bounds__(kThreads16) peak_mfma16_i8_kernel(int iters, int random,
+                                                                    int* sink)
+{
+    const uint32_t lane = threadIdx.x % 64;
+    uint32_t       h    = (blockIdx.x * kThreads16 + threadIdx.x) * 0x9E3779B9u + 0x7F4A7C15u;
+    v4i            a, b;
+    for(int i = 0; i < 4; ++i) {
+        h ^= h >> 15;
+        h *= 0x2C1B3C6Du;
+        h ^= h >> 12;
+        a[i] = random ? (int)h : 0;
+        h *= 0x297A2D39u;
+        h ^= h >> 15;
+        b[i] = random ? (int)(h ^ lane) : 0;
+    }
+    v4i acc[2 * kChains];
+#pragma unroll
+    for(int c = 0; c < 2 * kChains; ++c) acc[c] = v4i{0, 0, 0, 0};
+    for(int it = 0; it < iters; ++it) {
+#pragma unroll
+        for(int c = 0; c < 2 * kChains; ++c)
+            acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[c], 0, 0, 0);
+        asm volatile("" : "+v"(a), "+v"(b));
+    }
+    int s = 0;
+#pragma unroll
+    for(int c = 0; c < 2 * kChains; ++c) s += acc[c].x + acc[c].y + acc[c].z + acc[c].w;
+    if(lane == 0) sink[blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64] = s;
+}
+
 // Grid-stride stream over `n16` 16-byte source chunks, kUnroll loads in
 // flight per lane (the best of a sweep over 2-16 loads, 256-1024 threads and
 // 1-16 blocks per CU on MI355X).  MODE 0 reads only; MODE 1 copies each chunk;
@@ -98,20 +135,27 @@ __global__ void peak_empty_kernel() {}
 
 extern "C" {
 
-// ops one peak_mfma launch performs: blocks x 4 waves x iters x kChains x
-// (2 * 32 * 32 * 32)
+// ops one peak_mfma launch performs (either form): blocks x 4 waves x iters
+// x kChains x (2 * 32 * 32 * 32)
 double w8a8_peak_mfma_ops(uint32_t blocks, uint32_t iters)
 {
     return (double)blocks * 4.0 * iters * kChains * 2.0 * 32 * 32 * 32;
 }
 
-// One MFMA-only launch of `blocks` blocks of 4 waves (one wave per SIMD at one
-// block per CU; use a multiple of the CU count).  sink: blocks * 4 ints.
-int w8a8_peak_mfma(uint32_t blocks, uint32_t iters, int random, int* sink, hipStream_t stream)
+// One MFMA-only launch of `blocks` blocks (use a multiple of the CU count):
+// 4 waves of the 32 x 32 x 32 form or 8 waves of the 16 x 16 x 64 form, the
+// same w8a8_peak_mfma_ops either way (iters even).  mode bit 0: random (1) or
+// zero (0) operands; bit 1: the 16 x 16 x 64 form.  sink: blocks * 8 ints.
+int w8a8_peak_mfma(uint32_t blocks, uint32_t iters, int mode, int* sink, hipStream_t stream)
 {
-    if(blocks == 0 || iters == 0 || sink == nullptr) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(peak_mfma_i8_kernel, dim3(blocks), dim3(256), 0, stream, (int)iters, random,
-                       sink);
+    if(blocks == 0 || iters == 0 || iters % 2 || sink == nullptr || mode < 0 || mode > 3)
+        return (int)hipErrorInvalidValue;
+    if(mode & 2)
+        hipLaunchKernelGGL(peak_mfma16_i8_kernel, dim3(blocks), dim3(kThreads16), 0, stream,
+                           (int)(iters / 2), mode & 1, sink);
+    else
+        hipLaunchKernelGGL(peak_mfma_i8_kernel, dim3(blocks), dim3(256), 0, stream, (int)iters,
+                           mode & 1, sink);
     return (int)hipGetLastError();
 }
 
