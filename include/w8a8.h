@@ -165,8 +165,11 @@ int w8a8_gemm(uint32_t m, uint32_t n, uint32_t k, const int8_t* a, const int8_t*
  * arguments as w8a8_gemm, primary layout only (A [m, lda] row-major, B
  * [n, ldb] K-contiguous, 16-byte aligned, lda, ldb, k multiples of 16, A and
  * B each under 2 GiB).  All tiles' k-tiles are cut into `blocks` contiguous
- * equal ranges (0: one per CU; never more than the problem's k-tiles), one
- * block each, as the reference sample's units_per_cta (:223-226); a tile
+ * equal ranges (never more than the problem's k-tiles), one block each, as
+ * the reference sample's units_per_cta (:223-226); 0: the library picks the
+ * count, at most one per CU, and the tile shape from an estimate of the
+ * longest block's work plus the partials it sums (any count and shape give
+ * the same C); a tile
  * covered by several blocks is summed in int32 by the last of them to finish
  * (one launch, no host synchronisation), so C equals w8a8_gemm's bit for bit.
  * workspace: 16-byte aligned, w8a8_gemm_streamk_workspace_size bytes (tile

@@ -232,7 +232,8 @@ def gemm_streamk(a, b, scale_a=None, scale_b=None, tensor_scale_a: float = 1.0,
                  tensor_scale_b: float = 1.0, out_dtype=None, blocks: int = 0, out=None,
                  workspace=None):
     """w8a8_gemm_streamk: the GEMM of gemm() (a int8 [M, K], b int8 [N, K]) with
-    every tile's k-tiles cut into `blocks` equal ranges (0: one per CU)."""
+    every tile's k-tiles cut into `blocks` equal ranges (0: the library picks,
+    at most one per CU)."""
     torch = _torch()
     _require_cuda(a, b, scale_a, scale_b)
     out_dtype = out_dtype or torch.float16

@@ -564,17 +564,53 @@ struct ExplicitSk {
     size_t       bytes;
 };
 
+// Estimated critical path of a stream-K plan on tile configuration C: the
+// longest block's k-tiles at C's rate per CU (`tops`, whole chip, measured on
+// the dense kernels: the smaller tiles sustain less), plus the partials the
+// last piece of the most-split tile reads back at `xbw` bytes/s (device-scope
+// loads; fitted to the square and cfg3 CLI shapes, lower for the larger
+// tiles, whose kernels spill around the exchange).  Splitting a tile over P
+// blocks costs its last block P - 1 partials, so fewer, larger tiles win
+// only where their pieces stay few: 2048^3 ran 75 µs on 256 x 256 tiles (4
+// pieces each) against 26 µs on 128 x 128 tiles (one block per tile).
+template <class C>
+double sk_cost(const gemm::SkPlan& s, double tops, double xbw)
+{
+    const uint64_t u    = (s.total() + s.blocks - 1) / s.blocks;
+    uint32_t       pmax = 1;
+    for(uint32_t t = 0; t < s.ntiles; ++t) pmax = std::max(pmax, s.pieces(t));
+    const double unit_s = 2.0 * C::kBM * C::kBN * C::kBK / (tops / device_cus());
+    return (double)u * unit_s + (pmax - 1) * (double)gemm::Partial<C>::kBytes / xbw;
+}
+
+// blocks = 0: the block count is chosen too, among one per CU and 1/2, 1/4,
+// 1/8 of that: a few tiles cut into many pieces cost their last blocks more
+// partials than the extra blocks save (512^3: 16 pieces per tile on 256
+// blocks, 4 on 64).
 ExplicitSk explicit_streamk(uint32_t m, uint32_t n, uint32_t k, uint32_t blocks)
 {
-    const uint32_t G  = blocks ? blocks : device_cus();
     const uint32_t nk = (k + 127) / 128;
-    auto plan = [&](uint32_t bm, uint32_t bn) {
-        const uint32_t tiles = ((m + bm - 1) / bm) * ((n + bn - 1) / bn);
-        return gemm::SkPlan{nk, tiles, (uint32_t)std::min<uint64_t>(G, (uint64_t)tiles * nk)};
-    };
-    ExplicitSk e{TileCfg::kMain, plan(GemmMain::kBM, GemmMain::kBN), 0};
-    if(e.plan.total() < 8ull * G) e = ExplicitSk{TileCfg::kMidM, plan(GemmMidM::kBM, GemmMidM::kBN), 0};
-    if(e.plan.total() < 8ull * G) e = ExplicitSk{TileCfg::kSmall, plan(GemmSmall::kBM, GemmSmall::kBN), 0};
+    ExplicitSk     e{TileCfg::kMain, {}, 0};
+    double         best = 1e300;
+    for(uint32_t div = 1; div <= (blocks ? 1u : 8u); div *= 2) {
+        const uint32_t G = blocks ? blocks : std::max(1u, device_cus() / div);
+        auto plan = [&](uint32_t bm, uint32_t bn) {
+            const uint32_t tiles = ((m + bm - 1) / bm) * ((n + bn - 1) / bn);
+            return gemm::SkPlan{nk, tiles, (uint32_t)std::min<uint64_t>(G, (uint64_t)tiles * nk)};
+        };
+        const ExplicitSk cand[3] = {
+            {TileCfg::kMain, plan(GemmMain::kBM, GemmMain::kBN), 0},
+            {TileCfg::kMidM, plan(GemmMidM::kBM, GemmMidM::kBN), 0},
+            {TileCfg::kSmall, plan(GemmSmall::kBM, GemmSmall::kBN), 0}};
+        const double cost[3] = {sk_cost<GemmMain>(cand[0].plan, 2.5e15, 13e9),
+                                sk_cost<GemmMidM>(cand[1].plan, 2.1e15, 15e9),
+                                sk_cost<GemmSmall>(cand[2].plan, 1.7e15, 35e9)};
+        for(int c = 0; c < 3; ++c)
+            if(cost[c] < best * (1 - 1e-9)) {
+                best = cost[c];
+                e    = cand[c];
+            }
+    }
     e.bytes = e.cfg == TileCfg::kMain   ? gemm::sk_workspace_bytes<GemmMain>(e.plan)
               : e.cfg == TileCfg::kMidM ? gemm::sk_workspace_bytes<GemmMidM>(e.plan)
                                         : gemm::sk_workspace_bytes<GemmSmall>(e.plan);

@@ -26,18 +26,21 @@ def sample_rows(m, seed):
     return np.unique(rows)
 
 
-# (m, n, k, blocks); blocks 0 = one per CU (256).  Tiles are 256 x 256 when
-# every block gets >= 8 k-tiles, else 128 x 256 under the same rule, else
-# 128 x 128; k-tiles are 128 deep.
+# (m, n, k, blocks); blocks 0 = one per CU (256).  The tile (256 x 256,
+# 128 x 256 or 128 x 128; k-tiles 128 deep) is the one with the shortest
+# estimated critical path (sk_cost, csrc/gemm_i8.hip); the comments give the
+# choice for 256 CUs.
 CASES = [
     (512, 512, 4096, 0),     # the reference sample's first default: 16 tiles of 128 x 128, 2 k-tiles a block
-    (1024, 1024, 4096, 0),   # 64 tiles of 128 x 128, 8 k-tiles a block
-    (2048, 2048, 4096, 0),   # 64 tiles of 256 x 256, 8 k-tiles a block
+    (1024, 1024, 4096, 0),   # 64 tiles of 128 x 128, 8 k-tiles a block, 4 pieces a tile
+    (2048, 2048, 4096, 0),   # 256 tiles of 128 x 128: one whole tile per block, no pieces
     (4096, 4096, 4096, 0),   # 256 tiles of 256 x 256: one whole tile per block, no pieces
-    (4100, 3000, 160, 100),  # 792 tiles x 2 k-tiles (a K tail), ragged edges: whole tiles and pieces
+    (512, 1024, 4096, 7),    # 8 tiles of 256 x 256 on 7 blocks: whole tiles and 2-piece tiles
+    (512, 512, 4096, 7),     # 8 tiles of 128 x 256 on 7 blocks: the same on the middle tile
+    (4100, 3000, 160, 100),  # 128 x 128, 2 k-tiles a tile (a K tail), ragged edges: whole tiles and pieces
     (1000, 1000, 1008, 0),   # 64 tiles, ragged edges, a K tail in the last k-tile
-    (300, 600, 8192, 2),     # 6 tiles of 256 x 256 on 2 blocks: three whole tiles each
-    (300, 600, 8192, 4),     # ... on 4 blocks: a whole tile and half of the next in each
+    (300, 600, 8192, 2),     # 9 tiles of 128 x 256 on 2 blocks: four and a half tiles each
+    (300, 600, 8192, 4),     # 128 x 128 on 4 blocks: whole tiles and pieces
     (256, 256, 256, 1),      # one block does everything
     (256, 256, 256, 20),     # more blocks than k-tiles: clamped to 8
     (777, 1234, 4112, 333),  # odd block count, 33 k-tiles a tile, ragged everything
