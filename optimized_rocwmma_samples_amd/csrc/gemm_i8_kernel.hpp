@@ -88,7 +88,9 @@ struct Cfg {
     static constexpr int kSubK    = kBK / kMfmaK;        // MFMA k-groups per tile
 
     static_assert(kChunks == 2 || kChunks == 4 || kChunks == 8, "BK in {32, 64, 128}");
-    static_assert(kSubK % 2 == 0 || kSubK == 1, "fragment ping-pong needs an even group count");
+    // the fragment slots alternate by k-group parity within a k-tile, and the
+    // first group of every k-tile uses slot 0
+    static_assert(kSubK % 2 == 0, "fragment ping-pong needs an even k-group count per k-tile");
     static_assert(kLoadsA * kWaves * 1024 == kABytes && kLoadsB * kWaves * 1024 == kBBytes,
                   "tile bytes must split evenly into 1 KiB wave-loads");
     static_assert(kMfma == 32 || kMfma == 16, "32x32x32 or 16x16x64 MFMA");
