@@ -60,7 +60,7 @@ __device__ __forceinline__ bool find_slot(uint32_t count, uint32_t target, F til
 
 // Local tile id -> (tm, tn) with GROUP_M grouping inside one problem.
 template <class C>
-__device__ __forceinline__ void local_tile(uint32_t id, uint32_t m, uint32_t n, uint32_t& m0,
+__host__ __device__ inline void local_tile(uint32_t id, uint32_t m, uint32_t n, uint32_t& m0,
                                            uint32_t& n0)
 {
     const uint32_t tiles_m = (m + C::kBM - 1) / C::kBM;
@@ -121,14 +121,16 @@ struct TailSplit {
     uint32_t base, left, parts;
 };
 
-__device__ __forceinline__ TailSplit tail_split(uint32_t total, uint32_t cus, uint32_t nk,
+__host__ __device__ inline TailSplit tail_split(uint32_t total, uint32_t cus, uint32_t nk,
                                                 bool enabled)
 {
     TailSplit s{total, 0u, 1u};
     if(!enabled || cus < 2) return s;
     const uint32_t left = total % cus;
     if(left == 0 || left > cus / 2) return s;
-    const uint32_t parts = min(min(cus / left, nk / kMinKtPerPart), kMaxParts);
+    uint32_t parts = cus / left;
+    parts          = parts < nk / kMinKtPerPart ? parts : nk / kMinKtPerPart;
+    parts          = parts < kMaxParts ? parts : kMaxParts;
     if(parts < 2) return s;
     return TailSplit{total - left, left, parts};
 }
@@ -142,27 +144,77 @@ __device__ __forceinline__ uint32_t moe_rows_of(const MoeArgs& q, uint32_t e)
     return min((uint32_t)cnt, q.rows - (uint32_t)st);
 }
 
-template <class C>
+// MoE tile shapes.  C is the block tile; W, its wide partner, has half the
+// rows and twice the columns in the same block of waves (W = C: no wide
+// tiles).  An expert's rows split into whole C tile rows and a rest; a rest
+// of at most W::kBM rows runs as one row of W tiles, which covers its
+// outputs with half the MFMA work of a C tile row, a larger rest as one more
+// C row.  (A top-k routing leaves many experts a rest of a few dozen rows:
+// an expert of 1050 rows takes 4 C rows + 1 W row instead of 5 C rows.)
+// Logical tile order: expert by expert, its C tiles (GROUP_M order) and then
+// its W tiles, so a W tile reads its weight rows soon after the expert's C
+// tiles did.
+template <class C, class W>
+struct MoeShape {
+    static constexpr bool kWide = !std::is_same<C, W>::value;
+    static_assert(!kWide || (2 * W::kBM == C::kBM && W::kBN == 2 * C::kBN
+                             && W::kThreads == C::kThreads && W::kBK == C::kBK),
+                  "W: half the rows and twice the columns of C, the same block and BK");
+
+    // rows of an expert that C tiles cover (the rest, if any, is W's)
+    __host__ __device__ static uint32_t c_rows(uint32_t rows)
+    {
+        const uint32_t rest = rows % C::kBM;
+        return kWide && rest != 0 && rest <= (uint32_t)W::kBM ? rows - rest : rows;
+    }
+    __host__ __device__ static uint32_t c_tiles(uint32_t rows, uint32_t n)
+    {
+        return (c_rows(rows) + C::kBM - 1) / C::kBM * ((n + C::kBN - 1) / C::kBN);
+    }
+    __host__ __device__ static uint32_t w_tiles(uint32_t rows, uint32_t n)
+    {
+        return c_rows(rows) != rows ? (n + W::kBN - 1) / W::kBN : 0u;
+    }
+    __host__ __device__ static uint32_t tiles(uint32_t rows, uint32_t n)
+    {
+        return c_tiles(rows, n) + w_tiles(rows, n);
+    }
+    // origin of the expert's tile `local` (< tiles(rows, n)); wide: a W tile
+    __host__ __device__ static void origin(uint32_t local, uint32_t rows, uint32_t n,
+                                           uint32_t& m0, uint32_t& n0, bool& wide)
+    {
+        const uint32_t nc = c_tiles(rows, n);
+        wide              = local >= nc;
+        if(wide) {
+            m0 = c_rows(rows);
+            n0 = (local - nc) * W::kBN;
+        } else {
+            local_tile<C>(local, c_rows(rows), n, m0, n0);
+        }
+    }
+};
+
+template <class C, class W>
 __device__ __forceinline__ uint32_t moe_total_tiles(const MoeArgs& q)
 {
-    const uint32_t tiles_n = (q.n + C::kBN - 1) / C::kBN;
-    auto tiles = [&](uint32_t e) { return (moe_rows_of(q, e) + C::kBM - 1) / C::kBM * tiles_n; };
     uint32_t e, first, total;
-    find_slot(q.experts, 0xFFFFFFFFu, tiles, e, first, total);
+    find_slot(q.experts, 0xFFFFFFFFu,
+              [&](uint32_t i) { return MoeShape<C, W>::tiles(moe_rows_of(q, i), q.n); }, e, first,
+              total);
     return total;
 }
 
-// Problem and tile origin of logical MoE tile `lid` (< total).
-template <class C, int OUT>
+// Problem, expert, first row, tile origin and shape (wide: W) of logical
+// MoE tile `lid` (< total).
+template <class C, class W, int OUT>
 __device__ __forceinline__ void moe_tile(const MoeArgs& q, uint32_t lid, KArgs& p, uint32_t& m0,
-                                         uint32_t& n0, uint32_t* expert = nullptr,
-                                         uint32_t* first_row = nullptr)
+                                         uint32_t& n0, uint32_t& e, uint32_t& row0, bool& wide)
 {
-    const uint32_t tiles_n = (q.n + C::kBN - 1) / C::kBN;
-    auto tiles = [&](uint32_t e) { return (moe_rows_of(q, e) + C::kBM - 1) / C::kBM * tiles_n; };
-    uint32_t e, first, total;
-    find_slot(q.experts, lid, tiles, e, first, total);
-    const uint32_t row0 = (uint32_t)q.expert_start[e];
+    using S = MoeShape<C, W>;
+    uint32_t first, total;
+    find_slot(q.experts, lid, [&](uint32_t i) { return S::tiles(moe_rows_of(q, i), q.n); }, e,
+              first, total);
+    row0  = (uint32_t)q.expert_start[e];
     p.a   = q.a + (size_t)row0 * q.lda;
     p.b   = q.w + (size_t)e * q.w_stride;
     p.c   = static_cast<int8_t*>(q.c) + (size_t)row0 * q.ldc * (OUT == W8A8_OUT_I32 ? 4 : 2);
@@ -176,25 +228,23 @@ __device__ __forceinline__ void moe_tile(const MoeArgs& q, uint32_t lid, KArgs& 
     p.ldc = q.ldc;
     p.tsa = q.tsa;
     p.tsb = q.tsb;
-    if(expert) *expert = e;
-    if(first_row) *first_row = row0;
-    local_tile<C>(lid - first, p.m, p.n, m0, n0);
+    S::origin(lid - first, p.m, p.n, m0, n0, wide);
 }
 
 // ---------------------------------------------------------------------------
 // SiLU(gate) * up epilogue of the MoE gate_up GEMM (w8a8_moe_gate_up_silu).
-// The weights' rows come interleaved in blocks of 16: 8 gate rows, then the
-// 8 up rows of the same outputs (w8a8_moe_interleave_gate_up).  In the MFMA
-// layout a lane holds, for each 32-column MFMA tile j, four runs g of 4
-// columns, (g * 8 + half * 4 + e); with that interleave run g = 2 * gp is
-// gate and g = 2 * gp + 1 is up of the same 4 outputs
-//   o = n0 / 2 + wn * kWaveN / 2 + j * 16 + gp * 8 + half * 4 + e,
+// The weights' rows come interleaved in blocks of 32: 16 gate rows, then the
+// 16 up rows of the same outputs (w8a8_moe_interleave_gate_up).  In the
+// 16 x 16 MFMA layout a lane holds, for each 16-column MFMA tile, a run of
+// 4 columns 4 (lane / 16) + e; with that interleave tile 2 p is gate and
+// tile 2 p + 1 is up of the same 4 outputs
+//   o = n0 / 2 + wn * kWaveN / 2 + 16 p + 4 (lane / 16) + e,
 // so silu(g) * u is formed in registers: g and u rounded to fp16 (the values
 // the unfused gate_up GEMM would write), a = silu_mul_epi(g, u) in fp32, h =
 // fp16(a).  h is written at half the gate_up width, and each wave writes,
 // per row, the max over its kWaveN / 2 outputs of |float(h) * s2[e, o]| to
-// pmax[n0 / kWaveN + wn][row] (group-major, so the 32 rows of an MFMA tile
-// are 128 contiguous bytes): the requantization then knows every row's scale
+// pmax[n0 / kWaveN + wn][row] (group-major, so a wave's rows are contiguous
+// floats): the requantization then knows every row's scale
 // before it reads the row.  The SiLU kernels use wave tiles kWaveN = 128
 // wide, so each wave's h rows are 128-byte lines.
 // ---------------------------------------------------------------------------
@@ -309,86 +359,130 @@ __device__ __forceinline__ void epilogue_silu(const KArgs& p, uint32_t m0, uint3
     }
 }
 
-template <class C, int OUT, bool SILU = false>
+// One whole MoE tile of shape X (C or W) with its epilogue.
+template <class X, int OUT, bool SILU>
+__device__ __forceinline__ void moe_whole(const KArgs& p, uint32_t m0, uint32_t n0, uint32_t e,
+                                          uint32_t row0, const SiluOut& so, uint32_t nk,
+                                          int vec_ok, int8_t* lds)
+{
+    if constexpr(SILU) {
+        Acc<X>       acc;
+        EpiScales<X> sc;
+        gemm_tile_acc<X, true>(p, m0, n0, vec_ok, lds, 0, nk, acc, sc);
+        epilogue_silu<X>(p, m0, n0, lds, 0, acc, sc, so.h + (size_t)row0 * so.ldh, so.pmax + row0,
+                         so.s2 ? so.s2 + (size_t)e * so.inter : nullptr, so.ldh, so.ldp,
+                         so.inter);
+    } else {
+        gemm_tile<X, OUT>(p, m0, n0, vec_ok, lds);
+    }
+}
+
+// The fixup of a split MoE tile of shape X for this block's waves: sum the
+// parts' partials (slots slot * parts ...) and run the epilogue.
+template <class X, int OUT, bool SILU>
+__device__ __forceinline__ void moe_fix(const MoeArgs& q, const KArgs& p, uint32_t m0,
+                                        uint32_t n0, uint32_t e, uint32_t row0, const SiluOut& so,
+                                        uint32_t slot, uint32_t parts, int wave_base, int vec_ok,
+                                        int8_t* lds)
+{
+    Acc<X> acc;
+    acc.zero();
+    const uint32_t tid = wave_base * kWave + threadIdx.x;
+    for(uint32_t part = 0; part < parts; ++part)
+        add_partial<X>(q.ws + (size_t)(slot * parts + part) * Partial<X>::kInts, tid, acc);
+    if constexpr(SILU) {
+        const int    wave = wave_base + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+        EpiScales<X> sc;
+        sc.load(p, m0, n0, wave / X::kWavesN, wave % X::kWavesN, threadIdx.x % kWave, vec_ok);
+        epilogue_silu<X>(p, m0, n0, lds, wave_base, acc, sc, so.h + (size_t)row0 * so.ldh,
+                         so.pmax + row0,
+                         so.s2 ? so.s2 + (size_t)e * so.inter : nullptr, so.ldh, so.ldp,
+                         so.inter);
+    } else {
+        tile_epilogue<X, OUT>(p, m0, n0, vec_ok, lds, acc, wave_base);
+    }
+}
+
+// MoE GEMM over C tiles and, for the experts' short rests, W tiles
+// (MoeShape); W = C: C tiles only.  The two shapes have the same wave tile,
+// so they share the partial slot layout and the fixup blocks.
+template <class C, class W, int OUT, bool SILU = false>
 __global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_moe_kernel(MoeArgs q, int vec_ok,
                                                                       SiluOut so)
 {
+    static_assert(Partial<W>::kInts == Partial<C>::kInts
+                      && Partial<W>::kPieces == Partial<C>::kPieces
+                      && Partial<W>::kFixupLds == Partial<C>::kFixupLds,
+                  "W and C share the partial slots and the fixup blocks");
+    constexpr bool kWide = MoeShape<C, W>::kWide;
     extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
-    const uint32_t  total = moe_total_tiles<C>(q);
+    const uint32_t  total = moe_total_tiles<C, W>(q);
     const uint32_t  nk    = (q.k + C::kBK - 1) / C::kBK;
     const TailSplit sp    = tail_split(total, q.cus, nk, q.ws != nullptr);
+    KArgs           p;
+    uint32_t        m0, n0, e, row0;
+    bool            wide;
     if(blockIdx.x < sp.base) {
-        KArgs    p;
-        uint32_t m0, n0, e, row0;
-        moe_tile<C, OUT>(q, xcd_remap(blockIdx.x, sp.base), p, m0, n0, &e, &row0);
-        if constexpr(SILU) {
-            Acc<C>       acc;
-            EpiScales<C> sc;
-            gemm_tile_acc<C, true>(p, m0, n0, vec_ok, lds, 0, nk, acc, sc);
-            epilogue_silu<C>(p, m0, n0, lds, 0, acc, sc, so.h + (size_t)row0 * so.ldh,
-                             so.pmax + row0,
-                             so.s2 ? so.s2 + (size_t)e * so.inter : nullptr, so.ldh, so.ldp,
-                             so.inter);
-        } else {
-            gemm_tile<C, OUT>(p, m0, n0, vec_ok, lds);
-        }
+        moe_tile<C, W, OUT>(q, xcd_remap(blockIdx.x, sp.base), p, m0, n0, e, row0, wide);
+        if(kWide && wide)
+            moe_whole<W, OUT, SILU>(p, m0, n0, e, row0, so, nk, vec_ok, lds);
+        else
+            moe_whole<C, OUT, SILU>(p, m0, n0, e, row0, so, nk, vec_ok, lds);
         return;
     }
     const uint32_t x = blockIdx.x - sp.base;
     if(x >= sp.left * sp.parts) return;
     const uint32_t slot = x / sp.parts, part = x % sp.parts;
-    KArgs          p;
-    uint32_t       m0, n0;
-    moe_tile<C, OUT>(q, sp.base + slot, p, m0, n0);
     const uint32_t kt0 = part * nk / sp.parts, kt1 = (part + 1) * nk / sp.parts;
-    gemm_tile<C, OUT, true>(p, m0, n0, vec_ok, lds, kt0, kt1 - kt0,
-                            q.ws + (size_t)x * Partial<C>::kInts);
+    moe_tile<C, W, OUT>(q, sp.base + slot, p, m0, n0, e, row0, wide);
+    int32_t* const ws = q.ws + (size_t)x * Partial<C>::kInts;
+    if(kWide && wide)
+        gemm_tile<W, OUT, true>(p, m0, n0, vec_ok, lds, kt0, kt1 - kt0, ws);
+    else
+        gemm_tile<C, OUT, true>(p, m0, n0, vec_ok, lds, kt0, kt1 - kt0, ws);
 }
 
 // Split tiles, kPieces blocks each: a block holds kFixupWaves of the tile's
 // waves, sums their accumulators over the parts in order and runs their part
 // of the tile epilogue.
-template <class C, int OUT, bool SILU = false>
+template <class C, class W, int OUT, bool SILU = false>
 __global__ void __launch_bounds__(Partial<C>::kFixupWaves * kWave, 1)
     gemm_i8_moe_fixup_kernel(MoeArgs q, int vec_ok, SiluOut so)
 {
+    constexpr bool kWide = MoeShape<C, W>::kWide;
     extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
-    const uint32_t  total = moe_total_tiles<C>(q);
-    const uint32_t  nk    = (q.k + C::kBK - 1) / C::kBK;
-    const TailSplit sp    = tail_split(total, q.cus, nk, q.ws != nullptr);
-    const uint32_t  slot  = blockIdx.x / Partial<C>::kPieces;
+    const uint32_t  total     = moe_total_tiles<C, W>(q);
+    const uint32_t  nk        = (q.k + C::kBK - 1) / C::kBK;
+    const TailSplit sp        = tail_split(total, q.cus, nk, q.ws != nullptr);
+    const uint32_t  slot      = blockIdx.x / Partial<C>::kPieces;
     const int       wave_base = (int)(blockIdx.x % Partial<C>::kPieces) * Partial<C>::kFixupWaves;
     if(slot >= sp.left) return;
     KArgs    p;
     uint32_t m0, n0, e, row0;
-    moe_tile<C, OUT>(q, sp.base + slot, p, m0, n0, &e, &row0);
-    Acc<C> acc;
-    acc.zero();
-    const uint32_t tid = wave_base * kWave + threadIdx.x;
-    for(uint32_t part = 0; part < sp.parts; ++part)
-        add_partial<C>(q.ws + (size_t)(slot * sp.parts + part) * Partial<C>::kInts, tid, acc);
-    if constexpr(SILU) {
-        const int    wave = wave_base + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-        EpiScales<C> sc;
-        sc.load(p, m0, n0, wave / C::kWavesN, wave % C::kWavesN, threadIdx.x % kWave, vec_ok);
-        epilogue_silu<C>(p, m0, n0, lds, wave_base, acc, sc, so.h + (size_t)row0 * so.ldh,
-                         so.pmax + row0,
-                         so.s2 ? so.s2 + (size_t)e * so.inter : nullptr, so.ldh, so.ldp,
-                         so.inter);
-    } else {
-        tile_epilogue<C, OUT>(p, m0, n0, vec_ok, lds, acc, wave_base);
-    }
+    bool     wide;
+    moe_tile<C, W, OUT>(q, sp.base + slot, p, m0, n0, e, row0, wide);
+    if(kWide && wide)
+        moe_fix<W, OUT, SILU>(q, p, m0, n0, e, row0, so, slot, sp.parts, wave_base, vec_ok, lds);
+    else
+        moe_fix<C, OUT, SILU>(q, p, m0, n0, e, row0, so, slot, sp.parts, wave_base, vec_ok, lds);
 }
 
-// One flag per (config, output type, kernel kind): the two output types of a
+// One flag per (configs, output type, kernel kind): the two output types of a
 // kernel share a function-pointer type, so the kernel itself cannot key it.
-template <class C, int OUT, int KIND>
+// The dynamic LDS is the larger of the two tiles' rings.
+template <class C, class W>
+constexpr int moe_lds_bytes()
+{
+    return C::kLdsBytes > W::kLdsBytes ? C::kLdsBytes : W::kLdsBytes;
+}
+
+template <class C, int OUT, int KIND, class W = C>
 void raise_lds_once(const void* kern)
 {
     static std::once_flag once;
     std::call_once(once, [&] {
         (void)hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  C::kLdsBytes);
+                                  moe_lds_bytes<C, W>());
         (void)hipGetLastError();
     });
 }
@@ -411,7 +505,8 @@ hipError_t launch_grouped(const KArgs* groups_dev, uint32_t ngroups, uint32_t to
 }
 
 // Grid bound: every expert's last m tile may be partial, so at most
-// ceil(rows / BM) + experts m tiles in total; a tail split adds at most
+// ceil(rows / BM) + experts C tile rows in total (a row of W tiles replaces
+// one C row and has at most as many tiles); a tail split adds at most
 // cus - 1 blocks.  The fixup launch has kPieces blocks per split tile (at
 // most cus / 2 split tiles).
 template <class C>
@@ -421,59 +516,52 @@ size_t moe_workspace_bytes(uint32_t cus)
 }
 
 template <class C>
-hipError_t launch_moe(const MoeArgs& q, int out_type, int vec_ok, hipStream_t stream)
+uint64_t moe_grid_bound(const MoeArgs& q)
 {
     const uint32_t tiles_n = (q.n + C::kBN - 1) / C::kBN;
-    const uint64_t bound   = ((uint64_t)(q.rows + C::kBM - 1) / C::kBM + q.experts) * tiles_n;
+    return ((uint64_t)(q.rows + C::kBM - 1) / C::kBM + q.experts) * tiles_n;
+}
+
+template <class C, class W, int OUT, bool SILU>
+hipError_t launch_moe_kernels(const MoeArgs& q, const SiluOut& so, int vec_ok, hipStream_t stream)
+{
+    const uint64_t bound = moe_grid_bound<C>(q);
     if(bound == 0) return hipSuccess;
     const bool     split = q.ws != nullptr && q.cus >= 2;
     const uint64_t grid  = bound + (split ? q.cus : 0);
     const uint32_t fixup_blocks = q.cus / 2 * Partial<C>::kPieces;
     if(grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
-    if(out_type == W8A8_OUT_I32) {
-        raise_lds_once<C, W8A8_OUT_I32, 1>(reinterpret_cast<const void*>(gemm_i8_moe_kernel<C, W8A8_OUT_I32>));
-        hipLaunchKernelGGL((gemm_i8_moe_kernel<C, W8A8_OUT_I32>), dim3((uint32_t)grid),
-                           dim3(C::kThreads), C::kLdsBytes, stream, q, vec_ok, SiluOut{});
-        if(split) {
-            hipLaunchKernelGGL((gemm_i8_moe_fixup_kernel<C, W8A8_OUT_I32>), dim3(fixup_blocks),
-                               dim3(Partial<C>::kFixupWaves * kWave), Partial<C>::kFixupLds,
-                               stream, q, vec_ok, SiluOut{});
-        }
-    } else {
-        raise_lds_once<C, W8A8_OUT_F16, 1>(reinterpret_cast<const void*>(gemm_i8_moe_kernel<C, W8A8_OUT_F16>));
-        hipLaunchKernelGGL((gemm_i8_moe_kernel<C, W8A8_OUT_F16>), dim3((uint32_t)grid),
-                           dim3(C::kThreads), C::kLdsBytes, stream, q, vec_ok, SiluOut{});
-        if(split) {
-            hipLaunchKernelGGL((gemm_i8_moe_fixup_kernel<C, W8A8_OUT_F16>), dim3(fixup_blocks),
-                               dim3(Partial<C>::kFixupWaves * kWave), Partial<C>::kFixupLds,
-                               stream, q, vec_ok, SiluOut{});
-        }
-    }
+    constexpr int kLds = moe_lds_bytes<C, W>();
+    raise_lds_once<C, OUT, (SILU ? 2 : 1), W>(
+        reinterpret_cast<const void*>(gemm_i8_moe_kernel<C, W, OUT, SILU>));
+    hipLaunchKernelGGL((gemm_i8_moe_kernel<C, W, OUT, SILU>), dim3((uint32_t)grid),
+                       dim3(C::kThreads), kLds, stream, q, vec_ok, so);
+    if(split)
+        hipLaunchKernelGGL((gemm_i8_moe_fixup_kernel<C, W, OUT, SILU>), dim3(fixup_blocks),
+                           dim3(Partial<C>::kFixupWaves * kWave), Partial<C>::kFixupLds, stream,
+                           q, vec_ok, so);
     return hipGetLastError();
+}
+
+// C tiles and, for the experts' rests of at most W::kBM rows, W tiles (W = C:
+// C tiles only).
+template <class C, class W = C>
+hipError_t launch_moe(const MoeArgs& q, int out_type, int vec_ok, hipStream_t stream)
+{
+    return out_type == W8A8_OUT_I32
+               ? launch_moe_kernels<C, W, W8A8_OUT_I32, false>(q, SiluOut{}, vec_ok, stream)
+               : launch_moe_kernels<C, W, W8A8_OUT_F16, false>(q, SiluOut{}, vec_ok, stream);
 }
 
 // The gate_up GEMM with the SiLU epilogue (q.n = 2 * inter interleaved
 // columns, fp16 scales path; the caller checked vec_ok and the alignment of
-// h, ldh and s2).
-template <class C>
+// h, ldh and s2).  Both tiles' waves are kWaveN wide, the width of one pmax
+// group.
+template <class C, class W = C>
 hipError_t launch_moe_silu(const MoeArgs& q, const SiluOut& so, int vec_ok, hipStream_t stream)
 {
-    const uint32_t tiles_n = (q.n + C::kBN - 1) / C::kBN;
-    const uint64_t bound   = ((uint64_t)(q.rows + C::kBM - 1) / C::kBM + q.experts) * tiles_n;
-    if(bound == 0) return hipSuccess;
-    const bool     split = q.ws != nullptr && q.cus >= 2;
-    const uint64_t grid  = bound + (split ? q.cus : 0);
-    const uint32_t fixup_blocks = q.cus / 2 * Partial<C>::kPieces;
-    if(grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
-    raise_lds_once<C, W8A8_OUT_F16, 2>(
-        reinterpret_cast<const void*>(gemm_i8_moe_kernel<C, W8A8_OUT_F16, true>));
-    hipLaunchKernelGGL((gemm_i8_moe_kernel<C, W8A8_OUT_F16, true>), dim3((uint32_t)grid),
-                       dim3(C::kThreads), C::kLdsBytes, stream, q, vec_ok, so);
-    if(split)
-        hipLaunchKernelGGL((gemm_i8_moe_fixup_kernel<C, W8A8_OUT_F16, true>), dim3(fixup_blocks),
-                           dim3(Partial<C>::kFixupWaves * kWave), Partial<C>::kFixupLds, stream,
-                           q, vec_ok, so);
-    return hipGetLastError();
+    static_assert(C::kWaveN == W::kWaveN, "one pmax group per wave column in both tiles");
+    return launch_moe_kernels<C, W, W8A8_OUT_F16, true>(q, so, vec_ok, stream);
 }
 
 } // namespace gemm

@@ -126,24 +126,24 @@ constexpr uint32_t kOob         = 0x80000000u;
 
 // Hardware dispatches block ids round-robin over the 8 XCDs.  Return the
 // logical tile id such that each XCD owns a contiguous range of logical ids.
-__device__ __forceinline__ uint32_t xcd_remap(uint32_t bid, uint32_t total)
+__host__ __device__ inline uint32_t xcd_remap(uint32_t bid, uint32_t total)
 {
     constexpr uint32_t kXcd = 8;
     const uint32_t     q    = total / kXcd;
     const uint32_t     r    = total % kXcd;
     const uint32_t     x    = bid % kXcd;
     const uint32_t     i    = bid / kXcd;
-    return x * q + min(x, r) + i;
+    return x * q + (x < r ? x : r) + i;
 }
 
 template <int GROUP_M>
-__device__ __forceinline__ void tile_coords(uint32_t lid, uint32_t tiles_m, uint32_t tiles_n,
+__host__ __device__ inline void tile_coords(uint32_t lid, uint32_t tiles_m, uint32_t tiles_n,
                                             uint32_t& tm, uint32_t& tn)
 {
     const uint32_t per_group = GROUP_M * tiles_n;
     const uint32_t group     = lid / per_group;
     const uint32_t first_m   = group * GROUP_M;
-    const uint32_t gsize     = min(tiles_m - first_m, (uint32_t)GROUP_M);
+    const uint32_t gsize     = tiles_m - first_m < (uint32_t)GROUP_M ? tiles_m - first_m : GROUP_M;
     const uint32_t in_group  = lid % per_group;
     tm                       = first_m + in_group % gsize;
     tn                       = in_group / gsize;

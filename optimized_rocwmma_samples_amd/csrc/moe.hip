@@ -727,6 +727,9 @@ __global__ void __launch_bounds__(256)
 }
 
 using GemmGrouped = gemm::Cfg<256, 256, 128, 2, 2, 4, 4, 16>;
+// GemmGrouped's wide partner: an expert's rest of at most 128 rows runs as
+// 128 x 512 tiles (8 waves of 128 x 64, as GemmGrouped; 2 stages of 80 KiB).
+using GemmGroupedWide = gemm::Cfg<128, 512, 128, 2, 1, 8, 4, 16>;
 // MoE GEMM over experts of a few hundred rows: 128-row tiles waste less of
 // each expert's last tile row (moe_tile_rows_128).
 using GemmGroupedMid = gemm::Cfg<128, 256, 128, 3, 2, 4, 4, 16>;
@@ -948,15 +951,16 @@ hipError_t launch_moe_gemm(const MoeGemmArgs& a, hipStream_t stream)
     // rows (the sort's padded capacity) / experts stands for the rows per expert
     if(moe_tile_rows_128(a.rows, a.experts))
         return gemm::launch_moe<GemmGroupedMid>(q, a.out_type, vec_ok, stream);
-    return gemm::launch_moe<GemmGrouped>(q, a.out_type, vec_ok, stream);
+    return gemm::launch_moe<GemmGrouped, GemmGroupedWide>(q, a.out_type, vec_ok, stream);
 }
 
 // The SiLU epilogue's tiles: wave tiles 128 columns wide (64 outputs, one
 // 128-byte line of h per row and wave), otherwise as GemmGrouped /
 // GemmGroupedMid (16 x 16 x 64 MFMA, whose lane layout the 32-row gate/up
 // interleave matches).
-using GemmSilu    = gemm::Cfg<256, 256, 128, 2, 4, 2, 4, 16>;
-using GemmSiluMid = gemm::Cfg<128, 256, 128, 3, 4, 2, 4, 16>;
+using GemmSilu     = gemm::Cfg<256, 256, 128, 2, 4, 2, 4, 16>;
+using GemmSiluMid  = gemm::Cfg<128, 256, 128, 3, 4, 2, 4, 16>;
+using GemmSiluWide = gemm::Cfg<128, 512, 128, 2, 2, 4, 4, 16>; // GemmSilu's wide partner
 static_assert(GemmSilu::kWaveN == GemmSiluMid::kWaveN, "one pmax layout for both tiles");
 static_assert(gemm::Partial<GemmSilu>::kBytes == gemm::Partial<GemmGrouped>::kBytes
                   && gemm::Partial<GemmSiluMid>::kBytes == gemm::Partial<GemmGroupedMid>::kBytes,
@@ -1007,7 +1011,7 @@ hipError_t launch_moe_gate_up_silu(const MoeSiluArgs& a, hipStream_t stream)
     const int vec_ok = a.scale_w == nullptr || reinterpret_cast<uintptr_t>(a.scale_w) % 16 == 0;
     hipError_t e = moe_tile_rows_128(a.rows, a.experts)
                        ? gemm::launch_moe_silu<GemmSiluMid>(q, so, vec_ok, stream)
-                       : gemm::launch_moe_silu<GemmSilu>(q, so, vec_ok, stream);
+                       : gemm::launch_moe_silu<GemmSilu, GemmSiluWide>(q, so, vec_ok, stream);
     if(e != hipSuccess) return e;
 
     const uint64_t h_bytes  = (uint64_t)a.rows * a.inter * 2;

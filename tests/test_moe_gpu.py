@@ -197,23 +197,35 @@ def _tail_split_parts(total, cus, nk):
     return (left, parts) if parts >= 2 else (0, 1)
 
 
-# (expert row counts, K, N) on 256 CUs (tile rows of 256 or 128, _tile_rows):
-# 18 tile rows x 16 = 288 tiles leave 32 tail tiles (expert 2, whose second
-# tile row holds 44 rows) cut in 2; 5 tile rows of 128 x 2 = 10 tiles (fewer
-# than the CUs) each cut in 8; one expert of 17 tile rows (16 tail tiles cut
-# in 2); an empty expert between two others (4 tile rows x 16 = 64 tiles,
-# all cut in 2)
+# (expert row counts, K, N) on 256 CUs (_moe_tiles): rows 1000 / 3000 / 300
+# take 4 / 12 / 1 rows of 256 x 256 tiles and expert 2's rest of 44 rows a
+# row of 128 x 512 tiles: 272 + 8 = 280 tiles leave 24 tail tiles cut in 2;
+# 5 tile rows of 128 x 2 = 10 tiles (fewer than the CUs) each cut in 8; one
+# expert of 17 tile rows (16 tail tiles cut in 2); an empty expert between
+# two others whose rests of 44 and 4 rows take 128 x 512 tiles (32 + 16 = 48
+# tiles, all cut in 2: split tiles of both shapes)
 SPLIT_CASES = [([1000, 3000, 300], 4096, 4096), ([200, 300], 16384, 512),
                ([4352], 4096, 4096), ([300, 0, 260], 4096, 4096)]
 
 
-def _tile_rows(counts, rows):
-    # 128-row tiles when u128 * 0.8 > u256 for the average padded rows per
-    # expert (the library's choice), else 256
+def _moe_tiles(counts, rows, n):
+    """Host restatement of the library's MoE tiling, used only to check that a
+    test shape takes the path it is meant to: 128-row tiles when u128 * 0.8 >
+    u256 for the average padded rows per expert, else 256-row tiles, where an
+    expert's rest of at most 128 rows takes a row of 128 x 512 tiles.
+    Returns (tiles, tile rows, wide tiles)."""
     avg = rows / len(counts)
     u = {bm: avg / (np.ceil(avg / bm) * bm) for bm in (128, 256)}
     bm = 128 if u[128] * 0.8 > u[256] else 256
-    return sum(-(-c // bm) for c in counts), bm
+    tiles = wide = 0
+    for c in counts:
+        rest = c % bm
+        if bm == 256 and 0 < rest <= 128:
+            tiles += (c // 256) * (-(-n // 256)) + (-(-n // 512))
+            wide += -(-n // 512)
+        else:
+            tiles += -(-c // bm) * (-(-n // 256))
+    return tiles, bm, wide
 
 
 @pytest.mark.parametrize("counts,k,n", SPLIT_CASES)
@@ -230,7 +242,7 @@ def test_moe_gemm_tail_split_exact(w8a8, gpu, counts, k, n):
     sa = G.uniform(seed, G.TID_SA, (rows,), 1e-3, 1e-2)
     sw = G.uniform(seed, G.TID_SB, (e, n), 1e-3, 1e-2)
     cus = torch.cuda.get_device_properties(gpu).multi_processor_count
-    total = _tile_rows(counts, rows)[0] * (-(-n // 256))
+    total = _moe_tiles(counts, rows, n)[0]
     left, parts = _tail_split_parts(total, cus, -(-k // 128))
     assert left > 0 and parts >= 2, (total, cus, "shape does not exercise the tail split")
     args = (dev(a, gpu), dev(w, gpu), dev(start, gpu), dev(count, gpu))
@@ -258,7 +270,8 @@ def test_moe_gemm_tail_split_exact(w8a8, gpu, counts, k, n):
 
 
 # About 1000 tiles of 256 rows over four experts (four rounds of the CUs),
-# fp16 and int32, with the tail split (workspace) and without.
+# fp16 and int32, with the tail split (workspace) and without; the last
+# expert's rest of 8 rows runs as 16 whole 128 x 512 tiles.
 def test_moe_gemm_many_tiles_exact(w8a8, gpu):
     import torch
     counts, k, n, unit = [2000, 1500, 2500, 1800], 1024, 8192, 32
@@ -266,7 +279,7 @@ def test_moe_gemm_many_tiles_exact(w8a8, gpu):
     padded = -(-count // unit) * unit
     start = np.concatenate([[0], np.cumsum(padded)]).astype(np.int32)
     rows, e = int(start[-1]), len(counts)
-    assert _tile_rows(counts, rows)[1] == 256
+    assert _moe_tiles(counts, rows, n)[1:] == (256, 16)
     seed = 4242
     a = G.int8(seed, G.TID_A, (rows, k))
     w = G.int8(seed, G.TID_B, (e, n, k))
@@ -525,6 +538,59 @@ def test_moe_gate_up_silu(w8a8, gpu, t, k, e, h, inter, unit, with_s2):
             assert (qg[r1:start[x + 1]] == 99).all() and (rg[r1:start[x + 1]] == -1).all()
     # silu's exp differs from numpy's by an ulp or so: the fp16 activation, and
     # through it q or r, may differ in rare near-ties
+    assert off1 <= max(2, int(1e-3 * total * inter)), f"{off1} off-by-one values"
+    assert exact >= total - max(2, total // 100), f"{total - exact} row scales differ"
+
+
+# Explicit expert row counts for the 256-row SiLU tile: rests of 1-128 rows
+# (300, 40, 1100, 128) take rows of 128 x 512 tiles, a rest of 129 rows and
+# 1000 rows take 256-row tiles, and one expert is empty.  inter = 512 (1024
+# interleaved columns): 40 + 8 = 48 tiles, every one cut along K by the tail
+# split, so the fixup kernel runs the SiLU epilogue of both tile shapes;
+# inter = 7168: 560 + 112 = 672 tiles, a last round of 160 (not split), all
+# whole.  The oracle checks each expert's first and last rows and a sample.
+SILU_WIDE_COUNTS = [300, 1000, 40, 1100, 0, 129, 128]
+
+
+@pytest.mark.parametrize("inter,k,split", [(512, 4096, True), (7168, 256, False)])
+def test_moe_gate_up_silu_wide_rests(w8a8, gpu, inter, k, split):
+    import torch
+    unit, seed = 32, inter + k
+    count = np.array(SILU_WIDE_COUNTS, np.int32)
+    padded = -(-count // unit) * unit
+    start = np.concatenate([[0], np.cumsum(padded)]).astype(np.int32)
+    rows, e = int(start[-1]), len(count)
+    tiles, bm, wide = _moe_tiles(SILU_WIDE_COUNTS, rows, 2 * inter)
+    assert bm == 256 and wide > 0
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
+    assert (_tail_split_parts(tiles, cus, -(-k // 128))[0] > 0) == split, tiles
+    a = G.int8(seed, G.TID_A, (rows, k))
+    wgu = G.int8(seed, G.TID_B, (e, 2 * inter, k))
+    sa = G.uniform(seed, G.TID_SA, (rows,), 1e-3, 1e-2)
+    sgu = G.uniform(seed, G.TID_SB, (e, 2 * inter), 1e-3, 1e-2)
+    s2 = G.uniform(seed, G.TID_S, (e, inter), 0.5, 2.0)
+    w_il, s_il = w8a8.moe_interleave_gate_up(dev(wgu, gpu), dev(sgu, gpu))
+    q = torch.full((rows, inter), 99, dtype=torch.int8, device=gpu)
+    r = torch.full((rows,), -1.0, dtype=torch.float32, device=gpu)
+    w8a8.moe_gate_up_silu(dev(a, gpu), w_il, dev(start, gpu), dev(count, gpu), dev(sa, gpu), s_il,
+                          dev(s2, gpu), q=q, row_scale=r)
+    qg, rg = host(q), host(r)
+    off1 = exact = total = 0
+    for x in range(e):
+        r0, r1 = start[x], start[x] + count[x]
+        if r1 > r0:
+            pick = np.unique(np.concatenate([np.arange(r0, min(r1, r0 + 8)),
+                                             np.arange(max(r0, r1 - 40), r1),
+                                             np.random.default_rng(x).integers(r0, r1, 24)]))
+            gu = O.dequant_f16(O.gemm_i32(a[pick], wgu[x]), sa[pick], sgu[x])
+            qe, re = O.smoothquant(_silu_h16(gu), s2[x])
+            d = np.abs(qg[pick].astype(np.int32) - qe)
+            assert d.max() <= 1
+            off1 += int((d != 0).sum())
+            exact += int((rg[pick].view(np.int32) == re.view(np.int32)).sum())
+            total += pick.size
+        if r1 < start[x + 1]:  # padding rows untouched
+            assert (qg[r1:start[x + 1]] == 99).all() and (rg[r1:start[x + 1]] == -1).all()
     assert off1 <= max(2, int(1e-3 * total * inter)), f"{off1} off-by-one values"
     assert exact >= total - max(2, total // 100), f"{total - exact} row scales differ"
 
