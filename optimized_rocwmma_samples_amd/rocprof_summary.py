@@ -30,6 +30,12 @@ def short_name(name: str) -> str:
     return base.replace("w8a8::", "")
 
 
+def compact_name(name: str) -> str:
+    """short_name without the gemm:: namespace and the blanks after template
+    argument commas, so kernels with two tile configurations fit a column."""
+    return short_name(name).replace("gemm::", "").replace(", ", ",")
+
+
 def _rows(pattern: str):
     for path in sorted(glob.glob(pattern, recursive=True)):
         with open(path, newline="") as f:
@@ -57,10 +63,10 @@ def trace(directory: str, match: str = "w8a8|gemm|sq_|neg") -> str:
         if not re.search(match, name):
             continue
         dur = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
-        groups[(short_name(name), _grid(r))].append(dur)
-    out = [f"{'kernel':84s} {'grid':>9s} {'calls':>5s} {'avg_us':>10s} {'min_us':>10s}"]
+        groups[(compact_name(name), _grid(r))].append(dur)
+    out = [f"{'kernel':88s} {'grid':>9s} {'calls':>5s} {'avg_us':>10s} {'min_us':>10s}"]
     for (name, grid), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
-        out.append(f"{name[:84]:84s} {grid:>9s} {len(d):5d} {sum(d) / len(d) / 1e3:10.2f} "
+        out.append(f"{name[:88]:88s} {grid:>9s} {len(d):5d} {sum(d) / len(d) / 1e3:10.2f} "
                    f"{min(d) / 1e3:10.2f}")
     return "\n".join(out)
 
