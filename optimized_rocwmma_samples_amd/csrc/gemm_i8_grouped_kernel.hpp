@@ -321,21 +321,24 @@ __device__ __forceinline__ void epilogue_silu(const KArgs& p, uint32_t m0, uint3
             const int    uv[4]  = {uq.x, uq.y, uq.z, uq.w};
             const float  sgv[4] = {sg.x, sg.y, sg.z, sg.w};
             const float  suv[4] = {su.x, su.y, su.z, su.w};
-            uint32_t     hb[4];
+            float        act[4];
 #pragma unroll
             for(int e = 0; e < 4; ++e) {
-                const float g = half_bits_to_float(
-                    float_to_half_bits_2step(((float)gv[e] * sc.sa[i]) * sgv[e]));
-                const float u = half_bits_to_float(
-                    float_to_half_bits_2step(((float)uv[e] * sc.sa[i]) * suv[e]));
-                hb[e] = float_to_half_bits_2step(silu_mul_epi(g, u));
-                mx    = fmaxf(mx, fabsf(half_bits_to_float(hb[e]) * s2v[q][e]));
+                // g and u rounded to fp16 together, as the unfused GEMM stores them
+                const uint32_t gu = float2_to_half2_bits_2step(
+                    ((float)gv[e] * sc.sa[i]) * sgv[e], ((float)uv[e] * sc.sa[i]) * suv[e]);
+                act[e] = silu_mul_epi(half_bits_to_float(gu & 0xFFFFu), half_bits_to_float(gu >> 16));
             }
+            const uint32_t h01 = float2_to_half2_bits_2step(act[0], act[1]);
+            const uint32_t h23 = float2_to_half2_bits_2step(act[2], act[3]);
+            const uint32_t hb[4] = {h01 & 0xFFFFu, h01 >> 16, h23 & 0xFFFFu, h23 >> 16};
+#pragma unroll
+            for(int e = 0; e < 4; ++e) mx = fmaxf(mx, fabsf(half_bits_to_float(hb[e]) * s2v[q][e]));
             const int oc   = q * 16 + lgrp * 4; // output column within the wave
             const int phys = S::chunk(oc >> 3, row);
             v2i       pk;
-            pk.x = (int)(hb[0] | (hb[1] << 16));
-            pk.y = (int)(hb[2] | (hb[3] << 16));
+            pk.x = (int)h01;
+            pk.y = (int)h23;
             *reinterpret_cast<v2i*>(stage + row * kRowBytes + phys * 16
                                     + S::half((oc >> 2) & 1, row) * 8) = pk;
         }

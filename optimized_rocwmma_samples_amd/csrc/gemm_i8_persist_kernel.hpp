@@ -82,14 +82,13 @@ __device__ __forceinline__ void epilogue_f16_persist(const KArgs& p, __amdgpu_bu
                 const float4 sb     = sc.sb[j];
                 const int    vv[4]  = {v.x, v.y, v.z, v.w};
                 const float  sbv[4] = {sb.x, sb.y, sb.z, sb.w};
-                uint32_t     h[4];
+                float        f[4];
 #pragma unroll
-                for(int e = 0; e < 4; ++e)
-                    h[e] = float_to_half_bits_2step(((float)vv[e] * sc.sa[i]) * sbv[e]);
+                for(int e = 0; e < 4; ++e) f[e] = ((float)vv[e] * sc.sa[i]) * sbv[e];
                 const int phys = S::chunk(col >> 3, row);
                 v2i       pk;
-                pk.x = (int)(h[0] | (h[1] << 16));
-                pk.y = (int)(h[2] | (h[3] << 16));
+                pk.x = (int)float2_to_half2_bits_2step(f[0], f[1]);
+                pk.y = (int)float2_to_half2_bits_2step(f[2], f[3]);
                 *reinterpret_cast<v2i*>(slice + row * P::kRowBytes + phys * 16
                                         + S::half((col >> 2) & 1, row) * 8) = pk;
             }

@@ -715,10 +715,7 @@ __global__ void __launch_bounds__(256)
     if(vec && c0 + 8 <= n) {
         // two roundings (the fp32 sum, then fp16): the last fma must not fold
         // into a mixed-precision fma that rounds to fp16 once
-        auto pk = [&](int x) {
-            return (uint32_t)float_to_half_bits_2step(acc[x])
-                   | ((uint32_t)float_to_half_bits_2step(acc[x + 1]) << 16);
-        };
+        auto pk = [&](int x) { return float2_to_half2_bits_2step(acc[x], acc[x + 1]); };
         *reinterpret_cast<uint4*>(dst) = make_uint4(pk(0), pk(2), pk(4), pk(6));
     } else {
         for(int x = 0; x < 8; ++x)

@@ -51,7 +51,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t b
 
 __device__ __forceinline__ uint32_t pack_half2(float a, float b)
 {
-    return (uint32_t)float_to_half_bits_2step(a) | ((uint32_t)float_to_half_bits_2step(b) << 16);
+    return float2_to_half2_bits_2step(a, b);
 }
 
 template <int CPL, int WPR, int THREADS, int BPC, bool RES, bool YOUT, bool QUANT>

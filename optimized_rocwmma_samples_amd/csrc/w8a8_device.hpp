@@ -97,6 +97,18 @@ __device__ __forceinline__ uint16_t float_to_half_bits_2step(float f)
     return float_to_half_bits(f);
 }
 
+// Two fp32 results as packed fp16 (a in the low half), each rounded in the
+// same two steps as float_to_half_bits_2step: one v_cvt_pk_f16_f32 on gfx950
+// (round to nearest even, as v_cvt_f16_f32) instead of two conversions and a
+// merge.
+__device__ __forceinline__ uint32_t float2_to_half2_bits_2step(float a, float b)
+{
+    typedef float    f2_t __attribute__((ext_vector_type(2)));
+    typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+    asm("" : "+v"(a), "+v"(b));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2_t{a, b}), h2_t));
+}
+
 // int8 quantization of one smoothed value (reference order: (x*s)*inv, rint,
 // clamp to +-qmax, rocwmma_smoothquant.cpp:110-113).
 __device__ __forceinline__ int quant_i8(float p, float inv, float qmax)
