@@ -54,15 +54,15 @@ struct Persist {
 // pass; every lane issues exactly Persist<C>::kStores 16-byte stores.  The
 // host guarantees N % 8 == 0, ldc % 8 == 0 and a 16-byte aligned C, so an
 // 8-column chunk is either inside the matrix or entirely past it.
-// nt: non-temporal stores, for outputs larger than the MALL (they cannot
+// NT: non-temporal stores, for outputs larger than the MALL (they cannot
 // stay resident, and write-allocating them leaves the MALL full of dirty
 // lines that the next kernel pays to write back: the quantizer that follows
 // the 470 MB gate_up output of cfg3 runs 62 instead of 89 us).
-template <class C>
+template <class C, bool NT>
 __device__ __forceinline__ void epilogue_f16_persist(const KArgs& p, __amdgpu_buffer_rsrc_t rc,
                                                      uint32_t m0, uint32_t n0, int8_t* slice,
                                                      int lane, int wm, int wn, const Acc<C>& acc,
-                                                     const EpiScales<C>& sc, int nt)
+                                                     const EpiScales<C>& sc)
 {
     using P               = Persist<C>;
     using S               = StageSwz<P::kRowChunks>;
@@ -93,19 +93,29 @@ __device__ __forceinline__ void epilogue_f16_persist(const KArgs& p, __amdgpu_bu
                                         + S::half((col >> 2) & 1, row) * 8) = pk;
             }
         }
-        // read back row-contiguous (a wave's LDS accesses complete in order,
-        // so the next pass's writes cannot overtake these reads)
+        // read the pass back row-contiguous, all its reads before its stores;
+        // each 16-byte chunk as its two 8-byte halves, from the positions the
+        // writes put them at (no select to swap them back).  A wave's LDS
+        // accesses complete in order, so the next pass's writes cannot
+        // overtake these reads.
+        v4i out[P::kStPerPass];
 #pragma unroll
         for(int q = 0; q < P::kStPerPass; ++q) {
-            const int      r    = q * P::kRowsPerSt + lane / P::kRowChunks;
-            const int      phys = S::chunk(chunk, r);
-            const v4i      v    = S::unswap(*reinterpret_cast<const v4i*>(slice + r * P::kRowBytes + phys * 16), r);
-            const uint32_t m    = m0 + wm * C::kWaveM + pass * P::kPassRows + r;
-            const uint32_t off  = (m < p.m && n_in) ? (m * p.ldc + n) * 2 : kOob;
-            if(nt)
-                __builtin_amdgcn_raw_buffer_store_b128(v, rc, off, 0, kCpolNonTemporal);
-            else
-                __builtin_amdgcn_raw_buffer_store_b128(v, rc, off, 0, 0);
+            const int     r   = q * P::kRowsPerSt + lane / P::kRowChunks;
+            const int8_t* src = slice + r * P::kRowBytes + S::chunk(chunk, r) * 16;
+            const v2i     lo  = *reinterpret_cast<const v2i*>(src + S::half(0, r) * 8);
+            const v2i     hi  = *reinterpret_cast<const v2i*>(src + S::half(1, r) * 8);
+            out[q]            = v4i{lo.x, lo.y, hi.x, hi.y};
+        }
+        // row mr + q * kRowsPerSt at byte offset off0 + q * step (in range rows
+        // only: the host keeps every element offset of C below 2^31)
+        const uint32_t mr   = m0 + wm * C::kWaveM + pass * P::kPassRows + lane / P::kRowChunks;
+        const uint32_t off0 = (mr * p.ldc + n) * 2;
+        const uint32_t step = P::kRowsPerSt * p.ldc * 2;
+#pragma unroll
+        for(int q = 0; q < P::kStPerPass; ++q) {
+            const uint32_t off = (mr + q * P::kRowsPerSt < p.m && n_in) ? off0 + q * step : kOob;
+            __builtin_amdgcn_raw_buffer_store_b128(out[q], rc, off, 0, NT ? kCpolNonTemporal : 0);
         }
     }
 }
@@ -268,7 +278,10 @@ __global__ void __launch_bounds__(C::kThreads, 1) gemm_i8_persist_kernel(KArgs p
         sc.load(p, m0, n0, wm, wn, elane, vec_ok);
         kstep(nk == 1 && j > 0, std::true_type{});
         __builtin_amdgcn_sched_barrier(0);
-        epilogue_f16_persist<C>(p, rc, m0, n0, slice, elane, wm, wn, acc, sc, nt);
+        if(nt)
+            epilogue_f16_persist<C, true>(p, rc, m0, n0, slice, elane, wm, wn, acc, sc);
+        else
+            epilogue_f16_persist<C, false>(p, rc, m0, n0, slice, elane, wm, wn, acc, sc);
         __builtin_amdgcn_sched_barrier(0);
         // the next k-step (landed at the last barrier, not refilled since)
         fp.first(lds + (step % C::kStages) * C::kStageBytes);
