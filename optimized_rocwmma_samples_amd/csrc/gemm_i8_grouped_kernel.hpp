@@ -352,13 +352,27 @@ __device__ __forceinline__ void epilogue_silu(const KArgs& p, uint32_t m0, uint3
     // accesses in order)
     const int      chunk = lane % kRowChunks;
     const uint32_t o     = oc0 + chunk * 8;
+    constexpr int  kSt   = C::kWaveM / kRowsPerSt; // stores per lane
+    constexpr int  kBat  = kSt < 4 ? kSt : 4;
+    static_assert(kSt % kBat == 0, "whole batches");
 #pragma unroll
-    for(int qq = 0; qq < C::kWaveM / kRowsPerSt; ++qq) {
-        const int      row  = qq * kRowsPerSt + lane / kRowChunks;
-        const int      phys = S::chunk(chunk, row);
-        const v4i      v    = S::unswap(*reinterpret_cast<const v4i*>(stage + row * kRowBytes + phys * 16), row);
-        const uint32_t m    = m0 + wm * C::kWaveM + row;
-        if(m < p.m && o < inter) *reinterpret_cast<v4i*>(h + (size_t)m * ldh + o) = v;
+    for(int q0 = 0; q0 < kSt; q0 += kBat) {
+        // a batch of reads (each chunk as its two 8-byte halves, where the
+        // writes put them) before its stores
+        v4i out[kBat];
+#pragma unroll
+        for(int b = 0; b < kBat; ++b) {
+            const int     row = (q0 + b) * kRowsPerSt + lane / kRowChunks;
+            const int8_t* src = stage + row * kRowBytes + S::chunk(chunk, row) * 16;
+            const v2i     lo  = *reinterpret_cast<const v2i*>(src + S::half(0, row) * 8);
+            const v2i     hi  = *reinterpret_cast<const v2i*>(src + S::half(1, row) * 8);
+            out[b]            = v4i{lo.x, lo.y, hi.x, hi.y};
+        }
+#pragma unroll
+        for(int b = 0; b < kBat; ++b) {
+            const uint32_t m = m0 + wm * C::kWaveM + (q0 + b) * kRowsPerSt + lane / kRowChunks;
+            if(m < p.m && o < inter) *reinterpret_cast<v4i*>(h + (size_t)m * ldh + o) = out[b];
+        }
     }
 }
 

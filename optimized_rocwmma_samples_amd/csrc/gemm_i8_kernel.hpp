@@ -538,8 +538,8 @@ struct EpiScales {
 // rows, one half) over 32 banks = 128 bytes, so the chunk is XOR-swizzled with
 // the row bits above the rows that share a 128-byte window and the half flips
 // with row bit 3: the 32 writes then fill each of the window's 16 8-byte slots
-// twice, with no conflict cycles.  The read-back swaps the halves back on the
-// rows that flipped them.
+// twice, with no conflict cycles.  The read-back reads each chunk as its two
+// halves, each from where it was put.
 template <int kRowChunks>
 struct StageSwz {
     static_assert(kRowChunks == 4 || kRowChunks == 8 || kRowChunks == 16, "row of 4-16 chunks");
@@ -547,10 +547,6 @@ struct StageSwz {
     static constexpr int kShift = kRowChunks == 4 ? 1 : 0; // 64-byte rows: two per window
     __device__ static __forceinline__ int  chunk(int ch, int row) { return ch ^ ((row >> kShift) & (kSwz - 1)); }
     __device__ static __forceinline__ int  half(int h, int row) { return h ^ ((row >> 3) & 1); }
-    __device__ static __forceinline__ v4i  unswap(v4i v, int row)
-    {
-        return ((row >> 3) & 1) ? v4i{v.z, v.w, v.x, v.y} : v;
-    }
 };
 
 template <class C>
@@ -598,21 +594,42 @@ __device__ __forceinline__ void epilogue_f16_lds(const KArgs& p, uint32_t m0, ui
     const bool     st16  = vec_ok && (reinterpret_cast<uintptr_t>(p.c) % 16 == 0) && (p.ldc % 8 == 0);
     const int      chunk = lane % kRowChunks;
     const uint32_t n     = n0 + wn * C::kWaveN + chunk * 8;
+    // a tile wholly inside C with 16-byte rows: every store is a whole chunk
+    const bool     inner = st16 && m0 + C::kBM <= p.m && n0 + C::kBN <= p.n;
+    constexpr int  kSt   = C::kWaveM / kRowsPerSt; // stores per lane
+    constexpr int  kBat  = kSt < 4 ? kSt : 4;
+    static_assert(kSt % kBat == 0, "whole batches");
 #pragma unroll
-    for(int q = 0; q < C::kWaveM / kRowsPerSt; ++q) {
-        const int      row  = q * kRowsPerSt + lane / kRowChunks;
-        const int      phys = S::chunk(chunk, row);
-        const v4i      v    = S::unswap(*reinterpret_cast<const v4i*>(stage + row * kRowBytes + phys * 16), row);
-        const uint32_t m    = m0 + wm * C::kWaveM + row;
-        if(m >= p.m || n >= p.n) continue;
-        uint16_t* dst = reinterpret_cast<uint16_t*>(p.c) + (size_t)m * p.ldc + n;
-        if(st16 && n + 8 <= p.n) {
-            *reinterpret_cast<v4i*>(dst) = v;
-        } else {
-            const uint32_t w[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+    for(int q0 = 0; q0 < kSt; q0 += kBat) {
+        // a batch of reads before its stores; each 16-byte chunk as its two
+        // 8-byte halves, from the positions the writes put them at
+        v4i out[kBat];
 #pragma unroll
-            for(int e = 0; e < 8; ++e)
-                if(n + e < p.n) dst[e] = (uint16_t)(w[e / 2] >> (16 * (e % 2)));
+        for(int b = 0; b < kBat; ++b) {
+            const int     row = (q0 + b) * kRowsPerSt + lane / kRowChunks;
+            const int8_t* src = stage + row * kRowBytes + S::chunk(chunk, row) * 16;
+            const v2i     lo  = *reinterpret_cast<const v2i*>(src + S::half(0, row) * 8);
+            const v2i     hi  = *reinterpret_cast<const v2i*>(src + S::half(1, row) * 8);
+            out[b]            = v4i{lo.x, lo.y, hi.x, hi.y};
+        }
+#pragma unroll
+        for(int b = 0; b < kBat; ++b) {
+            const uint32_t m   = m0 + wm * C::kWaveM + (q0 + b) * kRowsPerSt + lane / kRowChunks;
+            const v4i      v   = out[b];
+            uint16_t*      dst = reinterpret_cast<uint16_t*>(p.c) + (size_t)m * p.ldc + n;
+            if(inner) {
+                *reinterpret_cast<v4i*>(dst) = v;
+                continue;
+            }
+            if(m >= p.m || n >= p.n) continue;
+            if(st16 && n + 8 <= p.n) {
+                *reinterpret_cast<v4i*>(dst) = v;
+            } else {
+                const uint32_t w[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+#pragma unroll
+                for(int e = 0; e < 8; ++e)
+                    if(n + e < p.n) dst[e] = (uint16_t)(w[e / 2] >> (16 * (e % 2)));
+            }
         }
     }
 }
