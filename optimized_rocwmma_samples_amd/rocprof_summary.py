@@ -73,6 +73,7 @@ def trace(directory: str, match: str = "w8a8|gemm|sq_|neg") -> str:
 
 def pmc(directories: list[str], match: str = "w8a8|gemm|sq_|neg") -> str:
     vals = defaultdict(lambda: defaultdict(list))
+    durs = defaultdict(dict)  # dispatch id -> duration (ns), per kernel
     for d in directories:
         for r in _rows(os.path.join(d, "**", "*counter_collection.csv")):
             name = r.get("Kernel_Name", "")
@@ -80,12 +81,46 @@ def pmc(directories: list[str], match: str = "w8a8|gemm|sq_|neg") -> str:
                 continue
             key = (short_name(name), r.get("Grid_Size", "?"))
             vals[key][r["Counter_Name"]].append(float(r["Counter_Value"]))
+            if r.get("Start_Timestamp") and r.get("End_Timestamp"):
+                durs[key][(d, r.get("Dispatch_Id"))] = (int(r["End_Timestamp"])
+                                                        - int(r["Start_Timestamp"]))
     out = []
     for (name, grid), counters in sorted(vals.items()):
         out.append(f"{name} grid={grid}")
+        avg = {c: sum(v) / len(v) for c, v in counters.items()}
         for c, v in sorted(counters.items()):
-            out.append(f"    {c:34s} dispatches={len(v):3d} avg={sum(v) / len(v):.6g}")
+            out.append(f"    {c:34s} dispatches={len(v):3d} avg={avg[c]:.6g}")
+        dur = list(durs[(name, grid)].values())
+        out.extend("    " + line for line in _derived(avg, sum(dur) / len(dur) if dur else 0.0))
     return "\n".join(out)
+
+
+# MI355X: 8 XCDs of 32 CUs, 4 SIMDs per CU.  GRBM_GUI_ACTIVE is summed over
+# the XCDs; SQ_VALU_MFMA_BUSY_CYCLES over the SIMDs.
+XCDS, SIMDS = 8, 1024
+
+
+def _derived(avg: dict, dur_ns: float) -> list[str]:
+    """Metrics derived from one kernel's averaged counters: the MFMA pipes'
+    busy fraction at the clock the kernel ran at, that clock, LDS-active
+    cycles per MFMA-busy cycle and per int8 op, and the int8 rate."""
+    out = []
+    gui = avg.get("GRBM_GUI_ACTIVE")
+    busy = avg.get("SQ_VALU_MFMA_BUSY_CYCLES")
+    lds = avg.get("SQ_LDS_IDX_ACTIVE")
+    mops = avg.get("SQ_INSTS_VALU_MFMA_MOPS_I8")
+    if gui and busy is not None:
+        out.append(f"mfma_util (MFMA_BUSY / (SIMDs x GUI_ACTIVE / XCDs)) = "
+                   f"{busy / (SIMDS * gui / XCDS):.3f}")
+    if gui and dur_ns > 0:
+        out.append(f"clock_MHz (GUI_ACTIVE / XCDs / duration) = {gui / XCDS / dur_ns * 1e3:.0f}")
+    if lds is not None and busy:
+        out.append(f"lds_active_per_mfma_busy_cycle = {lds / busy:.3f}")
+    if lds is not None and mops:
+        out.append(f"lds_active_cycles_per_Mop_int8 = {lds / (mops * 512 / 1e6):.3f}")
+    if mops and dur_ns > 0:
+        out.append(f"int8_TOPS (MOPS_I8 x 512 / duration) = {mops * 512 / dur_ns / 1e3:.0f}")
+    return out
 
 
 CALIB_BYTES = 1 << 30

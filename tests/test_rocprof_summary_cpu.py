@@ -1,0 +1,78 @@
+"""rocprof_summary on small synthetic rocprofv3 CSV files: the kernel-trace
+table, the counter averages with their derived MFMA / LDS metrics, and the
+calibrated traffic lines that bench.py reads."""
+from __future__ import annotations
+
+import csv
+
+import pytest
+
+from optimized_rocwmma_samples_amd import rocprof_summary as R
+
+GEMM = ("void w8a8::gemm::gemm_i8_persist_kernel<w8a8::gemm::Cfg<256, 256, 128, 2, 2, 4, 4, 16> >"
+        "(w8a8::gemm::KArgs, int, int)")
+NEG = "void at::native::vectorized_elementwise_kernel<4, at::native::neg_kernel_cuda>(int)"
+
+
+def _write(path, fields, rows):
+    path.parent.mkdir(parents=True, exist_ok=True)
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=fields)
+        w.writeheader()
+        w.writerows(rows)
+
+
+def _counters(path, kernel, grid, values, t0=1000, dur=100_000):
+    fields = ["Dispatch_Id", "Grid_Size", "Kernel_Name", "Counter_Name", "Counter_Value",
+              "Start_Timestamp", "End_Timestamp"]
+    _write(path, fields, [{"Dispatch_Id": 1, "Grid_Size": grid, "Kernel_Name": kernel,
+                           "Counter_Name": c, "Counter_Value": v, "Start_Timestamp": t0,
+                           "End_Timestamp": t0 + dur} for c, v in values.items()])
+
+
+def test_trace_table_compacts_names_and_averages(tmp_path):
+    fields = ["Kernel_Name", "Grid_Size_X", "Grid_Size_Y", "Grid_Size_Z", "Start_Timestamp",
+              "End_Timestamp"]
+    _write(tmp_path / "t" / "run_kernel_trace.csv", fields,
+           [{"Kernel_Name": GEMM, "Grid_Size_X": 131072, "Grid_Size_Y": 1, "Grid_Size_Z": 1,
+             "Start_Timestamp": 0, "End_Timestamp": d} for d in (300_000, 500_000)])
+    lines = R.trace(str(tmp_path / "t")).splitlines()
+    assert len(lines) == 2
+    assert lines[1].startswith("gemm_i8_persist_kernel<Cfg<256,256,128,2,2,4,4,16> >")
+    cols = lines[1].split()
+    assert cols[-4:] == ["131072", "2", "400.00", "300.00"]
+
+
+def test_pmc_derived_metrics(tmp_path):
+    # 100 us at 2 GHz: GUI_ACTIVE = 8 XCDs x 200000 cycles; MFMA busy half the
+    # SIMD cycles; 1e9 units of 512 int8 ops
+    _counters(tmp_path / "p" / "run_counter_collection.csv", GEMM, 131072,
+              {"GRBM_GUI_ACTIVE": 8 * 200_000, "SQ_VALU_MFMA_BUSY_CYCLES": 1024 * 100_000,
+               "SQ_LDS_IDX_ACTIVE": 5_120_000, "SQ_INSTS_VALU_MFMA_MOPS_I8": 1e9})
+    out = R.pmc([str(tmp_path / "p")])
+    assert "mfma_util (MFMA_BUSY / (SIMDs x GUI_ACTIVE / XCDs)) = 0.500" in out
+    assert "clock_MHz (GUI_ACTIVE / XCDs / duration) = 2000" in out
+    assert "lds_active_per_mfma_busy_cycle = 0.050" in out
+    assert f"lds_active_cycles_per_Mop_int8 = {5_120_000 / 512e3:.3f}" in out
+    assert f"int8_TOPS (MOPS_I8 x 512 / duration) = {1e9 * 512 / 100_000 / 1e3:.0f}" in out
+
+
+def test_traffic_calibrates_on_the_copy(tmp_path):
+    # the copy reads and writes 2^30 bytes; its counters read half / all of it
+    for kind, cal, val in (("fetch", 2**30 / 1024 / 2, 1000.0), ("write", 2**30 / 1024, 250.0)):
+        d = tmp_path / kind
+        name = "FETCH_SIZE" if kind == "fetch" else "WRITE_SIZE"
+        _counters(d / "a" / "run_counter_collection.csv", NEG, 1 << 30, {name: cal})
+        _counters(d / "b" / "run_counter_collection.csv", GEMM, 131072, {name: val})
+    out = R.traffic(str(tmp_path / "fetch"), str(tmp_path / "write")).splitlines()
+    assert out[0].startswith("calibration fetch_factor=2.0000 write_factor=1.0000")
+    line = [l for l in out if "persist" in l][0]
+    assert line.endswith(f"bytes={(1000.0 * 2 + 250.0) * 1024:.0f}")
+
+
+def test_traffic_needs_the_calibration_copy(tmp_path):
+    for kind in ("fetch", "write"):
+        name = "FETCH_SIZE" if kind == "fetch" else "WRITE_SIZE"
+        _counters(tmp_path / kind / "run_counter_collection.csv", GEMM, 131072, {name: 1.0})
+    with pytest.raises(SystemExit):
+        R.traffic(str(tmp_path / "fetch"), str(tmp_path / "write"))
