@@ -58,6 +58,17 @@ def test_row_lengths(w8a8, gpu, n):
     check_exact(qg, rg, *O.smoothquant(x, s))
 
 
+@pytest.mark.parametrize("m,n", [(8192, 4096), (8197, 1000), (12289, 8)])
+def test_many_rows(w8a8, gpu, m, n):
+    # 8192+ rows of at most 4096 columns take the 4 x 256-thread launch per CU
+    # (rows not a multiple of the block's row groups)
+    seed = 400 + m + n
+    x = G.activations(seed, m, n)
+    s = G.uniform(seed, G.TID_S, (n,), 0.5, 2.0)
+    qg, rg = run_sq(w8a8, x, s, gpu)
+    check_exact(qg, rg, *O.smoothquant(x, s))
+
+
 @pytest.mark.parametrize("m", [1, 64, 65])
 @pytest.mark.parametrize("n", [8192, 12288, 16384, 28672])
 def test_decode_row_counts(w8a8, gpu, m, n):
