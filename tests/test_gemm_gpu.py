@@ -329,3 +329,30 @@ def test_config3_fused_projection(w8a8, gpu, name, k, n, m):
         none = torch.empty(0, dtype=torch.uint8, device=gpu)
         c2, _, _ = w8a8.fused_sq_gemm(dev(x, gpu), dev(s, gpu), wd, sbd, workspace=none)
         assert torch.equal(c.view(torch.int16), c2.view(torch.int16)), f"{name} m={m}: split"
+
+
+# Seeded random shapes over every dispatch the library makes (decode-size m,
+# the tile sizes and their K splits with the workspace, the persistent kernel
+# at 2+ tiles per CU, ragged m / n / k), int32 and fp16, against the oracle on
+# the first and last rows and a sample.
+GEMM_FUZZ_SEEDS = [21, 22, 23, 24, 25, 26]
+
+
+@pytest.mark.parametrize("seed", GEMM_FUZZ_SEEDS)
+def test_random_shapes(w8a8, gpu, seed):
+    import torch
+    rng = np.random.default_rng(seed)
+    m = int(rng.choice([1, 7, 64, 65, 300, 512, 1100, 2048, 4100, 8192]))
+    n = int(rng.choice([8, 136, 1000, 2056, 4096, 6144, 9000]))
+    k = int(rng.choice([16, 144, 1024, 2064, 4096, 8192]))
+    a, b, sa, sb = inputs(m, n, k, seed)
+    ws_bytes = w8a8.gemm_workspace_size(m, n, k)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=gpu) if ws_bytes else None
+    da, db = dev(a, gpu), dev(b, gpu)
+    ci = host(w8a8.gemm(da, db, out_dtype=torch.int32, workspace=ws))
+    cf = host(w8a8.gemm(da, db, dev(sa, gpu), dev(sb, gpu), workspace=ws))
+    pick = np.unique(np.concatenate([np.arange(min(m, 4)), np.arange(max(0, m - 4), m),
+                                     rng.integers(0, m, 24)]))
+    acc = O.gemm_i32(a[pick], b)
+    assert_i32_equal(ci[pick], acc)
+    assert_f16_bitexact(cf[pick], O.dequant_f16(acc, sa[pick], sb))

@@ -302,6 +302,52 @@ def test_moe_gemm_many_tiles_exact(w8a8, gpu):
         assert_f16_bitexact(cf[pick], O.dequant_f16(acc, sa[pick], sw[x]))
 
 
+# Seeded random expert layouts: empty experts, rests of a few rows (wide
+# 128 x 512 tiles), rests just above 128, whole tile rows; n not a multiple of
+# the tile; K = 4096 so that a partial last round is cut along K whenever the
+# tail split applies.  int32 and fp16, with and without the workspace, against
+# the oracle on each expert's first and last rows and a sample.
+MOE_FUZZ_SEEDS = [11, 12, 13, 14]
+
+
+@pytest.mark.parametrize("seed", MOE_FUZZ_SEEDS)
+def test_moe_gemm_random_layouts(w8a8, gpu, seed):
+    import torch
+    rng = np.random.default_rng(seed)
+    e = int(rng.integers(2, 10))
+    special = [0, 1, 17, 100, 128, 129, 255, 256, 300, 513, 1024, 1050]
+    counts = [int(rng.choice(special)) if rng.random() < 0.5 else int(rng.integers(0, 1400))
+              for _ in range(e)]
+    n = int(rng.choice([200, 520, 1000, 1536, 2056]))
+    k, unit = 4096, 32
+    count = np.array(counts, np.int32)
+    padded = -(-count // unit) * unit
+    start = np.concatenate([[0], np.cumsum(padded)]).astype(np.int32)
+    rows = max(int(start[-1]), 1)
+    a = G.int8(seed, G.TID_A, (rows, k))
+    w = G.int8(seed, G.TID_B, (e, n, k))
+    sa = G.uniform(seed, G.TID_SA, (rows,), 1e-3, 1e-2)
+    sw = G.uniform(seed, G.TID_SB, (e, n), 1e-3, 1e-2)
+    args = (dev(a, gpu), dev(w, gpu), dev(start[:e], gpu), dev(count, gpu))
+    kw = dict(scale_a=dev(sa, gpu), scale_w=dev(sw, gpu))
+    ws = torch.empty(max(1, w8a8.moe_gemm_workspace_size(e, rows, n, k)), dtype=torch.uint8,
+                     device=gpu)
+    ci = host(w8a8.moe_gemm(*args, out_dtype=torch.int32, workspace=ws))
+    cf = host(w8a8.moe_gemm(*args, workspace=ws, **kw))
+    cf0 = host(w8a8.moe_gemm(*args, workspace=None, **kw))
+    for x in range(e):
+        r0, r1 = int(start[x]), int(start[x]) + counts[x]
+        if r1 == r0:
+            continue
+        assert_f16_bitexact(cf[r0:r1], cf0[r0:r1])
+        pick = np.unique(np.concatenate([np.arange(r0, min(r1, r0 + 8)),
+                                         np.arange(max(r0, r1 - 40), r1),
+                                         np.random.default_rng(x).integers(r0, r1, 16)]))
+        acc = O.gemm_i32(a[pick], w[x])
+        assert_i32_equal(ci[pick], acc)
+        assert_f16_bitexact(cf[pick], O.dequant_f16(acc, sa[pick], sw[x]))
+
+
 def test_moe_gemm_leaves_padding_rows(w8a8, gpu):
     import torch
     t, k, e, h, n, unit = 100, 2, 4, 128, 64, 32
