@@ -348,6 +348,38 @@ def test_moe_gemm_random_layouts(w8a8, gpu, seed):
         assert_f16_bitexact(cf[pick], O.dequant_f16(acc, sa[pick], sw[x]))
 
 
+# More experts than one wave's lanes (the expert lookup scans them in chunks
+# of 64), ~600 rows each so 256-row tiles and wide tiles for the short rests.
+def test_moe_gemm_many_experts(w8a8, gpu):
+    import torch
+    rng = np.random.default_rng(77)
+    e, n, k, unit = 70, 520, 256, 32
+    counts = [int(c) for c in rng.integers(450, 760, e)]
+    counts[3], counts[40], counts[66] = 0, 513, 768
+    count = np.array(counts, np.int32)
+    padded = -(-count // unit) * unit
+    start = np.concatenate([[0], np.cumsum(padded)]).astype(np.int32)
+    rows = int(start[-1])
+    _, bm, wide = _moe_tiles(counts, rows, n)
+    assert bm == 256 and wide > 0
+    seed = 77
+    a = G.int8(seed, G.TID_A, (rows, k))
+    w = G.int8(seed, G.TID_B, (e, n, k))
+    sa = G.uniform(seed, G.TID_SA, (rows,), 1e-3, 1e-2)
+    sw = G.uniform(seed, G.TID_SB, (e, n), 1e-3, 1e-2)
+    args = (dev(a, gpu), dev(w, gpu), dev(start[:e], gpu), dev(count, gpu))
+    ci = host(w8a8.moe_gemm(*args, out_dtype=torch.int32))
+    cf = host(w8a8.moe_gemm(*args, scale_a=dev(sa, gpu), scale_w=dev(sw, gpu)))
+    for x in range(e):
+        r0, r1 = int(start[x]), int(start[x]) + counts[x]
+        if r1 == r0:
+            continue
+        pick = np.unique(np.concatenate([[r0, r1 - 1], np.random.default_rng(x).integers(r0, r1, 6)]))
+        acc = O.gemm_i32(a[pick], w[x])
+        assert_i32_equal(ci[pick], acc)
+        assert_f16_bitexact(cf[pick], O.dequant_f16(acc, sa[pick], sw[x]))
+
+
 def test_moe_gemm_leaves_padding_rows(w8a8, gpu):
     import torch
     t, k, e, h, n, unit = 100, 2, 4, 128, 64, 32
