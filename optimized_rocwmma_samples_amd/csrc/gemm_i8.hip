@@ -50,6 +50,10 @@ using DecMidW    = gemm::DecCfg<2, 2, 8, 2>; // packed, 32 < m <= 64, many slabs
 // packed, 32 < m <= 64 with a split-K workspace: 8 half slabs per block share
 // the A k-tile through LDS
 using DecWide    = gemm::DecWideCfg<8, 3>;
+// 4 waves of 32 weight rows: when 128-row panels give 3/4 to one round of
+// blocks, they run unsplit (no partials, no reduce launch) where 256-row
+// panels would need a K split: M = 64, W [28672, 8192] 55-56 -> 49 us.
+using DecWide4   = gemm::DecWideCfg<4, 4>;
 // A packed GEMM with at least this many 64-row slabs has enough blocks at
 // 64 rows per block to fill the chip; fewer slabs run 32 rows per block.
 constexpr uint32_t kWideSlabs = 384;
@@ -337,6 +341,13 @@ hipError_t launch_gemm_decode(const GemmArgs& g, bool packed, void* ws, size_t w
         if(packed && decode_wide_shape(g) && ws != nullptr) {
             // the workspace holds every panel's partials (panels run in stream order)
             const uint32_t splits = decode_wide_splits(g, p.n);
+            const uint32_t nb4    = (p.n + DecWide4::kRows - 1) / DecWide4::kRows;
+            if(splits > 1 && (uint64_t)nb4 * 4 >= (uint64_t)device_cus() * 3
+               && nb4 <= device_cus()) {
+                e = gemm::launch_decode_wide<DecWide4>(p, g.out_type, vec_ok, nullptr, 1, stream);
+                if(e != hipSuccess) return e;
+                continue;
+            }
             if(gemm::decode_ws_bytes(g.m, p.n, splits) <= ws_bytes) {
                 e = gemm::launch_decode_wide<DecWide>(p, g.out_type, vec_ok,
                                                       static_cast<int32_t*>(ws), splits, stream);

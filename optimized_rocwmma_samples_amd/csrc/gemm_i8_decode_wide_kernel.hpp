@@ -9,7 +9,7 @@
 //   * a block covers WV*32 weight rows (each wave a 32-row half slab of the
 //     packed layout, streamed into a RING-deep register ring), and its waves
 //     share each 64 x 128 A k-tile, loaded once per block into an LDS ring by
-//     global_load_lds (one 1 KiB wave-load per wave per k-tile) and read back
+//     LDS-DMA buffer loads (8 KiB per k-tile in 1 KiB wave-loads over the waves) and read back
 //     as MFMA fragments (16-byte chunks XOR-swizzled by row: conflict-free);
 //   * blockIdx.y splits K; each split writes its int32 partial tile to the
 //     workspace [split][M][ldw] with plain stores, and decode_reduce_kernel
@@ -34,9 +34,11 @@ struct DecWideCfg {
     static constexpr int kRows       = kWaves * 32;      // weight rows per block
     static constexpr int kAStage     = kMT * 32 * kPackK; // 8 KiB
     static constexpr int kLdsBytes   = kRing * kAStage;
-    static constexpr int kOpsPerTile = 4 + kAStage / 1024 / kWaves; // W frags + A wave-loads
+    static constexpr int kALoads     = kAStage / 1024 / kWaves; // A wave-loads per wave
+    static constexpr int kOpsPerTile = 4 + kALoads;              // W frags + A wave-loads
     static_assert(kWaves % 2 == 0, "whole 64-row slabs per block");
-    static_assert(kAStage / 1024 % kWaves == 0, "A k-tile splits into one wave-load per wave");
+    static_assert(kALoads >= 1 && kAStage / 1024 % kWaves == 0,
+                  "A k-tile splits into whole wave-loads per wave");
     static_assert(kRing >= 2 && kRing <= 4, "ring depth");
     static_assert(kOpsPerTile * (kRing - 1) < 64, "vmcnt range");
 };
@@ -67,14 +69,19 @@ __global__ void __launch_bounds__(C::kThreads) gemm_i8_decode_wide_kernel(KArgs 
     const uint32_t vb = nbase < p.n ? (nbase / kSlab) * nkt * (kPackFrags * 1024)
                                           + ((nbase % kSlab) / 32) * 4096 + lane * 16
                                     : kOob;
-    // A k-tile -> LDS: wave w fills rows 8w .. 8w+7, lane l writes physical
-    // chunk l%8 of row 8w + l/8, i.e. fetches logical chunk (l%8) ^ swz(row)
+    // A k-tile -> LDS: wave-load j (= wave * kALoads + i) fills rows 8j ..
+    // 8j+7, lane l writes physical chunk l%8 of row 8j + l/8, i.e. fetches
+    // logical chunk (l%8) ^ swz(row)
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<int8_t*>(p.a), 0, (int)((p.m - 1) * p.lda + p.k), kBufferFlags);
-    const uint32_t arow   = wave * 8 + lane / 8;
-    const uint32_t achunk = (lane % 8) ^ ((arow >> 1) & 7);
-    const uint32_t va     = arow < p.m ? arow * p.lda + achunk * 16 : kOob;
-    const uint32_t lds0   = (uint32_t)(uintptr_t)lds;
+    uint32_t achunk[C::kALoads], va[C::kALoads];
+#pragma unroll
+    for(int i = 0; i < C::kALoads; ++i) {
+        const uint32_t arow = (wave * C::kALoads + i) * 8 + lane / 8;
+        achunk[i]           = (lane % 8) ^ ((arow >> 1) & 7);
+        va[i]               = arow < p.m ? arow * p.lda + achunk[i] * 16 : kOob;
+    }
+    const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
 
     using WTile = v4i[4];
     WTile bq[C::kRing];
@@ -87,10 +94,14 @@ __global__ void __launch_bounds__(C::kThreads) gemm_i8_decode_wide_kernel(KArgs 
 #pragma unroll
         for(int g = 0; g < 4; ++g)
             bq[slot][g] = __builtin_amdgcn_raw_buffer_load_b128(rb, vbb, kofs + g * 1024, 0);
-        const uint32_t kk = kt * kPackK + achunk * 16;
-        const uint32_t v  = (live && va != kOob && kk < p.k) ? va + kt * kPackK : kOob;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            ra, (lds_void_t*)(uintptr_t)(lds0 + slot * C::kAStage + wave * 1024), 16, v, 0, 0, 0);
+#pragma unroll
+        for(int i = 0; i < C::kALoads; ++i) {
+            const uint32_t kk = kt * kPackK + achunk[i] * 16;
+            const uint32_t v  = (live && va[i] != kOob && kk < p.k) ? va[i] + kt * kPackK : kOob;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ra, (lds_void_t*)(uintptr_t)(lds0 + slot * C::kAStage + (wave * C::kALoads + i) * 1024),
+                16, v, 0, 0, 0);
+        }
     };
 
     v16i acc[C::kMT];

@@ -218,9 +218,12 @@ def test_config4_fused_decode(w8a8, gpu, config4_weights, m):
 
 # 32 < m <= 64 over packed weights with a workspace: the wide decode kernel
 # (A k-tile shared through LDS, K split across blocks, int32 partials summed by
-# a second kernel).  Every result must equal the unsplit kernel's bit for bit.
+# a second kernel), or, where 128-row panels fill 3/4 to one round of the CUs
+# and 256-row panels would need the split, its 4-wave form unsplit (the last
+# three shapes).  Every result must equal the unsplit kernel's bit for bit.
 WIDE_SHAPES = [(64, 4096, 4096), (33, 1000, 4112), (48, 300, 2048), (64, 70, 8192),
-               (40, 28672, 1024), (64, 8192, 14336), (57, 513, 256)]
+               (40, 28672, 1024), (64, 8192, 14336), (57, 513, 256),
+               (64, 28672, 2048), (57, 25000, 4112), (33, 32768, 2048)]
 
 
 @pytest.mark.parametrize("m,n,k", WIDE_SHAPES)
