@@ -50,9 +50,9 @@ using DecMidW    = gemm::DecCfg<2, 2, 8, 2>; // packed, 32 < m <= 64, many slabs
 // packed, 32 < m <= 64 with a split-K workspace: 8 half slabs per block share
 // the A k-tile through LDS
 using DecWide    = gemm::DecWideCfg<8, 3>;
-// 4 waves of 32 weight rows: when 128-row panels give 3/4 to one round of
-// blocks, they run unsplit (no partials, no reduce launch) where 256-row
-// panels would need a K split: M = 64, W [28672, 8192] 55-56 -> 49 us.
+// 4 waves of 32 weight rows: twice the blocks of DecWide, so half its K
+// splits for the same fill (fewer partials; none where DecWide needs 2):
+// M = 64, W [28672, 8192] 55.5 -> 49.9 us, W [8192, 28672] 59.0 -> 56.3 us.
 using DecWide4   = gemm::DecWideCfg<4, 4>;
 // A packed GEMM with at least this many 64-row slabs has enough blocks at
 // 64 rows per block to fill the chip; fewer slabs run 32 rows per block.
@@ -341,10 +341,14 @@ hipError_t launch_gemm_decode(const GemmArgs& g, bool packed, void* ws, size_t w
         if(packed && decode_wide_shape(g) && ws != nullptr) {
             // the workspace holds every panel's partials (panels run in stream order)
             const uint32_t splits = decode_wide_splits(g, p.n);
-            const uint32_t nb4    = (p.n + DecWide4::kRows - 1) / DecWide4::kRows;
-            if(splits > 1 && (uint64_t)nb4 * 4 >= (uint64_t)device_cus() * 3
-               && nb4 <= device_cus()) {
-                e = gemm::launch_decode_wide<DecWide4>(p, g.out_type, vec_ok, nullptr, 1, stream);
+            // the 4-wave form: twice the blocks, so half the splits for the
+            // same fill (1 = unsplit, no reduce launch)
+            const uint64_t b4 = (uint64_t)(p.n + DecWide4::kRows - 1) / DecWide4::kRows * (splits / 2);
+            if(splits % 2 == 0 && b4 * 4 >= (uint64_t)device_cus() * 3 && b4 <= device_cus()
+               && gemm::decode_ws_bytes(g.m, p.n, splits / 2) <= ws_bytes) {
+                e = gemm::launch_decode_wide<DecWide4>(p, g.out_type, vec_ok,
+                                                       static_cast<int32_t*>(ws), splits / 2,
+                                                       stream);
                 if(e != hipSuccess) return e;
                 continue;
             }
