@@ -415,10 +415,11 @@ hipError_t dispatch(const QuantRows& p, hipStream_t stream)
             if(n <= 512) return launch_stream<1, 1, 512>(p, stream);
             if(n <= 1024) return launch_stream<2, 1, 512>(p, stream);
             if(n <= 2048) return launch_stream<4, 1, 512>(p, stream);
-            // 8192+ rows: 4 blocks of 256 threads per CU keep more rows in
-            // flight (8192 x 4096 cold: 21.8 -> 20.9 us; at 2048 rows the
-            // single 512-thread block stays ahead)
-            if(n <= 4096 && p.rows >= 8192) return launch_stream<4, 2, 256, 4>(p, stream);
+            // 8192 to 32767 rows: 4 blocks of 256 threads per CU keep more
+            // rows in flight (8192 x 4096 cold: 21.8 -> 20.9 us); at 2048
+            // rows, and from 32768 rows on (131072 x 4096: 312 -> 293 us),
+            // the single 512-thread block stays ahead
+            if(n <= 4096 && p.rows >= 8192 && p.rows < 32768) return launch_stream<4, 2, 256, 4>(p, stream);
             if(n <= 4096) return launch_stream<4, 2, 512>(p, stream);
             if(n <= 8192) return launch_stream<4, 4, 512, 2>(p, stream);
             // one row group of 8 waves per block (4 chunks per lane) rather
