@@ -58,10 +58,12 @@ def test_row_lengths(w8a8, gpu, n):
     check_exact(qg, rg, *O.smoothquant(x, s))
 
 
-@pytest.mark.parametrize("m,n", [(8192, 4096), (8197, 1000), (12289, 8)])
+@pytest.mark.parametrize("m,n", [(8192, 4096), (8197, 1000), (12289, 8), (32767, 2056),
+                                 (32768, 2056)])
 def test_many_rows(w8a8, gpu, m, n):
-    # 8192+ rows of at most 4096 columns take the 4 x 256-thread launch per CU
-    # (rows not a multiple of the block's row groups)
+    # 8192 to 32767 rows of 2049-4096 columns take the 4 x 256-thread launch
+    # per CU, 32768 rows the single 512-thread block again (rows not a
+    # multiple of the block's row groups)
     seed = 400 + m + n
     x = G.activations(seed, m, n)
     s = G.uniform(seed, G.TID_S, (n,), 0.5, 2.0)
