@@ -296,28 +296,46 @@ def profiled_traffic(projs, cus):
     `achieved`, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
     of a bench run without the extras (scaled by the calibration copy).  The
     persistent kernel launches one block per CU for every projection it runs,
-    so its row is the average over those launches; tile-kernel rows are keyed
-    by their grid.  None when the profile does not cover these launches."""
+    so its launches share one (kernel, grid) row; where the profile also
+    lists that kernel's dispatches by position in the step's launch order
+    (`pos=<i>/<n>` lines, one per persistent projection), each projection
+    gets its own, else the row's average.  Tile-kernel rows are keyed by
+    their grid.  Returns (average, per projection, per-projection persistent
+    entries by launch order?); None, None, False when the profile does not
+    cover these launches."""
     import re
     if not TRAFFIC_PROFILE.exists():
-        return None, None
-    table, on = {}, False
+        return None, None, False
+    table, pos, on = {}, {}, False
     for line in TRAFFIC_PROFILE.read_text().splitlines():
         if line.startswith("## "):
             on = line.startswith(TRAFFIC_SECTION)
             continue
+        if not on:
+            continue
+        mp = re.match(r"traffic \S*gemm_i8_persist_kernel<\S*Cfg<256,256,\S* grid=(\d+) "
+                      r"pos=(\d+)/(\d+) .* bytes=(\d+)", line)
+        if mp:
+            pos[(int(mp.group(1)), int(mp.group(2)), int(mp.group(3)))] = int(mp.group(4))
+            continue
         mt = re.match(r"traffic \S*gemm_i8_(tile|persist)_kernel<\S*Cfg<256,256,\S* grid=(\d+) .* bytes=(\d+)",
                       line)
-        if on and mt:
+        if mt:
             table[(mt.group(1), int(mt.group(2)))] = int(mt.group(3))
-    per = []
-    for p in projs:
-        kind = projection_kernel(p, cus)
+    kinds = [projection_kernel(p, cus) for p in projs]
+    npersist = kinds.count("persist")
+    by_order = npersist > 1 and all((cus * 512, i, npersist) in pos for i in range(npersist))
+    per, ip = [], 0
+    for p, kind in zip(projs, kinds):
         grid = cus * 512 if kind == "persist" else -(-p["m"] // 256) * -(-p["n"] // 256) * 512
         if (kind, grid) not in table:
-            return None, None
-        per.append(table[(kind, grid)])
-    return sum(per) / len(per), per
+            return None, None, False
+        if kind == "persist" and by_order:
+            per.append(pos[(grid, ip, npersist)])
+            ip += 1
+        else:
+            per.append(table[(kind, grid)])
+    return sum(per) / len(per), per, by_order
 
 
 def bench_cfg3_smaller_m(torch, w8a8, dev, base, steps=10, sets=3):
@@ -708,7 +726,7 @@ def main(argv=None) -> int:
     log(json.dumps(per_proj))
 
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
-    traffic, traffic_per = profiled_traffic(projs, cus)
+    traffic, traffic_per, traffic_by_order = profiled_traffic(projs, cus)
     kinds = [projection_kernel(p, cus) for p in projs]
     algo_bytes = [p["m"] * p["k"] + p["n"] * p["k"] + 2 * p["m"] * p["n"] + 4 * (p["m"] + p["n"])
                   for p in projs]
@@ -722,8 +740,11 @@ def main(argv=None) -> int:
                 "kernel": " + ".join(
                     f"{'gemm_i8_persist_kernel<Cfg<256,256,128,2,2,4,4,16>>' if kd == 'persist' else 'gemm_i8_tile_kernel<Cfg<256,256,128,2,2,4,4,16>, F16>'} ({', '.join(nm for (nm, _, _), k2 in zip(LLAMA3_8B, kinds) if k2 == kd)})"
                     for kd in dict.fromkeys(kinds)),
-                "traffic_note": "per-projection entries of the persistent kernel are its average "
-                                "over the projections it runs (one block per CU each)",
+                "traffic_note": ("per-projection entries of the persistent kernel from its "
+                                 "dispatches by position in each step's launch order (qkv, "
+                                 "o_proj, gate_up)" if traffic_by_order else
+                                 "per-projection entries of the persistent kernel are its average "
+                                 "over the projections it runs (one block per CU each)"),
                 "avg_launch_us": gemm_avg_us,
                 "avg_launch_us_per_kernel": {
                     kd: sum(g for g, k2 in zip(g_ms, kinds) if k2 == kd) * 1e3

@@ -2,7 +2,7 @@
 
     python -m optimized_rocwmma_samples_amd.rocprof_summary trace DIR        # kernel trace
     python -m optimized_rocwmma_samples_amd.rocprof_summary pmc DIR [DIR..]  # counters
-    python -m optimized_rocwmma_samples_amd.rocprof_summary traffic FETCH_DIR WRITE_DIR
+    python -m optimized_rocwmma_samples_amd.rocprof_summary traffic FETCH_DIR WRITE_DIR [CYCLE [REGEX]]
 
 `traffic` turns FETCH_SIZE and WRITE_SIZE (KiB per dispatch, one run each) into
 bytes per dispatch, scaled by what the same counters read for the calibration
@@ -11,7 +11,12 @@ bytes read, 2^30 bytes written).  Output lines:
     traffic <kernel> grid=<g> fetch_kib=<f> write_kib=<w> bytes=<scaled total>
 
 Groups dispatches by (kernel, grid size) so the four projection GEMMs of one
-bench step appear as separate rows, and prints per-dispatch averages.
+bench step appear as separate rows, and prints per-dispatch averages.  With
+CYCLE (> 1), kernels matching REGEX (default "persist") whose dispatches of
+one grid come in a repeating order of CYCLE launches (the persistent GEMM runs
+qkv, o_proj, gate_up in every bench step, all with one block per CU) also get
+one line per position in that order, from the dispatches in Dispatch_Id order:
+    traffic <kernel> grid=<g> pos=<i>/<CYCLE> fetch_kib=<f> write_kib=<w> bytes=<b>
 """
 from __future__ import annotations
 
@@ -137,7 +142,19 @@ def _counter_avgs(directory: str, counter: str):
     return {k: sum(v) / len(v) for k, v in vals.items()}
 
 
-def traffic(fetch_dir: str, write_dir: str, match: str = "w8a8|gemm|sq_") -> str:
+def _counter_seqs(directory: str, counter: str):
+    """Per (kernel, grid): the counter's values in Dispatch_Id order."""
+    vals = defaultdict(list)
+    for r in _rows(os.path.join(directory, "**", "*counter_collection.csv")):
+        if r["Counter_Name"] != counter:
+            continue
+        key = (short_name(r.get("Kernel_Name", "")), r.get("Grid_Size", "?"))
+        vals[key].append((int(r.get("Dispatch_Id", 0)), float(r["Counter_Value"])))
+    return {k: [v for _, v in sorted(d)] for k, d in vals.items()}
+
+
+def traffic(fetch_dir: str, write_dir: str, match: str = "w8a8|gemm|sq_", cycle: int = 0,
+            cycle_match: str = "persist") -> str:
     fetch = _counter_avgs(fetch_dir, "FETCH_SIZE")
     write = _counter_avgs(write_dir, "WRITE_SIZE")
 
@@ -160,6 +177,19 @@ def traffic(fetch_dir: str, write_dir: str, match: str = "w8a8|gemm|sq_") -> str
         total = (f * ff + w * wf) * 1024
         out.append(f"traffic {name.replace(' ', '')} grid={grid} fetch_kib={f:.1f} "
                    f"write_kib={w:.1f} bytes={total:.0f}")
+    if cycle > 1:
+        fseq, wseq = _counter_seqs(fetch_dir, "FETCH_SIZE"), _counter_seqs(write_dir, "WRITE_SIZE")
+        for (name, grid), fs in sorted(fseq.items()):
+            ws = wseq.get((name, grid), [])
+            # each run is whole steps of its own (the two runs' step counts
+            # may differ: the bench settles the clocks for a fixed time)
+            if not re.search(cycle_match, name) or not ws or len(fs) % cycle or len(ws) % cycle:
+                continue
+            for i in range(cycle):
+                f = sum(fs[i::cycle]) / len(fs[i::cycle])
+                w = sum(ws[i::cycle]) / len(ws[i::cycle])
+                out.append(f"traffic {name.replace(' ', '')} grid={grid} pos={i}/{cycle} "
+                           f"fetch_kib={f:.1f} write_kib={w:.1f} bytes={(f * ff + w * wf) * 1024:.0f}")
     return "\n".join(out)
 
 
@@ -172,10 +202,13 @@ def main(argv: list[str]) -> int:
     elif argv[0] == "pmc":
         print(pmc(argv[1:]))
     else:
-        if len(argv) != 3:
+        if len(argv) not in (3, 4, 5):
             print(__doc__)
             return 2
-        print(traffic(argv[1], argv[2]))
+        extra = {"cycle": int(argv[3])} if len(argv) > 3 else {}
+        if len(argv) > 4:
+            extra["cycle_match"] = argv[4]
+        print(traffic(argv[1], argv[2], **extra))
     return 0
 
 

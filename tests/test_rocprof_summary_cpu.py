@@ -76,3 +76,44 @@ def test_traffic_needs_the_calibration_copy(tmp_path):
         _counters(tmp_path / kind / "run_counter_collection.csv", GEMM, 131072, {name: 1.0})
     with pytest.raises(SystemExit):
         R.traffic(str(tmp_path / "fetch"), str(tmp_path / "write"))
+
+
+def test_traffic_by_dispatch_order(tmp_path):
+    # three launches of one kernel and grid per step, two steps: one line per
+    # position of the cycle, from the dispatches in Dispatch_Id order
+    fields = ["Dispatch_Id", "Grid_Size", "Kernel_Name", "Counter_Name", "Counter_Value"]
+    for kind, name, cal, vals in (("fetch", "FETCH_SIZE", 2**30 / 1024 / 2, (10., 20., 30.)),
+                                  ("write", "WRITE_SIZE", 2**30 / 1024, (1., 2., 3.))):
+        rows = [{"Dispatch_Id": 1, "Grid_Size": 1 << 30, "Kernel_Name": NEG, "Counter_Name": name,
+                 "Counter_Value": cal}]
+        # written out of order: the summary sorts by Dispatch_Id
+        for d in (7, 2, 5, 3, 6, 4):
+            rows.append({"Dispatch_Id": d, "Grid_Size": 131072, "Kernel_Name": GEMM,
+                         "Counter_Name": name, "Counter_Value": vals[(d - 2) % 3] + (d >= 5)})
+        _write(tmp_path / kind / "run_counter_collection.csv", fields, rows)
+    out = R.traffic(str(tmp_path / "fetch"), str(tmp_path / "write"), cycle=3).splitlines()
+    pos = [l for l in out if " pos=" in l]
+    assert [l.split(" pos=")[1].split()[0] for l in pos] == ["0/3", "1/3", "2/3"]
+    for i, l in enumerate(pos):
+        f, w = (10. + 10 * i) + 0.5, (1. + i) + 0.5
+        assert f"fetch_kib={f:.1f} write_kib={w:.1f} bytes={(f * 2 + w) * 1024:.0f}" in l
+    # without a cycle, or for kernels the cycle pattern does not match: no pos lines
+    assert not [l for l in R.traffic(str(tmp_path / "fetch"), str(tmp_path / "write")).splitlines()
+                if " pos=" in l]
+    assert not [l for l in R.traffic(str(tmp_path / "fetch"), str(tmp_path / "write"), cycle=3,
+                                     cycle_match="tile").splitlines() if " pos=" in l]
+
+
+def test_bench_reads_per_projection_traffic_from_the_profile():
+    # the committed cfg3 profile lists the persistent kernel's dispatches by
+    # launch position: qkv, o_proj and gate_up get their own traffic (their
+    # algorithmic bytes differ by 5x), down its tile-kernel row
+    import sys
+    from pathlib import Path
+    sys.path.insert(0, str(Path(__file__).resolve().parents[1]))
+    import bench
+    projs = [dict(m=8192, k=k, n=n) for _, k, n in bench.LLAMA3_8B]
+    avg, per, by_order = bench.profiled_traffic(projs, 256)
+    assert by_order and len(per) == 4
+    assert per[2] > per[0] > per[1] > 0  # gate_up > qkv > o_proj
+    assert avg == pytest.approx(sum(per) / 4)
