@@ -96,6 +96,87 @@ def cpu_baseline(projs, rows: int):
     }
 
 
+def _oracle_libs():
+    """The CPU checkers (oracle port; the reference's gemm_cpu_h when
+    oracle/_ref was built) and the OpenMP thread count they run on."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib as O
+
+    return O, O.ref() is not None, int(O.oracle().w8a8o_num_threads())
+
+
+def cpu_baseline_quantizer(x, s, nbytes, budget_s=3.0):
+    """cfg1 on the host: the oracle quantizer (port of
+    rocwmma_smoothquant.cpp:74-121) over the whole cfg1 problem, repeated for
+    about budget_s seconds; GB/s over the same algorithmic bytes as the GPU
+    launch."""
+    O, _, threads = _oracle_libs()
+    O.smoothquant(x, s)  # first-touch of the outputs, thread pool start
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        O.smoothquant(x, s)
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= budget_s:
+            break
+    return {"value": nbytes * reps / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"the whole cfg1 problem (X fp16 [{x.shape[0]}, {x.shape[1]}]), {reps} "
+                      f"runs of the oracle quantizer in {dt:.1f} s"}
+
+
+def cpu_baseline_decode(layers, m=16):
+    """cfg4 on the host at M = 16 (the reference's gemm_cpu_h parallelizes over
+    rows: one thread per row): SmoothQuant of the activations (oracle port),
+    gemm_cpu_h over the whole weight matrix, dequant, for each Llama-70B MLP
+    weight; GB/s over the same algorithmic bytes as the GPU layers."""
+    O, use_ref, threads = _oracle_libs()
+    nbytes, t0 = 0, time.perf_counter()
+    for x, s, w, sb in layers:
+        n, k = w.shape
+        q, r = O.smoothquant(x[:m], s)
+        acc = O.ref_gemm_cpu_i8(q, w) if use_ref else O.gemm_i32(q, w)
+        O.dequant_f16(acc, r, sb)
+        nbytes += n * k + 4 * n + 2 * m * k + 4 * k + 2 * (m * k + 4 * m) + 2 * m * n
+    dt = time.perf_counter() - t0
+    return {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": min(threads, m),
+            "kind": "reference" if use_ref else "port",
+            "sample": f"M = {m}, both weights W1 [28672, 8192] and W2 [8192, 28672] whole: "
+                      f"SmoothQuant (oracle port) + gemm_cpu_h "
+                      f"({'reference common.hpp' if use_ref else 'oracle port'}) + dequant, "
+                      f"{nbytes / 1e9:.2f} GB of layer bytes in {dt:.1f} s"}
+
+
+def cpu_baseline_moe(x, logits, s, wgu, sgu, wd, sd, topk, rows_per_expert=16):
+    """cfg5 on the host: routing, sort and the MoE quantizer over all 4096
+    tokens (oracle port), then for the first `rows_per_expert` sorted rows of
+    every expert the gate_up GEMM (gemm_cpu_h), dequant, SiLU(gate)*up
+    requant (oracle), down GEMM and dequant; TOPS over those rows' GEMM ops."""
+    O, use_ref, threads = _oracle_libs()
+    gemm = O.ref_gemm_cpu_i8 if use_ref else O.gemm_i32
+    e = s.shape[0]
+    t0 = time.perf_counter()
+    w, ids = O.topk_softmax(logits, topk)
+    count, start, padded, sorted_ids, dst = O.moe_sort(ids, e, 32)
+    qa, ra = O.moe_smoothquant(x, s, ids, dst_row=dst, rows=sorted_ids.size)
+    ops = 0.0
+    for xe in range(e):
+        r0 = int(start[xe])
+        r1 = r0 + min(rows_per_expert, int(count[xe]))
+        if r1 == r0:
+            continue
+        gu = O.dequant_f16(gemm(qa[r0:r1], wgu[xe]), ra[r0:r1], sgu[xe])
+        q2, r2 = O.silu_mul_quant(gu)
+        O.dequant_f16(gemm(q2, wd[xe]), r2, sd[xe])
+        ops += 2.0 * (r1 - r0) * (wgu.shape[1] * wgu.shape[2] + wd.shape[1] * wd.shape[2])
+    dt = time.perf_counter() - t0
+    return {"value": ops / dt / 1e12, "unit": "TOPS", "cores": min(threads, rows_per_expert),
+            "kind": "reference" if use_ref else "port",
+            "sample": f"routing + sort + MoE quantizer over all {x.shape[0]} tokens, then "
+                      f"{rows_per_expert} sorted rows of each of the {e} experts through gate_up "
+                      f"gemm_cpu_h ({'reference common.hpp' if use_ref else 'oracle port'}) + "
+                      f"SiLU requant + down: {ops / 1e9:.1f} GOP in {dt:.1f} s"}
+
+
 def graph_us(torch, calls, repeat=1):
     """Per-call GPU time of `calls` (a list of closures that enqueue work on
     torch's current stream): captured once into a HIP graph on a side stream,
@@ -137,10 +218,11 @@ def quantizer_sets(torch, dev, gen, m, n, nsets):
     return sets
 
 
-def bench_quantizer(torch, w8a8, dev, gen, iters=48):
+def bench_quantizer(torch, w8a8, dev, gen, iters=48, cpu=True):
     """Config 1: X fp16 [2048, 4096].  Cold: 24 buffer sets (600 MB, over the
     256 MB MALL) used in turn, so every launch reads HBM; warm: one set
-    relaunched, as the reference measures (inputs MALL-resident)."""
+    relaunched, as the reference measures (inputs MALL-resident).  cpu: the
+    oracle quantizer timed on the host over the first set."""
     m, n = 2048, 4096
     sets = quantizer_sets(torch, dev, gen, m, n, 24)
     calls = [(lambda b=sets[i % len(sets)]: w8a8.smoothquant(b[0], b[1], out=b[2], row_scale=b[3]))
@@ -154,7 +236,10 @@ def bench_quantizer(torch, w8a8, dev, gen, iters=48):
             "frac_hbm": nbytes / (cold * 1e-6) / PEAK_HBM_BPS,
             "warm_us_per_launch": warm, "warm_GBps": nbytes / (warm * 1e-6) / 1e9,
             "note": "cold = 24 rotating buffer sets (every launch reads HBM); warm = one set, "
-                    "MALL-resident like the reference's repeated launches"}
+                    "MALL-resident like the reference's repeated launches",
+            "cpu_baseline": (cpu_baseline_quantizer(sets[0][0].cpu().numpy(),
+                                                    sets[0][1].cpu().numpy(), nbytes)
+                             if cpu else None)}
 
 
 def bench_quantizer_sweep(torch, w8a8, dev, gen):
@@ -232,21 +317,24 @@ def bench_gemm_4096(torch, w8a8, dev, gen, iters=20):
             "TOPS": tops, "frac_mfma": tops * 1e12 / PEAK_INT8_OPS}
 
 
-def bench_decode(torch, w8a8, dev, gen, iters=20):
+def bench_decode(torch, w8a8, dev, gen, iters=20, cpu=True):
     """Config 4: fused SmoothQuant + packed-weight decode GEMM, Llama-70B MLP
     weights W1 [28672, 8192] and W2 [8192, 28672] at M in {1, 16, 64}.  Two
     copies of each weight (2 x 235 MB per shape, over the 256 MB MALL) are
     used in turn, so a launch does not find its weights in MALL."""
     shapes = [(28672, 8192), (8192, 28672)]
-    weights = {}
+    weights, host_w = {}, {}
     for n, k in shapes:
         copies = []
-        for _ in range(2):
+        for c in range(2):
             w = torch.randint(-127, 128, (n, k), generator=gen, device=dev, dtype=torch.int8)
             copies.append(w8a8.pack_weights(w))
+            if cpu and c == 0:
+                host_w[(n, k)] = w.cpu().numpy()
             del w
         sb = torch.rand(n, generator=gen, device=dev) * 9e-3 + 1e-3
         weights[(n, k)] = (copies, sb)
+    cpu_layers = []
     results = []
     for m in (1, 16, 64):
         bufs = {}
@@ -259,6 +347,9 @@ def bench_decode(torch, w8a8, dev, gen, iters=20):
         for (n, k) in shapes:
             x, s, q, r, out = bufs[(n, k)]
             copies, sb = weights[(n, k)]
+            if cpu and m == 16:
+                cpu_layers.append((x.cpu().numpy(), s.cpu().numpy(), host_w[(n, k)],
+                                   sb.cpu().numpy()))
             # split-K workspace (M = 64 takes one), allocated once
             wsz = w8a8.gemm_packed_workspace_size(m, n, k)
             ws = torch.empty(wsz, dtype=torch.uint8, device=dev) if wsz else None
@@ -275,7 +366,8 @@ def bench_decode(torch, w8a8, dev, gen, iters=20):
                             "frac_hbm": nbytes / (us * 1e-6) / PEAK_HBM_BPS,
                             "TOPS": 2.0 * m * n * k / (us * 1e-6) / 1e12})
     return {"workload": "cfg4 decode: fused SmoothQuant + packed-weight GEMM, graph-replayed "
-                        "(two weight copies per shape alternate: MALL-cold)", "layers": results}
+                        "(two weight copies per shape alternate: MALL-cold)", "layers": results,
+            "cpu_baseline": cpu_baseline_decode(cpu_layers) if cpu else None}
 
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "gemm_i8_persist_and_tile_kernels__cfg3_llama3_8b_and_cfg2.md"
@@ -409,14 +501,54 @@ def bench_cfg3_smaller_m(torch, w8a8, dev, base, steps=10, sets=3):
     return out
 
 
-def bench_moe(torch, w8a8, dev, gen, iters=10):
+def capture_graph(torch, calls, repeat=1):
+    """Capture `calls` (closures enqueuing work on torch's current stream),
+    `repeat` times over, into a HIP graph on a side stream after one eager
+    pass of them there (one-time setup stays out of the capture).  Returns
+    (graph, stream)."""
+    torch.cuda.synchronize()
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        for c in calls:
+            c()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        for _ in range(repeat):
+            for c in calls:
+                c()
+    g.replay()
+    torch.cuda.synchronize()
+    return g, st
+
+
+def replay_us(torch, g, st):
+    """GPU time of one replay of g, between two events on its stream."""
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(st):
+        e0.record()
+        g.replay()
+        e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) * 1e3
+
+
+def bench_moe(torch, w8a8, dev, gen, iters=10, rounds=6, cpu=True):
     """Config 5: Mixtral-8x7B-shaped MoE FFN, 4096 tokens, hidden 4096, ffn
-    14336, 8 experts, top-2.  One iteration = routing, sort, MoE SmoothQuant
-    into expert-sorted rows, gate_up expert GEMM with the SiLU(gate)*up
-    epilogue and the requantization (weights interleaved once beforehand),
-    down expert GEMM, combine; ops = 2 * 8192 rows * (28672*4096 + 4096*14336).
-    The same layer with the gate_up GEMM and the SiLU requantization as two
-    launches is timed alternately with it, the same way."""
+    14336, 8 experts, top-2.  One layer = routing, sort, MoE SmoothQuant into
+    expert-sorted rows, gate_up expert GEMM with the SiLU(gate)*up epilogue
+    and the requantization (weights interleaved once beforehand), down expert
+    GEMM, combine; ops = 2 * 8192 rows * (28672*4096 + 4096*14336).  The same
+    layer with the gate_up GEMM and the SiLU requantization as two launches
+    is the unfused form.
+    Every buffer (routing and sort outputs included) is allocated once, and
+    the layers are replayed from captured HIP graphs (`iters` layers per
+    graph), so no host-side work or allocation can enter the timed region:
+    the fused and unfused graphs alternate for `rounds` replays each after
+    0.3 s of untimed layers (the clocks settle under this load), and the
+    layer time is the mean over the replays.  Each stage is also timed alone,
+    `iters` launches of it per graph (`stage_us`); the last fused replay's
+    output is compared bitwise with an eager layer's."""
     t, h, inter, e, k = 4096, 4096, 14336, 8, 2
     x = torch.randn((t, h), generator=gen, device=dev)
     cols = torch.randperm(h, generator=gen, device=dev)[: round(0.005 * h)]
@@ -430,6 +562,13 @@ def bench_moe(torch, w8a8, dev, gen, iters=10):
     wd = torch.randint(-127, 128, (e, h, inter), generator=gen, device=dev, dtype=torch.int8)
     sd = torch.rand((e, h), generator=gen, device=dev) * 9e-3 + 1e-3
     cap = int(w8a8.library().w8a8_moe_sort_capacity(t, k, e, 32))
+    rw = torch.empty((t, k), dtype=torch.float32, device=dev)
+    rid = torch.empty((t, k), dtype=torch.int32, device=dev)
+    srt = dict(count=torch.empty(e, dtype=torch.int32, device=dev),
+               start=torch.empty(e + 1, dtype=torch.int32, device=dev),
+               padded=torch.empty(e, dtype=torch.int32, device=dev),
+               sorted_ids=torch.empty(cap, dtype=torch.int32, device=dev),
+               dst_row=torch.empty(t * k, dtype=torch.int32, device=dev))
     qa = torch.empty((cap, h), dtype=torch.int8, device=dev)
     ra = torch.empty(cap, dtype=torch.float32, device=dev)
     gu = torch.empty((cap, 2 * inter), dtype=torch.float16, device=dev)
@@ -442,79 +581,73 @@ def bench_moe(torch, w8a8, dev, gen, iters=10):
                           device=dev)
     sort_ws = torch.empty(max(1, w8a8.moe_sort_workspace_size(t, k, e)), dtype=torch.uint8,
                           device=dev)
+    st = {
+        "route": lambda: w8a8.topk_softmax(logits, k, out=(rw, rid)),
+        "sort": lambda: w8a8.moe_sort(rid, e, 32, workspace=sort_ws, out=srt),
+        "quant": lambda: w8a8.moe_smoothquant(x, s, rid, dst_row=srt["dst_row"], rows=cap,
+                                              out=qa, row_scale=ra),
+        "gate_up_silu": lambda: w8a8.moe_gate_up_silu(qa, wgu_il, srt["start"], srt["count"], ra,
+                                                      sgu_il, q=q2, row_scale=r2,
+                                                      workspace=ws_silu),
+        "gate_up": lambda: w8a8.moe_gemm(qa, wgu, srt["start"], srt["count"], ra, sgu, out=gu,
+                                         workspace=ws),
+        "silu_quant": lambda: w8a8.moe_silu_mul_quant(gu, srt["start"], srt["count"], q=q2,
+                                                      row_scale=r2),
+        "down": lambda: w8a8.moe_gemm(q2, wd, srt["start"], srt["count"], r2, sd, out=y,
+                                      workspace=ws),
+        "combine": lambda: w8a8.moe_combine(y, rw, srt["dst_row"], out=out),
+    }
     stages = ["route", "sort", "quant", "gate_up_silu", "down", "combine"]
-
-    def chain(ev=None):
-        mark = (lambda i: ev[i].record()) if ev is not None else (lambda i: None)
-        mark(0)
-        w, ids = w8a8.topk_softmax(logits, k)
-        mark(1)
-        srt = w8a8.moe_sort(ids, e, 32, workspace=sort_ws)
-        mark(2)
-        w8a8.moe_smoothquant(x, s, ids, dst_row=srt["dst_row"], rows=cap, out=qa, row_scale=ra)
-        mark(3)
-        w8a8.moe_gate_up_silu(qa, wgu_il, srt["start"], srt["count"], ra, sgu_il, q=q2,
-                              row_scale=r2, workspace=ws_silu)
-        mark(4)
-        w8a8.moe_gemm(q2, wd, srt["start"], srt["count"], r2, sd, out=y, workspace=ws)
-        mark(5)
-        w8a8.moe_combine(y, w, srt["dst_row"], out=out)
-        mark(6)
-
-    def chain_unfused(ev=None):  # the same layer with the gate_up GEMM and SiLU requant apart
-        mark = (lambda i: ev[i].record()) if ev is not None else (lambda i: None)
-        mark(0)
-        w, ids = w8a8.topk_softmax(logits, k)
-        mark(1)
-        srt = w8a8.moe_sort(ids, e, 32, workspace=sort_ws)
-        mark(2)
-        w8a8.moe_smoothquant(x, s, ids, dst_row=srt["dst_row"], rows=cap, out=qa, row_scale=ra)
-        mark(3)
-        w8a8.moe_gemm(qa, wgu, srt["start"], srt["count"], ra, sgu, out=gu, workspace=ws)
-        mark(4)
-        w8a8.moe_silu_mul_quant(gu, srt["start"], srt["count"], q=q2, row_scale=r2)
-        mark(5)
-        w8a8.moe_gemm(q2, wd, srt["start"], srt["count"], r2, sd, out=y, workspace=ws)
-        mark(6)
-        w8a8.moe_combine(y, w, srt["dst_row"], out=out)
-        mark(7)
-
-    # both forms alternate, after 0.3 s of them untimed (the clocks settle
-    # under this load), so neither is timed in a different power state
     stages_u = ["route", "sort", "quant", "gate_up", "silu_quant", "down", "combine"]
+    fused = [st[n] for n in stages]
+    unfused = [st[n] for n in stages_u]
+
+    for c in fused:  # eager reference layer
+        c()
+    torch.cuda.synchronize()
+    ref = out.clone()
     t_end = time.perf_counter() + 0.3
     while time.perf_counter() < t_end:
-        chain()
-        chain_unfused()
+        for c in fused + unfused:
+            c()
         torch.cuda.synchronize()
-    evs, evu = [], []
-    for rnd in range(iters):
-        for fn, dst, nm in ((chain, evs, len(stages) + 1), (chain_unfused, evu, len(stages_u) + 1))[
-                ::(1 if rnd % 2 == 0 else -1)]:
-            ev = [torch.cuda.Event(enable_timing=True) for _ in range(nm)]
-            fn(ev)
-            dst.append(ev)
+    gf, sf = capture_graph(torch, fused, iters)
+    gu_, su = capture_graph(torch, unfused, iters)
+    tf, tu = [], []
+    for rnd in range(rounds):
+        for g, stm, dst in ((gf, sf, tf), (gu_, su, tu))[::(1 if rnd % 2 == 0 else -1)]:
+            dst.append(replay_us(torch, g, stm) / iters)
+    gf.replay()  # the last replay: the fused layer's output
     torch.cuda.synchronize()
-    per = {st: sum(ev[j].elapsed_time(ev[j + 1]) for ev in evs) / iters * 1e3
-           for j, st in enumerate(stages)}
-    total_us = sum(ev[0].elapsed_time(ev[-1]) for ev in evs) / iters * 1e3
-    unf = {st: sum(ev[j].elapsed_time(ev[j + 1]) for ev in evu) / iters * 1e3
-           for j, st in enumerate(stages_u)}
-    unf_total = sum(ev[0].elapsed_time(ev[-1]) for ev in evu) / iters * 1e3
+    same = bool(torch.equal(out.view(torch.int16), ref.view(torch.int16)))
+    per = {}
+    for n in dict.fromkeys(stages + stages_u):
+        g, stm = capture_graph(torch, [st[n]], iters)
+        per[n] = min(replay_us(torch, g, stm) for _ in range(3)) / iters
+        del g
+    total_us = sum(tf) / len(tf)
+    unf_total = sum(tu) / len(tu)
     rows = t * k
     ops_gu = 2.0 * rows * 2 * inter * h
     ops_d = 2.0 * rows * h * inter
     return {"workload": "cfg5 MoE FFN, Mixtral-8x7B shape: 4096 tokens, hidden 4096, ffn 14336, "
                         "8 experts, top-2 (routing -> sort -> quant -> gate_up GEMM with the "
                         "SiLU*up epilogue + requant -> down -> combine)",
-            "us_per_layer": total_us, "TOPS": (ops_gu + ops_d) / (total_us * 1e-6) / 1e12,
-            "stage_us": per,
+            "timing": f"graph replays of {iters} layers, {rounds} replays per form alternating; "
+                      f"stages each in a graph of {iters} launches (best of 3 replays)",
+            "us_per_layer": total_us, "us_per_layer_replays": tf,
+            "TOPS": (ops_gu + ops_d) / (total_us * 1e-6) / 1e12,
+            "graph_matches_eager": same,
+            "stage_us": {n: per[n] for n in stages},
             "unfused_us_per_layer": unf_total,
-            "unfused_stage_us": unf,
-            "fused_saving_us": unf["gate_up"] + unf["silu_quant"] - per["gate_up_silu"],
+            "unfused_stage_us": {n: per[n] for n in stages_u},
+            "fused_saving_us": unf_total - total_us,
             "gate_up_silu_TOPS": ops_gu / (per["gate_up_silu"] * 1e-6) / 1e12,
             "down_TOPS": ops_d / (per["down"] * 1e-6) / 1e12,
-            "frac_mfma": (ops_gu + ops_d) / (total_us * 1e-6) / PEAK_INT8_OPS}
+            "frac_mfma": (ops_gu + ops_d) / (total_us * 1e-6) / PEAK_INT8_OPS,
+            "cpu_baseline": (cpu_baseline_moe(*(v.cpu().numpy() for v in
+                                                (x, logits, s, wgu, sgu, wd, sd)), k)
+                             if cpu else None)}
 
 
 def bench_hipblaslt_yardstick(torch, projs, iters=10):
@@ -767,7 +900,8 @@ def main(argv=None) -> int:
 
     extras = {}
     if not args.no_extras:
-        extras["smoothquant_cfg1"] = bench_quantizer(torch, w8a8, dev, gen)
+        cpu_x = not args.no_cpu_baseline
+        extras["smoothquant_cfg1"] = bench_quantizer(torch, w8a8, dev, gen, cpu=cpu_x)
         q1 = extras["smoothquant_cfg1"]
         q1["frac_stream21_cfg1_measured"] = q1["GBps"] / peaks["stream21_cfg1_GBps"]
         q1["frac_stream21_measured"] = q1["GBps"] / peaks["stream21_GBps"]
@@ -782,9 +916,9 @@ def main(argv=None) -> int:
         log(json.dumps(extras["gemm_cfg2"]))
         extras["cfg3_smaller_m"] = bench_cfg3_smaller_m(torch, w8a8, dev, projs)
         log(json.dumps(extras["cfg3_smaller_m"]))
-        extras["decode_cfg4"] = bench_decode(torch, w8a8, dev, gen)
+        extras["decode_cfg4"] = bench_decode(torch, w8a8, dev, gen, cpu=cpu_x)
         log(json.dumps(extras["decode_cfg4"]))
-        extras["moe_cfg5"] = bench_moe(torch, w8a8, dev, gen)
+        extras["moe_cfg5"] = bench_moe(torch, w8a8, dev, gen, cpu=cpu_x)
         log(json.dumps(extras["moe_cfg5"]))
 
     if args.calibrate_copy:

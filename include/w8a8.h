@@ -184,6 +184,39 @@ int w8a8_gemm_streamk(uint32_t m, uint32_t n, uint32_t k, const int8_t* a, const
                       hipStream_t stream);
 
 /*
+ * The block count w8a8_gemm_streamk launches for this shape and `blocks`
+ * argument (0: the count the library picks; otherwise min(blocks, the
+ * problem's k-tiles)); 0 for an empty problem.  The reference sample prints
+ * its num_cus (rocwmma_streamk_gemm.cpp:223-226, :268-270).
+ */
+uint32_t w8a8_gemm_streamk_blocks(uint32_t m, uint32_t n, uint32_t k, uint32_t blocks);
+
+/*
+ * Sticky status of w8a8_gemm_streamk on the current device.  The last piece
+ * of a split tile waits for the other pieces' partials with a bounded poll
+ * (about 2^24 sleeps; never reached when every piece runs); if the bound
+ * expires it still finishes the tile, so every wave exits, but that tile may
+ * be wrong, and the launch sets W8A8_STREAMK_WAIT_EXPIRED in a per-device
+ * word that stays set until read with clear != 0.  The query synchronizes
+ * the device first (hipDeviceSynchronize), so it covers every launch already
+ * enqueued on any stream; it is a diagnostic, not for hot loops.  No
+ * counterpart in the reference (its reduce launch has no wait).
+ */
+#define W8A8_STREAMK_WAIT_EXPIRED 1u
+int w8a8_gemm_streamk_status(uint32_t* flags, int clear);
+
+/*
+ * Test hook of the bounded wait above: spin_limit polls before giving up
+ * (0: the default) and phantom_pieces pieces that the last piece of every
+ * split tile also waits for (0: none).  With phantom_pieces > 0 every split
+ * tile gives up after spin_limit polls (which must be in [1, 4096]), sums
+ * the partials that are there (all of them: the real pieces have arrived)
+ * and sets W8A8_STREAMK_WAIT_EXPIRED; nothing waits forever.  Process-wide;
+ * call w8a8_debug_streamk_wait(0, 0) to restore the defaults.
+ */
+int w8a8_debug_streamk_wait(uint32_t spin_limit, uint32_t phantom_pieces);
+
+/*
  * Bytes of the per-GPU scratch array w8a8_gemm_noalloc uses (32 MiB).
  */
 #define W8A8_NOALLOC_SCRATCH_BYTES (32u << 20)

@@ -30,12 +30,13 @@ from ._lib import (  # noqa: F401
     LAYOUT_A_ROW_B_NK,
     OUT_F16,
     OUT_I32,
+    STREAMK_WAIT_EXPIRED,
     W8A8Error,
 )
 
 __all__ = [
     "library", "version", "smoothquant", "moe_smoothquant", "gemm", "gemm_workspace_size",
-    "gemm_streamk",
+    "gemm_streamk", "gemm_streamk_blocks", "gemm_streamk_status",
     "fused_sq_gemm", "W8A8Error", "PackedWeights", "pack_weights", "pack_weights_size",
     "gemm_packed", "gemm_packed_workspace_size", "fused_sq_gemm_packed", "grouped_gemm",
     "topk_softmax", "moe_sort", "moe_sort_workspace_size", "moe_gemm", "moe_gemm_workspace_size", "moe_silu_mul_quant",
@@ -251,6 +252,22 @@ def gemm_streamk(a, b, scale_a=None, scale_b=None, tensor_scale_a: float = 1.0,
     return c
 
 
+def gemm_streamk_blocks(m: int, n: int, k: int, blocks: int = 0) -> int:
+    """w8a8_gemm_streamk_blocks: the block count gemm_streamk launches."""
+    return int(library().w8a8_gemm_streamk_blocks(m, n, k, blocks))
+
+
+def gemm_streamk_status(clear: bool = True) -> int:
+    """w8a8_gemm_streamk_status: the current device's sticky stream-K flags
+    (STREAMK_WAIT_EXPIRED when a split tile's bounded wait gave up), read after
+    a device-wide synchronisation; cleared when `clear`."""
+    import ctypes
+
+    flags = ctypes.c_uint32(0)
+    _lib.call("w8a8_gemm_streamk_status", ctypes.byref(flags), 1 if clear else 0)
+    return int(flags.value)
+
+
 def fused_sq_gemm(x, smooth_scale, w, scale_w, out=None, q=None, row_scale=None,
                   workspace=None):
     """SmoothQuant x [M, K] then C = dequant(q . w^T): returns (c fp16 [M, N], q, row_scale).
@@ -439,14 +456,24 @@ def grouped_gemm(problems, out_dtype=None, outs=None):
 _pending_descs: list = []  # (event, host descriptor array) of grouped_gemm calls in flight
 
 
-def topk_softmax(logits, topk: int):
-    """logits fp32 or fp16 [T, E] -> (weights fp32 [T, topk], ids int32 [T, topk])."""
+def topk_softmax(logits, topk: int, out=None):
+    """logits fp32 or fp16 [T, E] -> (weights fp32 [T, topk], ids int32 [T, topk]).
+    out: an optional (weights, ids) pair of contiguous tensors to write, so
+    that a caller's loop (or a captured graph) allocates nothing."""
     torch = _torch()
     _require_cuda(logits)
     logits = logits.contiguous()
     t, e = logits.shape
-    w = torch.empty((t, topk), dtype=torch.float32, device=logits.device)
-    ids = torch.empty((t, topk), dtype=torch.int32, device=logits.device)
+    if out is not None:
+        w, ids = out
+        if (tuple(w.shape) != (t, topk) or w.dtype != torch.float32 or not w.is_contiguous()
+                or tuple(ids.shape) != (t, topk) or ids.dtype != torch.int32
+                or not ids.is_contiguous()):
+            raise ValueError("topk_softmax: out must be contiguous (fp32 [T, topk], int32 [T, topk])")
+        _require_cuda(w, ids)
+    else:
+        w = torch.empty((t, topk), dtype=torch.float32, device=logits.device)
+        ids = torch.empty((t, topk), dtype=torch.int32, device=logits.device)
     _lib.call("w8a8_topk_softmax", _ptr(logits), 1 if logits.dtype == torch.float16 else 0,
               _ptr(w), _ptr(ids), t, e, topk, _stream(logits.device))
     return w, ids
@@ -457,23 +484,32 @@ def moe_sort_workspace_size(tokens: int, topk: int, experts: int) -> int:
     return int(library().w8a8_moe_sort_workspace_size(tokens, topk, experts))
 
 
-def moe_sort(topk_ids, experts: int, unit_size: int = 32, workspace="auto"):
+def moe_sort(topk_ids, experts: int, unit_size: int = 32, workspace="auto", out=None):
     """Stable expert sort of topk_ids int32 [T, k].  Returns a dict with
     count [E], start [E+1], padded [E], sorted_ids [capacity], dst_row [T*k].
     workspace: 'auto' (allocated here when T*k > 1024), None (one
     workgroup), or a device tensor of moe_sort_workspace_size bytes; the
-    outputs are identical either way."""
+    outputs are identical either way.  out: an optional dict of those five
+    int32 tensors (contiguous, at least those sizes) to write instead of
+    allocating them."""
     torch = _torch()
     _require_cuda(topk_ids)
     ids = topk_ids.contiguous()
     t, k = ids.shape
     cap = int(library().w8a8_moe_sort_capacity(t, k, experts, unit_size))
     d = ids.device
-    out = dict(count=torch.empty(experts, dtype=torch.int32, device=d),
-               start=torch.empty(experts + 1, dtype=torch.int32, device=d),
-               padded=torch.empty(experts, dtype=torch.int32, device=d),
-               sorted_ids=torch.empty(cap, dtype=torch.int32, device=d),
-               dst_row=torch.empty(t * k, dtype=torch.int32, device=d))
+    sizes = dict(count=experts, start=experts + 1, padded=experts, sorted_ids=cap, dst_row=t * k)
+    if out is not None:
+        for name, size in sizes.items():
+            v = out.get(name)
+            if (v is None or v.dtype != torch.int32 or not v.is_contiguous()
+                    or v.numel() < size):
+                raise ValueError(f"moe_sort: out['{name}'] must be a contiguous int32 tensor of "
+                                 f"at least {size} elements")
+            _require_cuda(v)
+    else:
+        out = {name: torch.empty(size, dtype=torch.int32, device=d)
+               for name, size in sizes.items()}
     ws, ws_bytes = _workspace(workspace, lambda: moe_sort_workspace_size(t, k, experts), d)
     _lib.call("w8a8_moe_sort", _ptr(ids), t, k, experts, unit_size, _ptr(out["count"]),
               _ptr(out["start"]), _ptr(out["padded"]), _ptr(out["sorted_ids"]), cap,
@@ -531,8 +567,15 @@ def moe_interleave_gate_up(w_gate_up, scale_w=None):
     """gate_up weights int8 [E, 2*inter, K] (+ scales [E, 2*inter]) -> the row
     order moe_gate_up_silu reads (blocks of 16 gate rows then their 16 up rows)."""
     torch = _torch()
-    _require_cuda(w_gate_up, scale_w)
     e, two_i, k = w_gate_up.shape
+    # the C ABI takes one row stride: rows of unit stride along K, experts
+    # packed back to back at 2 * inter rows each
+    if w_gate_up.stride(2) != 1 or w_gate_up.stride(0) != two_i * w_gate_up.stride(1):
+        raise ValueError("moe_interleave_gate_up: w_gate_up must be [E, 2*inter, K] with unit "
+                         "stride along K and experts 2*inter rows apart (call .contiguous())")
+    if scale_w is not None and not scale_w.is_contiguous():
+        raise ValueError("moe_interleave_gate_up: scale_w must be a contiguous [E, 2*inter]")
+    _require_cuda(w_gate_up, scale_w)
     wo = torch.empty((e, two_i, k), dtype=torch.int8, device=w_gate_up.device)
     so = torch.empty((e, two_i), dtype=torch.float32, device=w_gate_up.device) \
         if scale_w is not None else None
@@ -553,11 +596,22 @@ def moe_gate_up_silu(a, w_interleaved, expert_start, expert_count, scale_a=None,
     requantization for the down GEMM: a int8 [rows, K] expert-sorted,
     w_interleaved from moe_interleave_gate_up -> (q int8 [rows, inter], row_scale)."""
     torch = _torch()
+    rows, k = a.shape
+    e, two_i, kw = w_interleaved.shape
+    inter = two_i // 2
+    # the C ABI reads the weights as a contiguous [E, 2*inter, K] (ldw = K)
+    if kw != k or not w_interleaved.is_contiguous():
+        raise ValueError(f"moe_gate_up_silu: w_interleaved must be a contiguous [E, 2*inter, K={k}]"
+                         f" (got shape {tuple(w_interleaved.shape)}, "
+                         f"strides {tuple(w_interleaved.stride())})")
+    if a.stride(1) != 1:
+        raise ValueError("moe_gate_up_silu: a must have unit stride along K")
+    for name, t in (("scale_a", scale_a), ("scale_w_interleaved", scale_w_interleaved),
+                    ("smooth_scale", smooth_scale)):
+        if t is not None and not t.is_contiguous():
+            raise ValueError(f"moe_gate_up_silu: {name} must be contiguous")
     _require_cuda(a, w_interleaved, expert_start, expert_count, scale_a, scale_w_interleaved,
                   smooth_scale)
-    rows, k = a.shape
-    e, two_i, _ = w_interleaved.shape
-    inter = two_i // 2
     q = q if q is not None else torch.empty((rows, inter), dtype=torch.int8, device=a.device)
     r = row_scale if row_scale is not None else torch.empty(rows, dtype=torch.float32,
                                                             device=a.device)

@@ -22,6 +22,8 @@ LAYOUT_A_COL_B_KN = 1
 OUT_I32 = 0
 OUT_F16 = 1
 
+STREAMK_WAIT_EXPIRED = 1
+
 FOLD_MULTIPLY = 0
 FOLD_DIVIDE = 1
 
@@ -61,6 +63,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "w8a8_gemm_streamk_workspace_size": (_size, [_u32, _u32, _u32, _u32]),
     "w8a8_gemm_streamk": (_i32, [_u32, _u32, _u32, _ptr, _ptr, _ptr, _u32, _u32, _u32, _ptr, _ptr,
                                  _f32, _f32, _i32, _u32, _ptr, _size, _ptr]),
+    "w8a8_gemm_streamk_blocks": (_u32, [_u32, _u32, _u32, _u32]),
+    "w8a8_gemm_streamk_status": (_i32, [ctypes.POINTER(ctypes.c_uint32), _i32]),
+    "w8a8_debug_streamk_wait": (_i32, [_u32, _u32]),
     "w8a8_fused_sq_gemm": (_i32, [_ptr, _ptr, _ptr, _ptr, _ptr, _u32, _u32, _u32, _u32, _u32,
                                   _u32, _ptr, _ptr, _ptr, _size, _ptr]),
     "w8a8_pack_weights_size": (_size, [_u32, _u32]),

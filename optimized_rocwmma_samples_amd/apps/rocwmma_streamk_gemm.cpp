@@ -6,7 +6,7 @@
 // and reduces them in a second launch, :129-143, :185-211).
 // `rocwmma_streamk_gemm [M N K] [--blocks=B]`; default: the reference's
 // sizes (:286-297), 512^2 ... 4096^2 at K = 4096.  Result line
-//   [StreamK-GEMM] M=<M> N=<N> K=<K> num_cus=<blocks>  <ms> ms  <TF> TFlops/s
+//   [StreamK-GEMM] M=<M> N=<N> K=<K> num_cus=<blocks launched>  <ms> ms  <TF> TFlops/s
 #include "common.hpp"
 
 static void test_streamk(uint32_t m, uint32_t n, uint32_t k, uint32_t blocks, bool verify)
@@ -25,12 +25,9 @@ static void test_streamk(uint32_t m, uint32_t n, uint32_t k, uint32_t blocks, bo
         CHECK_W8A8(w8a8_gemm_streamk(m, n, k, da.p, dw.p, c, k, k, n, dsa.p, dsb.p, 1.f, 1.f, out,
                                      blocks, ws.p, wsb, nullptr));
     };
-    int dev = 0, cus = 0;
-    CHECK_HIP(hipGetDevice(&dev));
-    CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
     const double ms = app::bench_ms([&] { fn(dc.p, W8A8_OUT_F16); });
     std::cout << "[StreamK-GEMM] M=" << m << " N=" << n << " K=" << k
-              << " num_cus=" << (blocks ? blocks : (uint32_t)cus) << "  " << ms << " ms  "
+              << " num_cus=" << w8a8_gemm_streamk_blocks(m, n, k, blocks) << "  " << ms << " ms  "
               << 2.0 * m * n * k / (ms * 1e-3) / 1e12 << " TFlops/s\n";
     if(verify) {
         app::Dev<int32_t> di((size_t)m * n);
@@ -45,7 +42,10 @@ static void test_streamk(uint32_t m, uint32_t n, uint32_t k, uint32_t blocks, bo
                 bad += gi[rows[ri] * n + j] != acc[ri * n + j];
                 bad += gc[rows[ri] * n + j] != app::cpu_dequant(acc[ri * n + j], hsa[rows[ri]], hsb[j]);
             }
-        app::report(bad == 0, "mismatches=" + std::to_string(bad));
+        uint32_t flags = 0;
+        CHECK_W8A8(w8a8_gemm_streamk_status(&flags, 1));
+        app::report(bad == 0 && flags == 0,
+                    "mismatches=" + std::to_string(bad) + " status=" + std::to_string(flags));
     }
 }
 

@@ -2,7 +2,8 @@
 //
 // Each entry point validates its arguments on the host before touching HIP, so
 // every error path is testable without a GPU, then enqueues the kernels on the
-// caller's stream.  No entry point allocates device memory or synchronizes.
+// caller's stream.  No entry point allocates device memory; only the
+// diagnostic query w8a8_gemm_streamk_status synchronizes.
 #include "../../include/w8a8.h"
 #include "w8a8_internal.hpp"
 
@@ -360,6 +361,29 @@ int w8a8_gemm_streamk(uint32_t m, uint32_t n, uint32_t k, const int8_t* a, const
     if(reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
         return fail(W8A8_ERROR_INVALID_VALUE, "%s: workspace must be 16-byte aligned", fn);
     return hip_status(w8a8::launch_gemm_streamk(g, blocks, workspace, stream), fn);
+}
+
+uint32_t w8a8_gemm_streamk_blocks(uint32_t m, uint32_t n, uint32_t k, uint32_t blocks)
+{
+    return w8a8::streamk_blocks(m, n, k, blocks);
+}
+
+int w8a8_gemm_streamk_status(uint32_t* flags, int clear)
+{
+    if(!flags) return fail(W8A8_ERROR_INVALID_VALUE, "w8a8_gemm_streamk_status: null flags");
+    *flags = 0;
+    return hip_status(w8a8::streamk_status(flags, clear != 0), "w8a8_gemm_streamk_status");
+}
+
+int w8a8_debug_streamk_wait(uint32_t spin_limit, uint32_t phantom_pieces)
+{
+    if(phantom_pieces > 0 && (spin_limit == 0 || spin_limit > 4096))
+        return fail(W8A8_ERROR_INVALID_VALUE,
+                    "w8a8_debug_streamk_wait: phantom pieces need a spin limit in [1, 4096] "
+                    "(got %u): the wait they force must end quickly",
+                    spin_limit);
+    w8a8::streamk_debug_wait(spin_limit, phantom_pieces);
+    return W8A8_SUCCESS;
 }
 
 int w8a8_fused_sq_gemm(const void* x, const float* smooth_scale, const int8_t* w,

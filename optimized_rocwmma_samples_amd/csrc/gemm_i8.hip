@@ -13,7 +13,10 @@
 #include "w8a8_internal.hpp"
 
 #include <algorithm>
+#include <atomic>
+#include <map>
 #include <mutex>
+#include <tuple>
 
 namespace w8a8 {
 
@@ -592,8 +595,7 @@ template <class C>
 double sk_cost(const gemm::SkPlan& s, double tops, double xbw)
 {
     const uint64_t u    = (s.total() + s.blocks - 1) / s.blocks;
-    uint32_t       pmax = 1;
-    for(uint32_t t = 0; t < s.ntiles; ++t) pmax = std::max(pmax, s.pieces(t));
+    const uint32_t pmax = s.max_pieces();
     const double unit_s = 2.0 * C::kBM * C::kBN * C::kBK / (tops / device_cus());
     return (double)u * unit_s + (pmax - 1) * (double)gemm::Partial<C>::kBytes / xbw;
 }
@@ -602,7 +604,7 @@ double sk_cost(const gemm::SkPlan& s, double tops, double xbw)
 // 1/8 of that: a few tiles cut into many pieces cost their last blocks more
 // partials than the extra blocks save (512^3: 16 pieces per tile on 256
 // blocks, 4 on 64).
-ExplicitSk explicit_streamk(uint32_t m, uint32_t n, uint32_t k, uint32_t blocks)
+ExplicitSk plan_streamk(uint32_t m, uint32_t n, uint32_t k, uint32_t blocks)
 {
     const uint32_t nk = (k + 127) / 128;
     ExplicitSk     e{TileCfg::kMain, {}, 0};
@@ -632,6 +634,36 @@ ExplicitSk explicit_streamk(uint32_t m, uint32_t n, uint32_t k, uint32_t blocks)
     return e;
 }
 
+// plan_streamk memoized per (m, n, k, blocks): every w8a8_gemm_streamk call
+// needs the plan twice (the workspace check, then the launch) and a caller
+// sizing its workspace a third time; the plan depends on nothing else (the CU
+// count is the process's first device's).  The table is bounded: a caller
+// cycling through more shapes than kMaxPlans starts it over.
+ExplicitSk explicit_streamk(uint32_t m, uint32_t n, uint32_t k, uint32_t blocks)
+{
+    constexpr size_t kMaxPlans = 1024;
+    struct Key {
+        uint32_t m, n, k, blocks;
+        bool     operator<(const Key& o) const
+        {
+            return std::tie(m, n, k, blocks) < std::tie(o.m, o.n, o.k, o.blocks);
+        }
+    };
+    static std::mutex               mu;
+    static std::map<Key, ExplicitSk> plans;
+    const Key                        key{m, n, k, blocks};
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        const auto                  it = plans.find(key);
+        if(it != plans.end()) return it->second;
+    }
+    const ExplicitSk e = plan_streamk(m, n, k, blocks);
+    std::lock_guard<std::mutex> lock(mu);
+    if(plans.size() >= kMaxPlans) plans.clear();
+    plans.emplace(key, e);
+    return e;
+}
+
 } // namespace
 
 bool streamk_shape_ok(const GemmArgs& g)
@@ -653,19 +685,83 @@ uint32_t streamk_blocks(uint32_t m, uint32_t n, uint32_t k, uint32_t blocks)
     return explicit_streamk(m, n, k, blocks).plan.blocks;
 }
 
+// ---------------------------------------------------------------------------
+// The stream-K wait's status word (gemm::SkWatch): one per GPU, a file-scope
+// device array like the no-allocation scratch below, reached from the host
+// only through the address hipGetSymbolAddress returns for the current
+// device.  Zero-initialised when the code object loads; a kernel only ORs
+// bits into it; streamk_status reads (and optionally clears) it.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) uint32_t sk_status[64];
+
+namespace {
+
+hipError_t sk_status_ptr(uint32_t** ptr)
+{
+    constexpr int     kMaxDevices = 64;
+    static std::mutex mu;
+    static void*      addr[kMaxDevices] = {};
+    int               dev               = 0;
+    hipError_t        e                 = hipGetDevice(&dev);
+    if(e != hipSuccess) return e;
+    if(dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if(addr[dev] == nullptr) {
+        void* p = nullptr;
+        e       = hipGetSymbolAddress(&p, HIP_SYMBOL(sk_status));
+        if(e != hipSuccess) return e;
+        addr[dev] = p;
+    }
+    *ptr = static_cast<uint32_t*>(addr[dev]);
+    return hipSuccess;
+}
+
+// the wait's poll limit and phantom piece count (test hook only)
+std::atomic<uint32_t> g_sk_spin{gemm::kSkSpinLimit};
+std::atomic<uint32_t> g_sk_phantom{0};
+
+} // namespace
+
+void streamk_debug_wait(uint32_t spin, uint32_t phantom)
+{
+    g_sk_spin.store(spin ? spin : gemm::kSkSpinLimit);
+    g_sk_phantom.store(phantom);
+}
+
+hipError_t streamk_status(uint32_t* flags, bool clear)
+{
+    uint32_t*  ptr = nullptr;
+    hipError_t e   = sk_status_ptr(&ptr);
+    if(e != hipSuccess) return e;
+    // every launch that may set the word has finished, on any stream
+    if((e = hipDeviceSynchronize()) != hipSuccess) return e;
+    if((e = hipMemcpy(flags, ptr, sizeof(uint32_t), hipMemcpyDeviceToHost)) != hipSuccess) return e;
+    if(clear && *flags) {
+        const uint32_t zero = 0;
+        e = hipMemcpy(ptr, &zero, sizeof(uint32_t), hipMemcpyHostToDevice);
+    }
+    return e;
+}
+
 hipError_t launch_gemm_streamk(const GemmArgs& g, uint32_t blocks, void* ws, hipStream_t stream)
 {
     if(g.m == 0 || g.n == 0) return hipSuccess;
+    gemm::SkWatch watch{nullptr, g_sk_spin.load(), g_sk_phantom.load()};
+    const hipError_t err = sk_status_ptr(&watch.status);
+    if(err != hipSuccess) return err;
     const ExplicitSk e      = explicit_streamk(g.m, g.n, g.k, blocks);
     const KArgs      p      = make_kargs(g);
     const int        vec_ok = out_vec_ok(g);
     switch(e.cfg) {
     case TileCfg::kMain:
-        return gemm::launch_cfg_streamk<GemmMain>(p, g.out_type, vec_ok, 0, e.plan, ws, stream);
+        return gemm::launch_cfg_streamk<GemmMain>(p, g.out_type, vec_ok, 0, e.plan, ws, watch,
+                                                  stream);
     case TileCfg::kMidM:
-        return gemm::launch_cfg_streamk<GemmMidM>(p, g.out_type, vec_ok, 0, e.plan, ws, stream);
+        return gemm::launch_cfg_streamk<GemmMidM>(p, g.out_type, vec_ok, 0, e.plan, ws, watch,
+                                                  stream);
     default:
-        return gemm::launch_cfg_streamk<GemmSmall>(p, g.out_type, vec_ok, 0, e.plan, ws, stream);
+        return gemm::launch_cfg_streamk<GemmSmall>(p, g.out_type, vec_ok, 0, e.plan, ws, watch,
+                                                   stream);
     }
 }
 

@@ -56,6 +56,22 @@ struct SkPlan {
     {
         return b >= 1 && b < blocks && start(b) % nk != 0;
     }
+    // the most pieces any tile has: 1 + the most cuts (block ranges starting
+    // strictly inside a tile) that fall in one tile.  Block starts increase,
+    // so the cuts of one tile are consecutive blocks: O(blocks), not O(tiles)
+    __host__ __device__ uint32_t max_pieces() const
+    {
+        uint32_t best = 1, run = 1;
+        uint64_t cur = ~0ull;
+        for(uint32_t b = 1; b < blocks; ++b) {
+            if(!cut(b)) continue;
+            const uint64_t t = start(b) / nk;
+            run              = t == cur ? run + 1 : 2;
+            cur              = t;
+            best             = run > best ? run : best;
+        }
+        return best;
+    }
     // workspace: 2 counters per tile (256-byte aligned), then the slots
     __host__ __device__ size_t sync_bytes() const { return ((size_t)ntiles * 8 + 255) / 256 * 256; }
 };
@@ -129,6 +145,20 @@ __device__ __forceinline__ void add_partial_dev(const int32_t* part, Acc<C>& acc
 // count); the bound keeps every wave's exit certain.
 constexpr uint32_t kSkSpinLimit = 1u << 24;
 
+// The bounded wait's report.  A last piece whose wait expires still sums the
+// slots and runs the epilogue (every wave exits), but that tile may hold
+// stale partials, so it sets kSkWaitExpired in *status, a device word that
+// stays set until the host reads and clears it (w8a8_gemm_streamk_status).
+// spin: polls before giving up (kSkSpinLimit).  phantom: pieces the last
+// piece waits for beyond the real ones, 0 except from the host's test hook,
+// which forces the give-up path without a piece that never arrives.
+constexpr uint32_t kSkWaitExpired = 1u;
+struct SkWatch {
+    uint32_t* status;
+    uint32_t  spin;
+    uint32_t  phantom;
+};
+
 __global__ void __launch_bounds__(256) streamk_clear_kernel(uint32_t* sync, uint32_t n)
 {
     for(uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) sync[i] = 0;
@@ -137,7 +167,7 @@ __global__ void __launch_bounds__(256) streamk_clear_kernel(uint32_t* sync, uint
 template <class C, int OUT>
 __global__ void __launch_bounds__(C::kThreads, 1)
     gemm_i8_streamk_kernel(KArgs p, int vec_ok, uint32_t t0, SkPlan sk, uint32_t* sync,
-                           int32_t* part)
+                           int32_t* part, SkWatch watch)
 {
     extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
     __shared__ uint32_t bcast[2];
@@ -186,11 +216,15 @@ __global__ void __launch_bounds__(C::kThreads, 1)
             }
             // the last piece to arrive: wait for the others' partials, sum
             if(threadIdx.x == 0) {
-                uint32_t polls = 0;
+                const uint32_t want  = pieces + watch.phantom;
+                uint32_t       polls = 0;
                 while(__hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1
-                          < pieces
-                      && ++polls < kSkSpinLimit)
+                          < want
+                      && ++polls < watch.spin)
                     __builtin_amdgcn_s_sleep(2);
+                if(__hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 < want)
+                    __hip_atomic_fetch_or(watch.status, kSkWaitExpired, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
             }
             __syncthreads();
             for(uint32_t q = 0; q + 1 < pieces; ++q)
@@ -215,7 +249,7 @@ void raise_streamk_lds_once()
 // ws holds sk_workspace_bytes<C>(s) bytes (16-byte aligned).
 template <class C>
 hipError_t launch_cfg_streamk(const KArgs& p, int out_type, int vec_ok, uint32_t t0,
-                              const SkPlan& s, void* ws, hipStream_t stream)
+                              const SkPlan& s, void* ws, const SkWatch& watch, hipStream_t stream)
 {
     uint32_t*      sync = static_cast<uint32_t*>(ws);
     int32_t*       part = reinterpret_cast<int32_t*>(static_cast<int8_t*>(ws) + s.sync_bytes());
@@ -225,11 +259,13 @@ hipError_t launch_cfg_streamk(const KArgs& p, int out_type, int vec_ok, uint32_t
     if(out_type == W8A8_OUT_I32) {
         raise_streamk_lds_once<C, W8A8_OUT_I32>();
         hipLaunchKernelGGL((gemm_i8_streamk_kernel<C, W8A8_OUT_I32>), dim3(s.blocks),
-                           dim3(C::kThreads), C::kLdsBytes, stream, p, vec_ok, t0, s, sync, part);
+                           dim3(C::kThreads), C::kLdsBytes, stream, p, vec_ok, t0, s, sync, part,
+                           watch);
     } else {
         raise_streamk_lds_once<C, W8A8_OUT_F16>();
         hipLaunchKernelGGL((gemm_i8_streamk_kernel<C, W8A8_OUT_F16>), dim3(s.blocks),
-                           dim3(C::kThreads), C::kLdsBytes, stream, p, vec_ok, t0, s, sync, part);
+                           dim3(C::kThreads), C::kLdsBytes, stream, p, vec_ok, t0, s, sync, part,
+                           watch);
     }
     return hipGetLastError();
 }

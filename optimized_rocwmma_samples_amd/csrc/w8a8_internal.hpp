@@ -76,6 +76,12 @@ bool       streamk_shape_ok(const GemmArgs& g);
 size_t     streamk_workspace_bytes(uint32_t m, uint32_t n, uint32_t k, uint32_t blocks);
 uint32_t   streamk_blocks(uint32_t m, uint32_t n, uint32_t k, uint32_t blocks);
 hipError_t launch_gemm_streamk(const GemmArgs& g, uint32_t blocks, void* ws, hipStream_t stream);
+// The current device's stream-K status word (gemm::kSkWaitExpired bits),
+// read after a device-wide synchronisation, cleared when `clear`.
+hipError_t streamk_status(uint32_t* flags, bool clear);
+// Test hook of the stream-K wait: polls before giving up (0: the default)
+// and phantom pieces the last piece also waits for (0: none).
+void       streamk_debug_wait(uint32_t spin, uint32_t phantom);
 // Device address of the current GPU's W8A8_NOALLOC_SCRATCH_BYTES scratch
 // array (resolved once per device; gemm_i8.hip).
 hipError_t noalloc_scratch(void** ptr);

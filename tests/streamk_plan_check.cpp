@@ -9,10 +9,12 @@
 //   * the slot bases (the kernel's count of cut blocks starting before the
 //     tile) give each tile pieces(t) - 1 consecutive slots, disjoint from the
 //     other tiles' and ending exactly at sk_slots(plan);
-//   * a block meets at most two partly covered tiles.
+//   * a block meets at most two partly covered tiles;
+//   * max_pieces() equals the largest pieces(t).
 // Prints "OK <cases>" on success, the first failure otherwise (status 1).
 #include "../optimized_rocwmma_samples_amd/csrc/gemm_i8_streamk_kernel.hpp"
 
+#include <algorithm>
 #include <cstdio>
 #include <vector>
 
@@ -53,9 +55,10 @@ static int check(const SkPlan& s)
         if(owner[i] < 0) return fail(s, "k-tile not covered", i, 0);
         if(s.block_of(i) != (uint32_t)owner[i]) return fail(s, "block_of", i, s.block_of(i));
     }
-    uint32_t expect_base = 0;
+    uint32_t expect_base = 0, most = 1;
     for(uint32_t t = 0; t < s.ntiles; ++t) {
         if(s.pieces(t) != touch[t].size()) return fail(s, "pieces", t, s.pieces(t));
+        most = std::max<uint32_t>(most, (uint32_t)touch[t].size());
         uint32_t base = 0; // the kernel's count: cut blocks starting before the tile
         for(uint32_t b = 1; b < s.blocks; ++b)
             base += s.cut(b) && s.start(b) < (uint64_t)t * s.nk;
@@ -63,6 +66,7 @@ static int check(const SkPlan& s)
         expect_base += s.pieces(t) - 1;
     }
     if(expect_base != w8a8::gemm::sk_slots(s)) return fail(s, "sk_slots", expect_base, 0);
+    if(s.max_pieces() != most) return fail(s, "max_pieces", s.max_pieces(), most);
     return 0;
 }
 

@@ -406,3 +406,44 @@ def test_packed_workspace_size(w8a8):
     for m, n, k in ((1, 28672, 8192), (16, 4096, 4096), (32, 4096, 4096), (65, 4096, 4096),
                     (0, 64, 64)):
         assert lib.w8a8_gemm_packed_workspace_size(m, n, k) == 0
+
+
+def test_streamk_debug_wait_validation(w8a8):
+    # a forced give-up needs a short bounded wait; the defaults come back with (0, 0)
+    rc, msg = _status("w8a8_debug_streamk_wait", 0, 1)
+    assert rc == W.ERROR_INVALID_VALUE and "spin limit" in msg
+    rc, msg = _status("w8a8_debug_streamk_wait", 100000, 1)
+    assert rc == W.ERROR_INVALID_VALUE and "spin limit" in msg
+    assert W.library().w8a8_debug_streamk_wait(0, 0) == 0
+    rc, msg = _status("w8a8_gemm_streamk_status", None, 1)
+    assert rc == W.ERROR_INVALID_VALUE and "null" in msg
+
+
+def test_streamk_blocks_query_without_gpu(w8a8):
+    # an explicit count is clamped to the problem's k-tiles; an empty problem launches nothing
+    assert W.library().w8a8_gemm_streamk_blocks(256, 256, 256, 20) == 8
+    assert W.library().w8a8_gemm_streamk_blocks(256, 256, 256, 3) == 3
+    assert W.library().w8a8_gemm_streamk_blocks(0, 256, 256, 0) == 0
+
+
+def test_moe_weight_layout_checks(w8a8):
+    # the C ABI takes the gate_up weights as [E, 2*inter, K] rows of unit
+    # stride, experts back to back: the Python layer refuses other views
+    # before any call (checked on CPU tensors, before the device check)
+    import torch
+    w = torch.zeros((2, 32, 64), dtype=torch.int8)
+    with pytest.raises(ValueError, match="unit stride along K"):
+        W.moe_interleave_gate_up(w.transpose(1, 2).contiguous().transpose(1, 2))
+    with pytest.raises(ValueError, match="unit stride along K"):
+        W.moe_interleave_gate_up(torch.zeros((2, 48, 64), dtype=torch.int8)[:, :32])
+    a = torch.zeros((16, 64), dtype=torch.int8)
+    start = torch.zeros(2, dtype=torch.int32)
+    with pytest.raises(ValueError, match="K=64"):
+        W.moe_gate_up_silu(a, torch.zeros((2, 32, 96), dtype=torch.int8), start, start)
+    with pytest.raises(ValueError, match="contiguous"):
+        W.moe_gate_up_silu(a, torch.zeros((2, 32, 128), dtype=torch.int8)[:, :, :64], start, start)
+    with pytest.raises(ValueError, match="scale_w_interleaved"):
+        W.moe_gate_up_silu(a, w, start, start,
+                           scale_w_interleaved=torch.zeros((32, 2)).t())
+    with pytest.raises(ValueError, match="device tensors"):
+        W.moe_gate_up_silu(a, w, start, start)

@@ -696,3 +696,53 @@ def test_moe_ffn_chain_fused(w8a8, gpu):
         assert_f16_bitexact(y[r0:r1], y_exp)
     out_exp = O.moe_combine(y, host(parts["weights"]), dst)
     assert np.array_equal(host(out).view(np.uint16), out_exp.view(np.uint16))
+
+
+def test_moe_gate_up_silu_config5_full_size(w8a8, gpu):
+    """The kernel cfg5's bench times: the gate_up expert GEMM with the
+    SiLU(gate)*up epilogue and the requantization, at BASELINE config 5's full
+    shape (4096 tokens, top-2 of 8 experts, inter 14336, K = 4096), on the
+    expert-sorted rows the chain's own routing, sort and MoE quantizer produce.
+    Sampled rows of every expert (first, last and 24 spread) against the
+    oracle: q within one step, with the off-by-one fraction printed and
+    bounded, and row scales exact on all but a bounded few rows."""
+    import torch
+    t, h, inter, e, k = 4096, 4096, 14336, 8, 2
+    seed = G.config_seed(5)
+    gen = torch.Generator(device=gpu)
+    gen.manual_seed(seed + 1)
+    x = dev(G.activations(seed, t, h), gpu)
+    logits = dev(G.normal(seed, G.TID_LOGITS, (t, e), dtype=np.float32), gpu)
+    s = dev(G.uniform(seed, G.TID_EXPERT_S, (e, h), 0.5, 2.0), gpu)
+    wgu = torch.randint(-127, 128, (e, 2 * inter, h), generator=gen, device=gpu, dtype=torch.int8)
+    sgu = torch.rand((e, 2 * inter), generator=gen, device=gpu) * 9e-3 + 1e-3
+    w, ids = w8a8.topk_softmax(logits, k)
+    srt = w8a8.moe_sort(ids, e, 32)
+    rows = srt["sorted_ids"].numel()
+    qa, ra = w8a8.moe_smoothquant(x, s, ids, dst_row=srt["dst_row"], rows=rows)
+    w_il, s_il = w8a8.moe_interleave_gate_up(wgu, sgu)
+    q2 = torch.full((rows, inter), 99, dtype=torch.int8, device=gpu)
+    r2 = torch.full((rows,), -1.0, dtype=torch.float32, device=gpu)
+    w8a8.moe_gate_up_silu(qa, w_il, srt["start"], srt["count"], ra, s_il, q=q2, row_scale=r2)
+    start, count = host(srt["start"]), host(srt["count"])
+    qa_h, ra_h, qg, rg = host(qa), host(ra), host(q2), host(r2)
+    assert int(count.sum()) == t * k
+    off1 = exact = total = 0
+    for x_ in range(e):
+        r0, r1 = int(start[x_]), int(start[x_] + count[x_])
+        assert r1 > r0, "every expert receives tokens at this size"
+        pick = np.unique(np.r_[r0, r1 - 1, np.linspace(r0, r1 - 1, 24).astype(int)])
+        g = O.dequant_f16(O.gemm_i32(qa_h[pick], host(wgu[x_])), ra_h[pick], host(sgu[x_]))
+        qe, re = O.smoothquant(_silu_h16(g), np.ones(inter, np.float32))
+        d = np.abs(qg[pick].astype(np.int32) - qe)
+        assert d.max() <= 1, f"expert {x_}: q off by {d.max()}"
+        off1 += int((d != 0).sum())
+        exact += int((rg[pick].view(np.int32) == re.view(np.int32)).sum())
+        total += pick.size
+        if r1 < start[x_ + 1]:  # padding rows untouched
+            assert (qg[r1:start[x_ + 1]] == 99).all() and (rg[r1:start[x_ + 1]] == -1).all()
+    frac = off1 / (total * inter)
+    print(f"cfg5 gate_up_silu: {total} sampled rows x {inter}: {off1} q values off by one "
+          f"({frac:.2e}), {total - exact} row scales differ", flush=True)
+    assert off1 <= max(2, int(1e-3 * total * inter)), f"{off1} off-by-one values"
+    assert exact >= total - max(2, total // 100), f"{total - exact} row scales differ"

@@ -108,3 +108,51 @@ def test_streamk_refuses_bad_arguments(w8a8, gpu):
                                256, None, None, 1.0, 1.0, 1, 0, small.data_ptr(), small.numel(),
                                None)
     assert rc != 0 and "k % 16" in lib.w8a8_last_error().decode()
+
+
+def test_streamk_status_clear_after_normal_calls(w8a8, gpu):
+    """Every call above ran its waits to completion: the sticky word is 0."""
+    w8a8.gemm_streamk_status(clear=True)
+    a, b, _, _ = inputs(1024, 1024, 4096, 5)
+    ad, bd = dev(a, gpu), dev(b, gpu)
+    w8a8.gemm_streamk(ad, bd, blocks=0)
+    assert w8a8.gemm_streamk_status(clear=True) == 0
+
+
+def test_streamk_wait_expiry_is_reported(w8a8, gpu):
+    """The bounded wait's give-up path, forced from the host: the last piece of
+    each split tile also waits for one phantom piece and gives up after 16
+    polls.  Every wave still exits, the real partials are all there so C is
+    still exact, and the sticky flag reports the expiry until it is cleared."""
+    import torch
+    m, n, k = 1024, 1024, 4096   # 64 tiles of 128 x 128 on 256 blocks: 4 pieces a tile
+    a, b, _, _ = inputs(m, n, k, 6)
+    ad, bd = dev(a, gpu), dev(b, gpu)
+    ref = host(w8a8.gemm(ad, bd, out_dtype=torch.int32,
+                         workspace=torch.empty(0, dtype=torch.uint8, device=gpu)))
+    w8a8.gemm_streamk_status(clear=True)
+    lib = w8a8.library()
+    assert lib.w8a8_debug_streamk_wait(16, 1) == 0
+    try:
+        got = host(w8a8.gemm_streamk(ad, bd, out_dtype=torch.int32, blocks=0))
+    finally:
+        assert lib.w8a8_debug_streamk_wait(0, 0) == 0
+    assert_i32_equal(got, ref)
+    assert w8a8.gemm_streamk_status(clear=False) == w8a8.STREAMK_WAIT_EXPIRED
+    assert w8a8.gemm_streamk_status(clear=True) == w8a8.STREAMK_WAIT_EXPIRED
+    assert w8a8.gemm_streamk_status(clear=True) == 0
+    # defaults restored: the same call reports nothing
+    got = host(w8a8.gemm_streamk(ad, bd, out_dtype=torch.int32, blocks=0))
+    assert_i32_equal(got, ref)
+    assert w8a8.gemm_streamk_status(clear=True) == 0
+
+
+def test_streamk_blocks_query_matches_plan(w8a8, gpu):
+    """w8a8_gemm_streamk_blocks: an explicit count is clamped to the k-tiles,
+    0 picks at most one block per CU."""
+    import torch
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
+    assert w8a8.gemm_streamk_blocks(256, 256, 256, 20) == 8
+    assert w8a8.gemm_streamk_blocks(4096, 4096, 4096, 0) == cus
+    assert 1 <= w8a8.gemm_streamk_blocks(512, 512, 512, 0) <= cus
+    assert w8a8.gemm_streamk_blocks(0, 512, 512, 0) == 0
