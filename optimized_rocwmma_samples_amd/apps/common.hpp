@@ -88,6 +88,11 @@ inline Options parse(int argc, char** argv, const char* usage,
         const std::string a = argv[i];
         if(a == "-h" || a == "--help") {
             std::cout << "usage: " << usage << "\n";
+#if defined(W8A8_CPU_VERIFY)
+            std::cout << "CPU verify: on by default (debug build; --no-verify turns it off)\n";
+#else
+            std::cout << "CPU verify: off by default (--verify or W8A8_VERIFY=1 turns it on)\n";
+#endif
             std::exit(0);
         } else if(a == "--verify") {
             o.verify = true;

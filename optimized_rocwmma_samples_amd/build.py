@@ -7,7 +7,8 @@
 Every HIP translation unit is compiled with hipcc for gfx950 only.  The built
 library lands in optimized_rocwmma_samples_amd/lib/, the CLIs in
 optimized_rocwmma_samples_amd/bin/ (both git-ignored, both shipped with the
-tree to the GPU box).  `--debug` builds the CLIs with the CPU-verify switch on,
+tree to the GPU box).  `--debug` builds the CLIs with the CPU-verify switch on (the default build
+also puts debug builds of two CLIs in bin/debug/ for the GPU tests),
 the reference's `build.sh -d` (build.sh:43, a Debug build
 leaves NDEBUG undefined and enables the `#if !NDEBUG` check,
 rocwmma_perf_gemm.cpp:736-749).
@@ -138,6 +139,17 @@ def build_apps(debug: bool = False, verbose: bool = False, only: str | None = No
         return list(ex.map(one, srcs))
 
 
+# CLIs also built with the CPU-verify switch on, into bin/debug/, so that the
+# GPU tests can run a debug build without compiling on the GPU box
+DEBUG_APPS = ("rocwmma_smoothquant", "rocwmma_gemm_quantized")
+
+
+def build_debug_apps(verbose: bool = False) -> list[Path]:
+    return [exe for name in DEBUG_APPS
+            for exe in build_apps(debug=True, verbose=verbose, only=name,
+                                  bin_dir=BIN_DIR / "debug")]
+
+
 def clean() -> None:
     for d in (OBJ_DIR, LIB_DIR, BIN_DIR):
         shutil.rmtree(d, ignore_errors=True)
@@ -160,6 +172,8 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("-d", "--debug", action="store_true",
                     help="CLIs with the CPU-verify switch on (the reference's Debug build)")
     ap.add_argument("--no-apps", action="store_true", help="library only (same as -t w8a8)")
+    ap.add_argument("--apps-only", action="store_true",
+                    help="CLIs only, linked against the library already built in lib/")
     ap.add_argument("-v", "--verbose", action="store_true")
     args = ap.parse_args(argv)
     targets = [t for t in args.gpu_targets.replace(",", ";").split(";") if t]
@@ -169,8 +183,14 @@ def main(argv: list[str] | None = None) -> int:
         return 1
     if args.clean:
         clean()
-    lib = build_library(verbose=args.verbose, jobs=args.jobs)
-    print(f"built {lib}")
+    if args.apps_only:
+        if not LIB_PATH.exists():
+            print(f"[ERROR] --apps-only needs {LIB_PATH} (build the library first)",
+                  file=sys.stderr)
+            return 1
+    else:
+        lib = build_library(verbose=args.verbose, jobs=args.jobs)
+        print(f"built {lib}")
     if args.no_apps or args.target == "w8a8":
         return 0
     only = None if args.target == "all_samples" else args.target

@@ -9,6 +9,7 @@
 #   -i, --include-dir  accepted, unused (no rocWMMA headers are needed)
 #   -c, --clean        remove previous build outputs first
 #   -d, --debug        CLIs with the CPU-verify switch on
+#   --apps-only        CLIs only, against the library already in lib/
 #   -v, --verbose      print every compiler command
 #   -h, --help         this help
 set -euo pipefail

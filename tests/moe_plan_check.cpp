@@ -19,6 +19,7 @@
 #include "../optimized_rocwmma_samples_amd/csrc/gemm_i8_grouped_kernel.hpp"
 
 #include <cstdio>
+#include <cstdlib>
 #include <random>
 #include <vector>
 
@@ -83,8 +84,10 @@ static int check(const std::vector<uint32_t>& rows, uint32_t n, uint32_t nk, uin
     return 0;
 }
 
-int main()
+// argv[1]: random cases (default 800; the sanitizer build runs fewer)
+int main(int argc, char** argv)
 {
+    const int iters = argc > 1 ? std::atoi(argv[1]) : 800;
     using Main     = Cfg<256, 256, 128, 2, 2, 4, 4, 16>;
     using MainWide = Cfg<128, 512, 128, 2, 1, 8, 4, 16>;
     using Silu     = Cfg<256, 256, 128, 2, 4, 2, 4, 16>;
@@ -96,7 +99,7 @@ int main()
     const uint32_t ns[]      = {256, 300, 512, 768, 1000, 1536, 2048};
     const uint32_t cuss[]    = {256, 80, 7, 2, 0};
     long           cases     = 0;
-    for(int it = 0; it < 800; ++it) {
+    for(int it = 0; it < iters; ++it) {
         const size_t          E = 1 + rng() % 24;
         std::vector<uint32_t> rows(E);
         for(auto& r : rows)

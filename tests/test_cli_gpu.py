@@ -69,3 +69,18 @@ def test_runner_end_to_end(gpu, tmp_path):
     assert rows[0] == ["sample", "description", "metric", "value", "unit", "pct_peak"]
     assert {r[0] for r in rows[1:]} == {"rocwmma_smoothquant", "rocwmma_topk_softmax"}
     assert all(float(r[3]) > 0 for r in rows[1:])
+
+
+@pytest.mark.parametrize("name,args", [("rocwmma_smoothquant", ["256", "4096"]),
+                                       ("rocwmma_gemm_quantized", ["512", "512", "512"])])
+def test_debug_build_verifies_by_default(gpu, name, args):
+    """The debug build (build.sh -d) checks against the CPU without --verify."""
+    exe = BIN / "debug" / name
+    assert exe.exists(), f"{exe} not built"
+    print(f"running debug {name} {' '.join(args)}", flush=True)
+    r = subprocess.run([str(exe), *args], stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                       text=True, timeout=110)
+    assert r.returncode == 0, r.stdout[-3000:]
+    lines = r.stdout.splitlines()
+    assert any(l.strip().startswith("PASSED") for l in lines), r.stdout[-3000:]
+    assert not any(l.strip().startswith("FAILED") for l in lines), r.stdout[-3000:]
