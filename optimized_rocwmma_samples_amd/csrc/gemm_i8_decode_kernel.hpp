@@ -130,10 +130,10 @@ __device__ __forceinline__ void fuse_quantize(const FuseQ& fq, uint32_t m, uint3
                 if(c < chunks) {
                     float v[8];
                     smoothed(r, c, v);
-                    pk.x = (int)pack4_i8(quant_i8(v[0], inv[r], fq.qmax), quant_i8(v[1], inv[r], fq.qmax),
-                                         quant_i8(v[2], inv[r], fq.qmax), quant_i8(v[3], inv[r], fq.qmax));
-                    pk.y = (int)pack4_i8(quant_i8(v[4], inv[r], fq.qmax), quant_i8(v[5], inv[r], fq.qmax),
-                                         quant_i8(v[6], inv[r], fq.qmax), quant_i8(v[7], inv[r], fq.qmax));
+                    pk.x = (int)cvt_pack4_i8(quant_f(v[0], inv[r], fq.qmax), quant_f(v[1], inv[r], fq.qmax),
+                                             quant_f(v[2], inv[r], fq.qmax), quant_f(v[3], inv[r], fq.qmax));
+                    pk.y = (int)cvt_pack4_i8(quant_f(v[4], inv[r], fq.qmax), quant_f(v[5], inv[r], fq.qmax),
+                                             quant_f(v[6], inv[r], fq.qmax), quant_f(v[7], inv[r], fq.qmax));
                     if(first_block) *reinterpret_cast<v2i*>(fq.q + (size_t)r * k + c * 8) = pk;
                 }
                 *reinterpret_cast<v2i*>(qa + r * fq.pitch + c * 8) = pk;

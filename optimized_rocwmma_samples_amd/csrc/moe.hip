@@ -490,10 +490,10 @@ __global__ void __launch_bounds__(kSqThreads) silu_quant_vec_kernel(SiluRows p)
     for(int j = 0; j < CPL; ++j) {
         const float* v = pv + j * 8;
         v2i          pk;
-        pk.x = (int)pack4_i8(quant_i8(v[0], inv, qmax), quant_i8(v[1], inv, qmax),
-                             quant_i8(v[2], inv, qmax), quant_i8(v[3], inv, qmax));
-        pk.y = (int)pack4_i8(quant_i8(v[4], inv, qmax), quant_i8(v[5], inv, qmax),
-                             quant_i8(v[6], inv, qmax), quant_i8(v[7], inv, qmax));
+        pk.x = (int)cvt_pack4_i8(quant_f(v[0], inv, qmax), quant_f(v[1], inv, qmax),
+                                 quant_f(v[2], inv, qmax), quant_f(v[3], inv, qmax));
+        pk.y = (int)cvt_pack4_i8(quant_f(v[4], inv, qmax), quant_f(v[5], inv, qmax),
+                                 quant_f(v[6], inv, qmax), quant_f(v[7], inv, qmax));
         __builtin_amdgcn_raw_buffer_store_b64(
             pk, rq, (valid && col[j] != kOob) ? row * p.ldq + col[j] : kOob, 0, 0);
     }
@@ -615,10 +615,10 @@ __global__ void __launch_bounds__(kSqThreads) silu_requant_kernel(SiluRequant p)
                     v[2 * x + 1] = half_bits_to_float(hw[x] >> 16) * sv[2 * x + 1];
                 }
                 v2i pk;
-                pk.x = (int)pack4_i8(quant_i8(v[0], inv, qmax), quant_i8(v[1], inv, qmax),
-                                     quant_i8(v[2], inv, qmax), quant_i8(v[3], inv, qmax));
-                pk.y = (int)pack4_i8(quant_i8(v[4], inv, qmax), quant_i8(v[5], inv, qmax),
-                                     quant_i8(v[6], inv, qmax), quant_i8(v[7], inv, qmax));
+                pk.x = (int)cvt_pack4_i8(quant_f(v[0], inv, qmax), quant_f(v[1], inv, qmax),
+                                         quant_f(v[2], inv, qmax), quant_f(v[3], inv, qmax));
+                pk.y = (int)cvt_pack4_i8(quant_f(v[4], inv, qmax), quant_f(v[5], inv, qmax),
+                                         quant_f(v[6], inv, qmax), quant_f(v[7], inv, qmax));
                 __builtin_amdgcn_raw_buffer_store_b64(
                     pk, rq, col[j] != kOob ? row * p.ldq + col[j] : kOob, 0, 0);
             }

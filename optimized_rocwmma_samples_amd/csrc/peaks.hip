@@ -4,8 +4,10 @@
 //     back to back on operands held in registers, nothing else in the loop --
 //     the matrix-core rate the chip sustains at the clock it holds under that
 //     load;
-//   * a streaming copy: 16 bytes per lane per access, several accesses in
-//     flight per lane -- the HBM rate a plain read + write stream reaches;
+//   * streams (read only, copy, 2:1): 16 bytes per lane per access, 8 or 16
+//     accesses in flight per lane, grid-stride or contiguous per block, plain
+//     or non-temporal loads -- the HBM rate a plain stream reaches, as the
+//     best over those forms and the launch shapes the host sweeps;
 //   * an empty kernel -- the launch floor of back-to-back launches (timed by
 //     the caller in a captured graph).
 #include <hip/hip_runtime.h>
@@ -95,38 +97,83 @@ __global__ void __launch_bounds__(kThreads16) peak_mfma16_i8_kernel(int iters, i
     if(lane == 0) sink[blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64] = s;
 }
 
-// Grid-stride stream over `n16` 16-byte source chunks, kUnroll loads in
-// flight per lane (the best of a sweep over 2-16 loads, 256-1024 threads and
-// 1-16 blocks per CU on MI355X).  MODE 0 reads only; MODE 1 copies each chunk;
-// MODE 2 writes 8 bytes per 16 read (the quantizer's fp16 -> int8 ratio).
-// Stores are non-temporal (the faster form in the same sweep).
-constexpr int kUnroll        = 8;
-constexpr int kStreamThreads = 512;
+// Stream over `n16` 16-byte source chunks with kUnroll (U) loads in flight
+// per lane.  MODE 0 reads only; MODE 1 copies each chunk; MODE 2 writes 8
+// bytes per 16 read (the quantizer's fp16 -> int8 ratio).  Stores are
+// non-temporal.  Two partitions of the chunks over the grid:
+//   CONTIG = false: grid stride (lane i of the grid takes chunks i, i + G, ...);
+//   CONTIG = true : block b takes the contiguous range [b n16 / B, (b+1) n16 / B)
+//                   and walks it a wave instruction (1 KiB) at a time, the
+//                   way the quantizer walks its rows;
+// NT: loads with the non-temporal hint as well.  The host takes the best of
+// these forms over several block counts and block sizes, so a kernel of the
+// path that streams faster than every one of them means the ceiling is
+// still low, not that the path beats the memory system.
 typedef int v2i __attribute__((ext_vector_type(2)));
+constexpr int kStreamThreadsMax = 1024;
 
-template <int MODE>
-__global__ void __launch_bounds__(kStreamThreads) peak_stream_kernel(const v4i* __restrict__ src,
-                                                                     void* __restrict__ dst,
-                                                                     size_t n16, int* sink)
+template <int MODE, bool NT>
+__device__ __forceinline__ v4i stream_load(const v4i* p)
 {
-    const size_t stride = (size_t)gridDim.x * kStreamThreads;
-    size_t       i      = (size_t)blockIdx.x * kStreamThreads + threadIdx.x;
-    v4i          acc    = {0, 0, 0, 0};
+    if constexpr(NT)
+        return __builtin_nontemporal_load(p);
+    else
+        return *p;
+}
+
+template <int MODE, bool CONTIG, int U, bool NT>
+__global__ void __launch_bounds__(kStreamThreadsMax) peak_stream_kernel(
+    const v4i* __restrict__ src, void* __restrict__ dst, size_t n16, int* sink)
+{
+    const size_t threads = blockDim.x;
+    size_t       i, end, stride;
+    if constexpr(CONTIG) {
+        i      = (size_t)blockIdx.x * n16 / gridDim.x + threadIdx.x;
+        end    = (size_t)(blockIdx.x + 1) * n16 / gridDim.x;
+        stride = threads;
+    } else {
+        i      = (size_t)blockIdx.x * threads + threadIdx.x;
+        end    = n16;
+        stride = (size_t)gridDim.x * threads;
+    }
+    v4i  acc = {0, 0, 0, 0};
     auto put = [&](size_t j, const v4i& v) {
         if constexpr(MODE == 1) __builtin_nontemporal_store(v, static_cast<v4i*>(dst) + j);
         if constexpr(MODE == 2)
             __builtin_nontemporal_store(v2i{v.x ^ v.y, v.z ^ v.w}, static_cast<v2i*>(dst) + j);
         if constexpr(MODE == 0) acc ^= v;
     };
-    for(; i + (kUnroll - 1) * stride < n16; i += kUnroll * stride) {
-        v4i v[kUnroll];
+    for(; i + (U - 1) * stride < end; i += U * stride) {
+        v4i v[U];
 #pragma unroll
-        for(int u = 0; u < kUnroll; ++u) v[u] = src[i + u * stride];
+        for(int u = 0; u < U; ++u) v[u] = stream_load<MODE, NT>(src + i + u * stride);
 #pragma unroll
-        for(int u = 0; u < kUnroll; ++u) put(i + u * stride, v[u]);
+        for(int u = 0; u < U; ++u) put(i + u * stride, v[u]);
     }
-    for(; i < n16; i += stride) put(i, src[i]);
+    for(; i < end; i += stride) put(i, stream_load<MODE, NT>(src + i));
     if(MODE == 0 && acc.x == 0x13579BDF && acc.y == acc.z) sink[0] = acc.w; // keeps the loads live
+}
+
+// variant bits: 0 CONTIG, 1 U = 16 (else 8), 2 NT loads
+template <int MODE>
+hipError_t launch_stream(const v4i* s, void* d, size_t n16, uint32_t blocks, uint32_t threads,
+                         int variant, int* sink, hipStream_t st)
+{
+#define W8A8_PEAK_STREAM(C, U, N)                                                                 \
+    hipLaunchKernelGGL((peak_stream_kernel<MODE, C, U, N>), dim3(blocks), dim3(threads), 0, st, s, \
+                       d, n16, sink)
+    switch(variant) {
+    case 0: W8A8_PEAK_STREAM(false, 8, false); break;
+    case 1: W8A8_PEAK_STREAM(true, 8, false); break;
+    case 2: W8A8_PEAK_STREAM(false, 16, false); break;
+    case 3: W8A8_PEAK_STREAM(true, 16, false); break;
+    case 4: W8A8_PEAK_STREAM(false, 8, true); break;
+    case 5: W8A8_PEAK_STREAM(true, 8, true); break;
+    case 6: W8A8_PEAK_STREAM(false, 16, true); break;
+    default: W8A8_PEAK_STREAM(true, 16, true); break;
+    }
+#undef W8A8_PEAK_STREAM
+    return hipGetLastError();
 }
 
 __global__ void peak_empty_kernel() {}
@@ -160,26 +207,23 @@ int w8a8_peak_mfma(uint32_t blocks, uint32_t iters, int mode, int* sink, hipStre
 }
 
 // Stream `bytes` of src (a multiple of 16; src, dst 16-byte aligned) with
-// `blocks` blocks: mode 0 read only (dst unused, sink: one int), 1 copy to
-// dst (`bytes` written), 2 write bytes / 2 to dst.
-int w8a8_peak_stream(const void* src, void* dst, size_t bytes, uint32_t blocks, int mode,
-                     int* sink, hipStream_t stream)
+// `blocks` blocks of `threads` threads (64-1024, a multiple of 64) in the
+// form `variant` (0-7: bit 0 contiguous ranges per block, bit 1 16 loads in
+// flight per lane instead of 8, bit 2 non-temporal loads): mode 0 read only
+// (dst unused, sink: one int), 1 copy to dst (`bytes` written), 2 write
+// bytes / 2 to dst.
+int w8a8_peak_stream(const void* src, void* dst, size_t bytes, uint32_t blocks, uint32_t threads,
+                     int variant, int mode, int* sink, hipStream_t stream)
 {
     if(!src || bytes % 16 || blocks == 0 || reinterpret_cast<uintptr_t>(src) % 16
        || (mode != 0 && (!dst || reinterpret_cast<uintptr_t>(dst) % 16)) || (mode == 0 && !sink)
-       || mode < 0 || mode > 2)
+       || mode < 0 || mode > 2 || threads < 64 || threads > kStreamThreadsMax || threads % 64
+       || variant < 0 || variant > 7)
         return (int)hipErrorInvalidValue;
     const v4i* s = static_cast<const v4i*>(src);
-    if(mode == 0)
-        hipLaunchKernelGGL(peak_stream_kernel<0>, dim3(blocks), dim3(kStreamThreads), 0, stream, s,
-                           dst, bytes / 16, sink);
-    else if(mode == 1)
-        hipLaunchKernelGGL(peak_stream_kernel<1>, dim3(blocks), dim3(kStreamThreads), 0, stream, s,
-                           dst, bytes / 16, sink);
-    else
-        hipLaunchKernelGGL(peak_stream_kernel<2>, dim3(blocks), dim3(kStreamThreads), 0, stream, s,
-                           dst, bytes / 16, sink);
-    return (int)hipGetLastError();
+    if(mode == 0) return (int)launch_stream<0>(s, dst, bytes / 16, blocks, threads, variant, sink, stream);
+    if(mode == 1) return (int)launch_stream<1>(s, dst, bytes / 16, blocks, threads, variant, sink, stream);
+    return (int)launch_stream<2>(s, dst, bytes / 16, blocks, threads, variant, sink, stream);
 }
 
 int w8a8_peak_empty(hipStream_t stream)

@@ -109,19 +109,6 @@ rmsq_stream_kernel(NormRows p, uint32_t iters)
         return *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(lds) + l_off
                                                 + which * kTotal * 4 + j * 2048 + half * 1024);
     };
-    // fp16 y of chunk j (as floats), from the packed half(v) / x values
-    auto normalised = [&](const v4i& u16, int j, float rstd, float (&y)[8]) {
-        const float4 g0 = lds4(j, 0, 0);
-        const float4 g1 = lds4(j, 1, 0);
-        const float  g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-        const uint32_t w[4] = {(uint32_t)u16.x, (uint32_t)u16.y, (uint32_t)u16.z, (uint32_t)u16.w};
-#pragma unroll
-        for(int e = 0; e < 8; ++e) {
-            const float u = half_bits_to_float((w[e / 2] >> (16 * (e % 2))) & 0xFFFFu);
-            y[e]          = half_bits_to_float(float_to_half_bits_2step((u * rstd) * g[e]));
-        }
-    };
-
     int  slot    = 0;
     auto reduce  = [&](float v, bool is_max) {
         v = is_max ? wave_max(v) : wave_sum(v);
@@ -168,28 +155,39 @@ rmsq_stream_kernel(NormRows p, uint32_t iters)
         ss                = reduce(ss, false);
         const float rstd  = rsqrtf(ss / (float)n + p.eps);
 
-        // 2. y = half((u * rstd) * gamma); optional y store; absmax of y * s
+        // 2. y = half((u * rstd) * gamma) as packed fp16 pairs (u * rstd in
+        //    one v_fma_mix_f32 from the packed fp16 u); optional y store;
+        //    p = y * s (again one v_fma_mix_f32 from the packed y) kept in
+        //    registers for the quantize pass, and its absmax
         asm volatile("" : "+v"(l_off));
         float amax = 0.f;
+        float pv[QUANT ? CPL * 8 : 1];
 #pragma unroll
         for(int j = 0; j < CPL; ++j) {
-            float y[8];
-            normalised(x[j], j, rstd, y);
-            if constexpr(YOUT) {
-                v4i yh;
-                yh.x = (int)pack_half2(y[0], y[1]);
-                yh.y = (int)pack_half2(y[2], y[3]);
-                yh.z = (int)pack_half2(y[4], y[5]);
-                yh.w = (int)pack_half2(y[6], y[7]);
+            const float4   g0   = lds4(j, 0, 0);
+            const float4   g1   = lds4(j, 1, 0);
+            const float    g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+            const uint32_t w[4] = {(uint32_t)x[j].x, (uint32_t)x[j].y, (uint32_t)x[j].z,
+                                   (uint32_t)x[j].w};
+            uint32_t       yh[4];
+#pragma unroll
+            for(int e = 0; e < 4; ++e)
+                yh[e] = pack_half2(mul_h16_f32<false>(w[e], rstd) * g[2 * e],
+                                   mul_h16_f32<true>(w[e], rstd) * g[2 * e + 1]);
+            if constexpr(YOUT)
                 __builtin_amdgcn_raw_buffer_store_b128(
-                    yh, ry, (valid && coff[j] != kOob) ? r * p.ldy * 2 + coff[j] * 2 : kOob, 0, 0);
-            }
+                    v4i{(int)yh[0], (int)yh[1], (int)yh[2], (int)yh[3]}, ry,
+                    (valid && coff[j] != kOob) ? r * p.ldy * 2 + coff[j] * 2 : kOob, 0, 0);
             if constexpr(QUANT) {
-                const float4 s0 = lds4(j, 0, 1);
-                const float4 s1 = lds4(j, 1, 1);
+                const float4 s0   = lds4(j, 0, 1);
+                const float4 s1   = lds4(j, 1, 1);
                 const float  s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
 #pragma unroll
-                for(int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(y[e] * s[e]));
+                for(int e = 0; e < 8; e += 2) {
+                    pv[j * 8 + e]     = mul_h16_f32<false>(yh[e / 2], s[e]);
+                    pv[j * 8 + e + 1] = mul_h16_f32<true>(yh[e / 2], s[e + 1]);
+                    amax = fmaxf(fmaxf(amax, fabsf(pv[j * 8 + e])), fabsf(pv[j * 8 + e + 1]));
+                }
             }
         }
         if constexpr(QUANT) {
@@ -198,20 +196,15 @@ rmsq_stream_kernel(NormRows p, uint32_t iters)
             const float rs    = amax / qmax;
             if(valid && part == 0 && lane == 0) p.r[r] = rs;
             const float inv   = rs > 0.f ? 1.f / rs : 0.f;
-            // 3. quantize, recomputing y and y * s from registers and LDS
-            asm volatile("" : "+v"(l_off));
+            // 3. quantize the kept products
 #pragma unroll
             for(int j = 0; j < CPL; ++j) {
-                float y[8];
-                normalised(x[j], j, rstd, y);
-                const float4 s0 = lds4(j, 0, 1);
-                const float4 s1 = lds4(j, 1, 1);
-                const float  s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-                v2i pk;
-                pk.x = (int)pack4_i8(quant_i8(y[0] * s[0], inv, qmax), quant_i8(y[1] * s[1], inv, qmax),
-                                     quant_i8(y[2] * s[2], inv, qmax), quant_i8(y[3] * s[3], inv, qmax));
-                pk.y = (int)pack4_i8(quant_i8(y[4] * s[4], inv, qmax), quant_i8(y[5] * s[5], inv, qmax),
-                                     quant_i8(y[6] * s[6], inv, qmax), quant_i8(y[7] * s[7], inv, qmax));
+                const float* v = pv + j * 8;
+                v2i          pk;
+                pk.x = (int)cvt_pack4_i8(quant_f(v[0], inv, qmax), quant_f(v[1], inv, qmax),
+                                         quant_f(v[2], inv, qmax), quant_f(v[3], inv, qmax));
+                pk.y = (int)cvt_pack4_i8(quant_f(v[4], inv, qmax), quant_f(v[5], inv, qmax),
+                                         quant_f(v[6], inv, qmax), quant_f(v[7], inv, qmax));
                 __builtin_amdgcn_raw_buffer_store_b64(
                     pk, rq, (valid && coff[j] != kOob) ? r * p.ldq + coff[j] : kOob, 0, 0);
             }

@@ -34,6 +34,8 @@ namespace w8a8 {
 namespace {
 
 constexpr int kSqThreads = 256; // 4 waves
+// Cache-policy operand of the buffer builtins: the NT (non-temporal) bit.
+constexpr int kCpolNt = 2;
 constexpr int kSqWaves   = kSqThreads / kWave;
 
 struct RowSrc {
@@ -94,14 +96,14 @@ __global__ void __launch_bounds__(kSqThreads) sq_rows_kernel(QuantRows p)
                 const uint4 raw = *reinterpret_cast<const uint4*>(src.x + c);
                 const float4 s0 = *reinterpret_cast<const float4*>(src.s + c);
                 const float4 s1 = *reinterpret_cast<const float4*>(src.s + c + 4);
-                pv[j * 8 + 0] = half_bits_to_float(raw.x & 0xFFFFu) * s0.x;
-                pv[j * 8 + 1] = half_bits_to_float(raw.x >> 16) * s0.y;
-                pv[j * 8 + 2] = half_bits_to_float(raw.y & 0xFFFFu) * s0.z;
-                pv[j * 8 + 3] = half_bits_to_float(raw.y >> 16) * s0.w;
-                pv[j * 8 + 4] = half_bits_to_float(raw.z & 0xFFFFu) * s1.x;
-                pv[j * 8 + 5] = half_bits_to_float(raw.z >> 16) * s1.y;
-                pv[j * 8 + 6] = half_bits_to_float(raw.w & 0xFFFFu) * s1.z;
-                pv[j * 8 + 7] = half_bits_to_float(raw.w >> 16) * s1.w;
+                pv[j * 8 + 0] = mul_h16_f32<false>(raw.x, s0.x);
+                pv[j * 8 + 1] = mul_h16_f32<true>(raw.x, s0.y);
+                pv[j * 8 + 2] = mul_h16_f32<false>(raw.y, s0.z);
+                pv[j * 8 + 3] = mul_h16_f32<true>(raw.y, s0.w);
+                pv[j * 8 + 4] = mul_h16_f32<false>(raw.z, s1.x);
+                pv[j * 8 + 5] = mul_h16_f32<true>(raw.z, s1.y);
+                pv[j * 8 + 6] = mul_h16_f32<false>(raw.w, s1.z);
+                pv[j * 8 + 7] = mul_h16_f32<true>(raw.w, s1.w);
             } else {
 #pragma unroll
                 for(int e = 0; e < 8; ++e)
@@ -132,18 +134,18 @@ __global__ void __launch_bounds__(kSqThreads) sq_rows_kernel(QuantRows p)
 #pragma unroll
     for(int j = 0; j < CPL; ++j) {
         const uint32_t c = base + j * (8 * kWave);
-        int            qi[8];
-#pragma unroll
-        for(int e = 0; e < 8; ++e) qi[e] = quant_i8(pv[j * 8 + e], inv, qmax);
+        const float*   v = pv + j * 8;
         if(VEC && c + 8 <= n) {
             uint2 packed;
-            packed.x = pack4_i8(qi[0], qi[1], qi[2], qi[3]);
-            packed.y = pack4_i8(qi[4], qi[5], qi[6], qi[7]);
+            packed.x = cvt_pack4_i8(quant_f(v[0], inv, qmax), quant_f(v[1], inv, qmax),
+                                    quant_f(v[2], inv, qmax), quant_f(v[3], inv, qmax));
+            packed.y = cvt_pack4_i8(quant_f(v[4], inv, qmax), quant_f(v[5], inv, qmax),
+                                    quant_f(v[6], inv, qmax), quant_f(v[7], inv, qmax));
             *reinterpret_cast<uint2*>(qrow + c) = packed;
         } else {
 #pragma unroll
             for(int e = 0; e < 8; ++e)
-                if(c + e < n) qrow[c + e] = (int8_t)qi[e];
+                if(c + e < n) qrow[c + e] = (int8_t)quant_i8(v[e], inv, qmax);
         }
     }
 }
@@ -186,7 +188,12 @@ __global__ void __launch_bounds__(kSqThreads) sq_twopass_kernel(QuantRows p)
 // Results are bit-identical to sq_rows_kernel: same per-element operations.
 // ---------------------------------------------------------------------------
 
-template <int CPL, int WPR, int THREADS>
+// Bytes of x or q one streaming launch addresses at most (below the kernel's
+// out-of-range row offset, 0x7FFFFFF0).
+constexpr uint64_t kPanelBytes = 0x7F000000ull;
+
+// NT: x is read with the non-temporal cache policy (it is read once).
+template <int CPL, int WPR, int THREADS, bool NT = false>
 __global__ void __launch_bounds__(THREADS) sq_stream_kernel(QuantRows p, uint32_t iters)
 {
     constexpr int kStreamThreads = THREADS;
@@ -214,51 +221,62 @@ __global__ void __launch_bounds__(THREADS) sq_stream_kernel(QuantRows p, uint32_
     const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
         p.q, 0, (int)((p.rows - 1) * p.ldq + n), 0x00020000);
 
-    uint32_t coff[CPL]; // byte offset of each chunk in a row, or kOobOff
+    // Offsets of a chunk = the row's base + the chunk's column offset.  A
+    // column past N has offset kOobOff and a row past the end the base
+    // kOobRow: every sum of an in-range row and column stays below the
+    // buffer's size (< 2^31), and every other sum lies in [2^31, 2^32) (no
+    // wrap), past the buffer: one add per chunk, no select.
+    // (The host keeps both buffers under kPanelBytes < kOobRow.)
+    constexpr uint32_t kOobRow = 0x7FFFFFF0u;
+    uint32_t coff[CPL]; // q byte offset of each chunk in a row (its column), or kOobOff
+    uint32_t xoff[CPL]; // x byte offset of each chunk in a row, or kOobOff
 #pragma unroll
     for(int j = 0; j < CPL; ++j) {
         const uint32_t c = base + j * (8 * kWave);
         coff[j]          = c < n ? c : kOobOff;
+        xoff[j]          = c < n ? 2 * c : kOobOff;
     }
 
     using Row = v4i[CPL];
     Row  xa, xb;
     auto load_row = [&](Row& dst, uint32_t r) {
-        const bool     ok   = r < p.rows;
-        const uint32_t roff = r * p.ldx * 2;
+        const uint32_t roff = r < p.rows ? r * p.ldx * 2 : kOobRow;
 #pragma unroll
         for(int j = 0; j < CPL; ++j)
-            dst[j] = __builtin_amdgcn_raw_buffer_load_b128(
-                rx, (ok && coff[j] != kOobOff) ? roff + coff[j] * 2 : kOobOff, 0, 0);
+            dst[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, roff + xoff[j], 0,
+                                                           NT ? kCpolNt : 0);
     };
     // LDS offset of this lane's s values; made opaque once per row (below) so
     // the compiler re-reads s from LDS instead of pinning CPL*8 registers to it
     // for the whole kernel, which would cap the CU at one block
     uint32_t s_off = (part * kSpan + lane * 4) * 4;
-    auto smoothed = [&](const v4i& raw, int j, float (&v)[8]) {
+    // the 8 products x*s of chunk j (mul_h16_f32: one instruction each)
+    auto smoothed = [&](const v4i& raw, int j, float* v) {
         const float4 s0 = *reinterpret_cast<const float4*>(
             reinterpret_cast<const char*>(s_lds) + s_off + j * 2048);
         const float4 s1 = *reinterpret_cast<const float4*>(
             reinterpret_cast<const char*>(s_lds) + s_off + j * 2048 + 1024);
-        v[0] = half_bits_to_float((uint32_t)raw.x & 0xFFFFu) * s0.x;
-        v[1] = half_bits_to_float((uint32_t)raw.x >> 16) * s0.y;
-        v[2] = half_bits_to_float((uint32_t)raw.y & 0xFFFFu) * s0.z;
-        v[3] = half_bits_to_float((uint32_t)raw.y >> 16) * s0.w;
-        v[4] = half_bits_to_float((uint32_t)raw.z & 0xFFFFu) * s1.x;
-        v[5] = half_bits_to_float((uint32_t)raw.z >> 16) * s1.y;
-        v[6] = half_bits_to_float((uint32_t)raw.w & 0xFFFFu) * s1.z;
-        v[7] = half_bits_to_float((uint32_t)raw.w >> 16) * s1.w;
+        v[0] = mul_h16_f32<false>((uint32_t)raw.x, s0.x);
+        v[1] = mul_h16_f32<true>((uint32_t)raw.x, s0.y);
+        v[2] = mul_h16_f32<false>((uint32_t)raw.y, s0.z);
+        v[3] = mul_h16_f32<true>((uint32_t)raw.y, s0.w);
+        v[4] = mul_h16_f32<false>((uint32_t)raw.z, s1.x);
+        v[5] = mul_h16_f32<true>((uint32_t)raw.z, s1.y);
+        v[6] = mul_h16_f32<false>((uint32_t)raw.w, s1.z);
+        v[7] = mul_h16_f32<true>((uint32_t)raw.w, s1.w);
     };
     auto process = [&](const Row& x, uint32_t r, int parity) {
         asm volatile("" : "+v"(s_off));
-        // columns past N hold x = 0 and s = 0: they add nothing to the max
+        // columns past N hold x = 0 and s = 0: they add nothing to the max.
+        // The products stay in registers for the quantize pass.
+        float pv[CPL * 8];
         float amax = 0.f;
 #pragma unroll
         for(int j = 0; j < CPL; ++j) {
-            float v[8];
-            smoothed(x[j], j, v);
+            smoothed(x[j], j, pv + j * 8);
 #pragma unroll
-            for(int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+            for(int e = 0; e < 8; e += 2)
+                amax = fmaxf(fmaxf(amax, fabsf(pv[j * 8 + e])), fabsf(pv[j * 8 + e + 1]));
         }
         amax = wave_max(amax);
         if constexpr(WPR > 1) {
@@ -267,25 +285,21 @@ __global__ void __launch_bounds__(THREADS) sq_stream_kernel(QuantRows p, uint32_
 #pragma unroll
             for(int w = 0; w < WPR; ++w) amax = fmaxf(amax, red[parity][grp * WPR + w]);
         }
-        // recompute x*s in the quantize pass rather than keep CPL*8 products live
-        asm volatile("" : "+v"(s_off));
         const bool  valid = r < p.rows;
         const float qmax  = p.qmax;
         const float rs    = amax / qmax;
         if(valid && part == 0 && lane == 0) p.r[r] = rs;
         const float    inv  = rs > 0.f ? 1.f / rs : 0.f;
-        const uint32_t qoff = r * p.ldq;
+        const uint32_t qoff = valid ? r * p.ldq : kOobRow;
 #pragma unroll
         for(int j = 0; j < CPL; ++j) {
-            float v[8];
-            smoothed(x[j], j, v);
-            v2i pk;
-            pk.x = (int)pack4_i8(quant_i8(v[0], inv, qmax), quant_i8(v[1], inv, qmax),
-                                 quant_i8(v[2], inv, qmax), quant_i8(v[3], inv, qmax));
-            pk.y = (int)pack4_i8(quant_i8(v[4], inv, qmax), quant_i8(v[5], inv, qmax),
-                                 quant_i8(v[6], inv, qmax), quant_i8(v[7], inv, qmax));
-            __builtin_amdgcn_raw_buffer_store_b64(
-                pk, rq, (valid && coff[j] != kOobOff) ? qoff + coff[j] : kOobOff, 0, 0);
+            const float* v = pv + j * 8;
+            v2i          pk;
+            pk.x = (int)cvt_pack4_i8(quant_f(v[0], inv, qmax), quant_f(v[1], inv, qmax),
+                                     quant_f(v[2], inv, qmax), quant_f(v[3], inv, qmax));
+            pk.y = (int)cvt_pack4_i8(quant_f(v[4], inv, qmax), quant_f(v[5], inv, qmax),
+                                     quant_f(v[6], inv, qmax), quant_f(v[7], inv, qmax));
+            __builtin_amdgcn_raw_buffer_store_b64(pk, rq, qoff + coff[j], 0, 0);
         }
     };
 
@@ -339,7 +353,7 @@ __global__ void __launch_bounds__(THREADS) sq_stream_kernel(QuantRows p, uint32_
 
 // THREADS per block, BPC resident blocks per CU (the grid is BPC x CUs, each
 // block walking rows with a grid stride).
-template <int CPL, int WPR, int THREADS, int BPC = 1>
+template <int CPL, int WPR, int THREADS, int BPC = 1, bool NT = false>
 hipError_t launch_stream(const QuantRows& p, hipStream_t stream)
 {
     constexpr int  kGroups = THREADS / kWave / WPR;
@@ -356,14 +370,19 @@ hipError_t launch_stream(const QuantRows& p, hipStream_t stream)
         static std::once_flag once;
         std::call_once(once, [] {
             (void)hipFuncSetAttribute(
-                reinterpret_cast<const void*>(sq_stream_kernel<CPL, WPR, THREADS>),
+                reinterpret_cast<const void*>(sq_stream_kernel<CPL, WPR, THREADS, NT>),
                 hipFuncAttributeMaxDynamicSharedMemorySize, 131072);
             (void)hipGetLastError();
         });
     }
-    // x is addressed through a 32-bit buffer offset: launch row panels whose
-    // x span stays under 2 GiB
-    const uint32_t panel = (uint32_t)std::min<uint64_t>(p.rows, 0x7FFFFFFFull / ((uint64_t)p.ldx * 2));
+    // x and q are addressed through 32-bit buffer offsets: launch row panels
+    // whose x and q spans both stay under kPanelBytes (the kernel's
+    // out-of-range sentinels lie above it)
+    const uint64_t rows_x = kPanelBytes / ((uint64_t)p.ldx * 2);
+    const uint64_t rows_q = kPanelBytes / (uint64_t)p.ldq;
+    // (a single row spans only its own n columns, whatever the strides)
+    const uint32_t panel  = (uint32_t)std::max<uint64_t>(
+        1, std::min<uint64_t>(p.rows, std::min(rows_x, rows_q)));
     for(uint32_t r0 = 0; r0 < p.rows; r0 += panel) {
         QuantRows q = p;
         q.rows      = std::min(panel, p.rows - r0);
@@ -373,7 +392,7 @@ hipError_t launch_stream(const QuantRows& p, hipStream_t stream)
         const uint32_t need   = (q.rows + kGroups - 1) / kGroups;
         const uint32_t blocks = std::max<uint32_t>(1, std::min<uint32_t>(need, (uint32_t)max_blocks));
         const uint32_t iters  = (q.rows + blocks * kGroups - 1) / (blocks * kGroups);
-        hipLaunchKernelGGL((sq_stream_kernel<CPL, WPR, THREADS>), dim3(blocks), dim3(THREADS), lds,
+        hipLaunchKernelGGL((sq_stream_kernel<CPL, WPR, THREADS, NT>), dim3(blocks), dim3(THREADS), lds,
                            stream, q, iters);
         const hipError_t e = hipGetLastError();
         if(e != hipSuccess) return e;
@@ -415,17 +434,26 @@ hipError_t dispatch(const QuantRows& p, hipStream_t stream)
             if(n <= 512) return launch_stream<1, 1, 512>(p, stream);
             if(n <= 1024) return launch_stream<2, 1, 512>(p, stream);
             if(n <= 2048) return launch_stream<4, 1, 512>(p, stream);
-            // 8192 to 32767 rows: 4 blocks of 256 threads per CU keep more
-            // rows in flight (8192 x 4096 cold: 21.8 -> 20.9 us); at 2048
-            // rows, and from 32768 rows on (131072 x 4096: 312 -> 293 us),
-            // the single 512-thread block stays ahead
-            if(n <= 4096 && p.rows >= 8192 && p.rows < 32768) return launch_stream<4, 2, 256, 4>(p, stream);
-            if(n <= 4096) return launch_stream<4, 2, 512>(p, stream);
+            // Up to 4096 columns (cold, MALL-rotated buffers): below 1024
+            // rows two blocks of 256 threads per CU with a row over two waves
+            // (512 x 4096: 4.1 us); from 1024 rows x is read non-temporally
+            // (it is read once) and one wave holds a whole row, so its max
+            // needs no cross-wave merge: two blocks of 256 threads per CU
+            // (2048 x 4096: 9.1 -> 7.3 us, 3328 rows 12.9 -> 10.2 us), except
+            // 4096 to 32767 rows, where four blocks of 256 threads with a row
+            // over two waves keep more rows in flight (8192 rows: 17.4 us
+            // against 18.1), and from 32768 rows, where one 512-thread block
+            // of rows over two waves walks them (131072 rows: 307 -> 275 us)
+            if(n <= 4096 && p.rows < 1024) return launch_stream<4, 2, 256, 2>(p, stream);
+            if(n <= 4096 && p.rows >= 4096 && p.rows < 32768)
+                return launch_stream<4, 2, 256, 4, true>(p, stream);
+            if(n <= 4096 && p.rows >= 32768) return launch_stream<4, 2, 512, 1, true>(p, stream);
+            if(n <= 4096) return launch_stream<8, 1, 256, 2, true>(p, stream);
             if(n <= 8192) return launch_stream<4, 4, 512, 2>(p, stream);
-            // one row group of 8 waves per block (4 chunks per lane) rather
-            // than two of 4 waves (8 chunks per lane): n = 14336 cold, 512 /
-            // 2048 rows 9.7 -> 8.6 / 22.1 -> 20.8 us, level at 8192 rows
-            if(n <= 16384) return launch_stream<4, 8, 512>(p, stream);
+            // one row group of 16 waves per block (4 chunks per lane), x read
+            // non-temporally: n = 14336 cold, 2048 / 8192 rows 19.4 -> 16.7 /
+            // 64.2 -> 58.0 us
+            if(n <= 16384) return launch_stream<4, 8, 1024, 1, true>(p, stream);
             if(n <= 32768) return launch_stream<4, 16, 1024>(p, stream);
         }
     }

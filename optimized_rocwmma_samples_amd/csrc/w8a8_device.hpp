@@ -123,6 +123,57 @@ __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d)
            | ((uint32_t)d << 24);
 }
 
+// The quantizer's arithmetic in fewer VALU instructions, same results.
+//
+// float(x) * s for the fp16 x in the low (HI = false) or high half of a
+// packed pair, in one v_fma_mix_f32: the fp16 operand converts exactly and
+// x * s + 0 is rounded once, so the value is float(x) * s except that an
+// exact -0 product comes out +0, which nothing downstream tells apart (|p|
+// and rint(p * inv) are the same for both).
+template <bool HI>
+__device__ __forceinline__ float mul_h16_f32(uint32_t h2, float s)
+{
+    float r;
+    if constexpr(HI)
+        asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+            : "=v"(r)
+            : "v"(h2), "v"(s));
+    else
+        asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(s));
+    return r;
+}
+
+// rint(p * inv) clamped to [-qmax, qmax], as a float: quant_i8 before its
+// conversion.  v_med3_f32 of (v, -qmax, qmax) is the clamp in one
+// instruction, NaN included: with a NaN operand it returns the min3 of its
+// operands, -qmax, which is what fminf(fmaxf(NaN, -qmax), qmax) gives.
+__device__ __forceinline__ float quant_f(float p, float inv, float qmax)
+{
+    return __builtin_amdgcn_fmed3f(__builtin_rintf(p * inv), -qmax, qmax);
+}
+
+// Four quant_f results (integer-valued, within +-127) converted to int8 and
+// packed (a in the low byte): each v_cvt_i32_f32 writes its low byte straight
+// into its byte of the result (SDWA dst_sel, the other bytes kept), so the
+// packing costs no instruction beyond the conversions.
+__device__ __forceinline__ uint32_t cvt_pack4_i8(float a, float b, float c, float d)
+{
+    uint32_t r;
+    asm("v_cvt_i32_f32_sdwa %0, %1 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD"
+        : "=v"(r)
+        : "v"(a));
+    asm("v_cvt_i32_f32_sdwa %0, %1 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD"
+        : "+v"(r)
+        : "v"(b));
+    asm("v_cvt_i32_f32_sdwa %0, %1 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD"
+        : "+v"(r)
+        : "v"(c));
+    asm("v_cvt_i32_f32_sdwa %0, %1 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD"
+        : "+v"(r)
+        : "v"(d));
+    return r;
+}
+
 // (g / (1 + exp(-g))) * u in about a third of the instructions of expf and
 // the IEEE division (the requantization is VALU-bound with those):
 //   exp(-g) = 2^(ph + pl), ph + pl = -g * log2(e) with log2(e) in two parts

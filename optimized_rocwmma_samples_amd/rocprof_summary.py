@@ -106,19 +106,24 @@ XCDS, SIMDS = 8, 1024
 
 
 def _derived(avg: dict, dur_ns: float) -> list[str]:
-    """Metrics derived from one kernel's averaged counters: the MFMA pipes'
-    busy fraction at the clock the kernel ran at, that clock, LDS-active
-    cycles per MFMA-busy cycle and per int8 op, and the int8 rate."""
+    """Metrics derived from one kernel's averaged counters: MFMA-busy cycles
+    per GPU-busy cycle, LDS-active cycles per MFMA-busy cycle and per int8
+    op, and the int8 rate.
+
+    GRBM_GUI_ACTIVE counts the GPU's busy cycles over the whole window the
+    profiler brackets a dispatch with, launch and drain included, which is
+    longer than the kernel's own run (for kernels of a few microseconds,
+    several times longer), so MFMA_BUSY over it is a lower bound of the
+    MFMA pipes' busy fraction, and GUI_ACTIVE over the trace's duration is
+    not a clock: no clock is derived here."""
     out = []
     gui = avg.get("GRBM_GUI_ACTIVE")
     busy = avg.get("SQ_VALU_MFMA_BUSY_CYCLES")
     lds = avg.get("SQ_LDS_IDX_ACTIVE")
     mops = avg.get("SQ_INSTS_VALU_MFMA_MOPS_I8")
     if gui and busy is not None:
-        out.append(f"mfma_util (MFMA_BUSY / (SIMDs x GUI_ACTIVE / XCDs)) = "
-                   f"{busy / (SIMDS * gui / XCDS):.3f}")
-    if gui and dur_ns > 0:
-        out.append(f"clock_MHz (GUI_ACTIVE / XCDs / duration) = {gui / XCDS / dur_ns * 1e3:.0f}")
+        out.append(f"mfma_busy_per_gui_cycle (MFMA_BUSY / (SIMDs x GUI_ACTIVE / XCDs); "
+                   f"a lower bound) = {busy / (SIMDS * gui / XCDS):.3f}")
     if lds is not None and busy:
         out.append(f"lds_active_per_mfma_busy_cycle = {lds / busy:.3f}")
     if lds is not None and mops:

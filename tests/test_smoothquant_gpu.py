@@ -59,11 +59,14 @@ def test_row_lengths(w8a8, gpu, n):
 
 
 @pytest.mark.parametrize("m,n", [(8192, 4096), (8197, 1000), (12289, 8), (32767, 2056),
-                                 (32768, 2056)])
+                                 (32768, 2056), (1023, 4096), (1024, 4096), (3328, 4096),
+                                 (4095, 3000), (4096, 4000), (2048, 14336), (777, 16384)])
 def test_many_rows(w8a8, gpu, m, n):
-    # 8192 to 32767 rows of 2049-4096 columns take the 4 x 256-thread launch
-    # per CU, 32768 rows the single 512-thread block again (rows not a
-    # multiple of the block's row groups)
+    # the row-count boundaries of the launch choice for 2049-4096 columns
+    # (below 1024 rows: a row over two waves, two 256-thread blocks per CU;
+    # 1024-4095 and from 32768: one wave per row; 4096-32767: four
+    # 256-thread blocks per CU), rows not a multiple of the blocks' row
+    # groups, and 8193-16384 columns (one 16-wave row group per block)
     seed = 400 + m + n
     x = G.activations(seed, m, n)
     s = G.uniform(seed, G.TID_S, (n,), 0.5, 2.0)
@@ -95,6 +98,31 @@ def test_zero_rows_ties_and_qmax(w8a8, gpu):
     qg, rg = run_sq(w8a8, x, s, gpu)
     assert rg[0] == 0 and (qg[0] == 0).all()
     assert qg[1, :10].tolist() == [127, 2, 4, -2, 0, 2, 0, -2, 126, 4]
+
+
+@pytest.mark.parametrize("n", [1000, 4096, 14336])
+def test_non_finite_inputs_and_fractional_qmax(w8a8, gpu, n):
+    """Rows holding inf, -inf, NaN and the fp16 extremes, quantized with integer
+    and fractional quant_max: q and r equal the oracle's restatement of the
+    reference's float ops (a NaN element is ignored by the row max and lands on
+    -quant_max through fmaxf / fminf; an infinite row max gives r = inf,
+    inv = 0, so finite elements quantize to 0 and the infinite ones to
+    +-quant_max)."""
+    m = 12
+    x = G.activations(900 + n, m, n)
+    x[0, 3] = np.inf
+    x[1, 5] = -np.inf
+    x[2, 7] = np.nan
+    x[3, :4] = [np.nan, np.inf, -np.inf, np.nan]
+    x[4, 100] = np.float16(65504)
+    x[4, 101] = np.float16(-65504)
+    x[5, :] = np.nan
+    x[6, n - 1] = np.inf
+    x[7, ::97] = np.nan
+    s = G.uniform(900 + n, G.TID_S, (n,), 0.5, 2.0)
+    for qmax in (127.0, 100.6, 7.25, 0.5):
+        qg, rg = run_sq(w8a8, x, s, gpu, qmax)
+        check_exact(qg, rg, *O.smoothquant(x, s, qmax))
 
 
 def test_reference_default_fill(w8a8, gpu):
