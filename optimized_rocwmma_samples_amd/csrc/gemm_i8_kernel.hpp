@@ -601,16 +601,19 @@ __device__ __forceinline__ void epilogue_f16_lds(const KArgs& p, uint32_t m0, ui
     static_assert(kSt % kBat == 0, "whole batches");
 #pragma unroll
     for(int q0 = 0; q0 < kSt; q0 += kBat) {
-        // a batch of reads before its stores; each 16-byte chunk as its two
-        // 8-byte halves, from the positions the writes put them at
+        // a batch of reads before its stores; each 16-byte chunk in one
+        // ds_read_b128, its halves swapped back where the writes swapped them
+        // (free when row bit 3 is fixed per read, as with 8-chunk rows; a
+        // select per dword otherwise).  Two 8-byte reads per chunk instead
+        // hit the same half of each chunk from four rows of a half-wave: 256
+        // LDS bank-conflict cycles per 128 x 128 tile.
         v4i out[kBat];
 #pragma unroll
         for(int b = 0; b < kBat; ++b) {
             const int     row = (q0 + b) * kRowsPerSt + lane / kRowChunks;
             const int8_t* src = stage + row * kRowBytes + S::chunk(chunk, row) * 16;
-            const v2i     lo  = *reinterpret_cast<const v2i*>(src + S::half(0, row) * 8);
-            const v2i     hi  = *reinterpret_cast<const v2i*>(src + S::half(1, row) * 8);
-            out[b]            = v4i{lo.x, lo.y, hi.x, hi.y};
+            const v4i     v   = *reinterpret_cast<const v4i*>(src);
+            out[b]            = S::half(0, row) ? v4i{v.z, v.w, v.x, v.y} : v;
         }
 #pragma unroll
         for(int b = 0; b < kBat; ++b) {

@@ -94,18 +94,23 @@ __device__ __forceinline__ void epilogue_f16_persist(const KArgs& p, __amdgpu_bu
             }
         }
         // read the pass back row-contiguous, all its reads before its stores;
-        // each 16-byte chunk as its two 8-byte halves, from the positions the
-        // writes put them at (no select to swap them back).  A wave's LDS
-        // accesses complete in order, so the next pass's writes cannot
-        // overtake these reads.
+        // each 16-byte chunk in one ds_read_b128, its halves swapped back in
+        // registers where the writes swapped them (S::half: row bit 3).  With
+        // 8 rows per store, row bit 3 of read q is q's own low bit, a
+        // compile-time fact (the lane itself is opaque here), so the swap is
+        // a register renaming.  Two 8-byte reads per chunk instead (the lane
+        // offset unknown to the compiler) cost 512 LDS bank-conflict cycles
+        // per tile: four rows of a half-wave then hit the same half of every
+        // chunk.  A wave's LDS accesses complete in order, so the next pass's
+        // writes cannot overtake these reads.
+        static_assert(P::kRowsPerSt == 8, "row bit 3 of a read-back row is q's low bit");
         v4i out[P::kStPerPass];
 #pragma unroll
         for(int q = 0; q < P::kStPerPass; ++q) {
             const int     r   = q * P::kRowsPerSt + lane / P::kRowChunks;
             const int8_t* src = slice + r * P::kRowBytes + S::chunk(chunk, r) * 16;
-            const v2i     lo  = *reinterpret_cast<const v2i*>(src + S::half(0, r) * 8);
-            const v2i     hi  = *reinterpret_cast<const v2i*>(src + S::half(1, r) * 8);
-            out[q]            = v4i{lo.x, lo.y, hi.x, hi.y};
+            const v4i     v   = *reinterpret_cast<const v4i*>(src);
+            out[q]            = (q & 1) ? v4i{v.z, v.w, v.x, v.y} : v;
         }
         // row mr + q * kRowsPerSt at byte offset off0 + q * step (in range rows
         // only: the host keeps every element offset of C below 2^31)
