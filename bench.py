@@ -782,6 +782,27 @@ def measured_peaks(torch, dev, cus):
                                  "quantizer's cold cfg1 measurement with the arithmetic removed; "
                                  "best of 5 forms x 6 launch shapes")
     del pairs
+    # a read-only stream of one cfg4 weight matrix (28672 x 8192 bytes), two
+    # copies alternating (MALL-cold) in 20 graph-replayed launches: the decode
+    # GEMM's measurement with everything but the weight stream removed
+    wb = 28672 * 8192
+    bufs = [torch.empty(wb, dtype=torch.uint8, device=dev).fill_(2) for _ in range(2)]
+    best, arg = 0.0, None
+    for var in (1, 3, 5, 7):
+        for b, th in ((cus, 256), (cus, 512), (cus * 2, 256), (cus * 4, 256)):
+            calls = [(lambda bb=bufs[i % 2], b=b, th=th, v=var: stream(
+                torch.cuda.current_stream(dev).cuda_stream, bb.data_ptr(), bb.data_ptr(), wb, b,
+                th, v, 0)) for i in range(20)]
+            rate = wb / (graph_us(torch, calls) * 1e-6) / 1e9
+            if rate > best:
+                best, arg = rate, (var, b, th)
+    out["read_cfg4_GBps"] = best
+    out["read_cfg4_form"] = {"variant": arg[0], "blocks": arg[1], "threads": arg[2]}
+    out["read_cfg4_note"] = ("read-only stream of 235 MB (one cfg4 weight matrix), two copies in "
+                             "turn, 20 graph-replayed launches: the decode layers' measurement "
+                             "with the activations, MFMAs and outputs removed; best of 4 forms x "
+                             "4 launch shapes")
+    del bufs
     calls = [lambda: check(lib.w8a8_peak_empty(torch.cuda.current_stream(dev).cuda_stream),
                            "peak_empty")] * 48
     out["launch_floor_us"] = graph_us(torch, calls)
@@ -947,6 +968,8 @@ def main(argv=None) -> int:
         extras["cfg3_smaller_m"] = bench_cfg3_smaller_m(torch, w8a8, dev, projs)
         log(json.dumps(extras["cfg3_smaller_m"]))
         extras["decode_cfg4"] = bench_decode(torch, w8a8, dev, gen, cpu=cpu_x)
+        for layer in extras["decode_cfg4"]["layers"]:
+            layer["frac_read_cfg4_measured"] = layer["GBps"] / peaks["read_cfg4_GBps"]
         log(json.dumps(extras["decode_cfg4"]))
         extras["moe_cfg5"] = bench_moe(torch, w8a8, dev, gen, cpu=cpu_x)
         log(json.dumps(extras["moe_cfg5"]))

@@ -28,6 +28,11 @@
 namespace w8a8 {
 namespace gemm {
 
+// Cache policy of the weight stream: non-temporal.  Every weight byte is read
+// once per call and a layer's weights do not fit the MALL beside the rest of
+// a model, so nothing is lost by not keeping them.
+constexpr int kDecodeWeightPolicy = 2;
+
 template <int MT_, int NT_, int KW_, int RING_>
 struct DecCfg {
     static constexpr int kMT      = MT_;            // 32-row m tiles (1 or 2)
@@ -40,7 +45,7 @@ struct DecCfg {
     static constexpr int kLdsBytes = kKW * kWaveLds;
     static_assert(kMT == 1 || kMT == 2, "decode handles up to 64 rows per block");
     static_assert(kNT == 1 || kNT == 2, "a block covers half a slab or a whole one");
-    static_assert(kRing == 2 || kRing == 3, "ring depth");
+    static_assert(kRing >= 2 && kRing <= 6, "ring depth");
     static_assert(kLdsBytes <= 128 * 1024, "partials must fit in LDS");
 };
 
@@ -202,7 +207,8 @@ __global__ void __launch_bounds__(C::kThreads) gemm_i8_decode_kernel(KArgs p, in
             const uint32_t kofs = live ? kt * (kPackFrags * 1024) : 0u;
 #pragma unroll
             for(int f = 0; f < C::kNT * 4; ++f)
-                bq[slot][f] = __builtin_amdgcn_raw_buffer_load_b128(rb, vbb, kofs + f * 1024, 0);
+                bq[slot][f] = __builtin_amdgcn_raw_buffer_load_b128(rb, vbb, kofs + f * 1024,
+                                                                   kDecodeWeightPolicy);
         } else {
             // chunks at k >= K read zeros (k % 16 == 0, so a chunk is all in or out)
 #pragma unroll
@@ -212,7 +218,7 @@ __global__ void __launch_bounds__(C::kThreads) gemm_i8_decode_kernel(KArgs p, in
                 for(int j = 0; j < C::kNT; ++j) {
                     const uint32_t v
                         = (live && kk < p.k && vbr[j] != kOob) ? vbr[j] + kt * kPackK + g * 32 : kOob;
-                    bq[slot][j * 4 + g] = __builtin_amdgcn_raw_buffer_load_b128(rb, v, 0, 0);
+                    bq[slot][j * 4 + g] = __builtin_amdgcn_raw_buffer_load_b128(rb, v, 0, kDecodeWeightPolicy);
                 }
             }
         }
@@ -285,29 +291,23 @@ __global__ void __launch_bounds__(C::kThreads) gemm_i8_decode_kernel(KArgs p, in
 #pragma unroll
         for(int d = 0; d + 1 < C::kRing; ++d) issue(d, kt0 + d);
     }
+    // slot d of a round holds k-tile kt + d; before computing it, the slot
+    // freed one step earlier is refilled RING - 1 k-tiles ahead (tiles past
+    // kt1 read nothing)
     uint32_t kt = kt0;
-    if constexpr(C::kRing == 3) {
-        for(; kt + 3 <= kt1; kt += 3) {
-            issue(2, kt + 2);
-            compute(0);
-            issue(0, kt + 3);
-            compute(1);
-            issue(1, kt + 4);
-            compute(2);
+    for(; kt + C::kRing <= kt1; kt += C::kRing) {
+#pragma unroll
+        for(int d = 0; d < C::kRing; ++d) {
+            issue((d + C::kRing - 1) % C::kRing, kt + d + C::kRing - 1);
+            compute(d);
         }
-        if(kt < kt1) {
-            issue(2, kt + 2);
-            compute(0);
+    }
+#pragma unroll
+    for(int d = 0; d + 1 < C::kRing; ++d) {
+        if(kt + d < kt1) {
+            if(kt + d + C::kRing - 1 < kt1) issue((d + C::kRing - 1) % C::kRing, kt + d + C::kRing - 1);
+            compute(d);
         }
-        if(kt + 1 < kt1) compute(1);
-    } else {
-        for(; kt + 2 <= kt1; kt += 2) {
-            issue(1, kt + 1);
-            compute(0);
-            issue(0, kt + 2);
-            compute(1);
-        }
-        if(kt < kt1) compute(0);
     }
 
     // ---- reduce the KW partials through LDS --------------------------------

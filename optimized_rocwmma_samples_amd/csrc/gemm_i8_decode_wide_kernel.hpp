@@ -93,7 +93,8 @@ __global__ void __launch_bounds__(C::kThreads) gemm_i8_decode_wide_kernel(KArgs 
         const uint32_t kofs = live ? kt * (kPackFrags * 1024) : 0u;
 #pragma unroll
         for(int g = 0; g < 4; ++g)
-            bq[slot][g] = __builtin_amdgcn_raw_buffer_load_b128(rb, vbb, kofs + g * 1024, 0);
+            bq[slot][g] = __builtin_amdgcn_raw_buffer_load_b128(rb, vbb, kofs + g * 1024,
+                                                                kDecodeWeightPolicy);
 #pragma unroll
         for(int i = 0; i < C::kALoads; ++i) {
             const uint32_t kk = kt * kPackK + achunk[i] * 16;
