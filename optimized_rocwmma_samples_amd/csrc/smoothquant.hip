@@ -192,8 +192,9 @@ __global__ void __launch_bounds__(kSqThreads) sq_twopass_kernel(QuantRows p)
 // out-of-range row offset, 0x7FFFFFF0).
 constexpr uint64_t kPanelBytes = 0x7F000000ull;
 
-// NT: x is read with the non-temporal cache policy (it is read once).
-template <int CPL, int WPR, int THREADS, bool NT = false>
+// NT: x is read with the non-temporal cache policy (it is read once); NTS:
+// q is stored with it too.
+template <int CPL, int WPR, int THREADS, bool NT = false, bool NTS = false>
 __global__ void __launch_bounds__(THREADS) sq_stream_kernel(QuantRows p, uint32_t iters)
 {
     constexpr int kStreamThreads = THREADS;
@@ -299,7 +300,7 @@ __global__ void __launch_bounds__(THREADS) sq_stream_kernel(QuantRows p, uint32_
                                      quant_f(v[2], inv, qmax), quant_f(v[3], inv, qmax));
             pk.y = (int)cvt_pack4_i8(quant_f(v[4], inv, qmax), quant_f(v[5], inv, qmax),
                                      quant_f(v[6], inv, qmax), quant_f(v[7], inv, qmax));
-            __builtin_amdgcn_raw_buffer_store_b64(pk, rq, qoff + coff[j], 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b64(pk, rq, qoff + coff[j], 0, NTS ? kCpolNt : 0);
         }
     };
 
@@ -353,7 +354,7 @@ __global__ void __launch_bounds__(THREADS) sq_stream_kernel(QuantRows p, uint32_
 
 // THREADS per block, BPC resident blocks per CU (the grid is BPC x CUs, each
 // block walking rows with a grid stride).
-template <int CPL, int WPR, int THREADS, int BPC = 1, bool NT = false>
+template <int CPL, int WPR, int THREADS, int BPC = 1, bool NT = false, bool NTS = false>
 hipError_t launch_stream(const QuantRows& p, hipStream_t stream)
 {
     constexpr int  kGroups = THREADS / kWave / WPR;
@@ -370,7 +371,7 @@ hipError_t launch_stream(const QuantRows& p, hipStream_t stream)
         static std::once_flag once;
         std::call_once(once, [] {
             (void)hipFuncSetAttribute(
-                reinterpret_cast<const void*>(sq_stream_kernel<CPL, WPR, THREADS, NT>),
+                reinterpret_cast<const void*>(sq_stream_kernel<CPL, WPR, THREADS, NT, NTS>),
                 hipFuncAttributeMaxDynamicSharedMemorySize, 131072);
             (void)hipGetLastError();
         });
@@ -392,7 +393,7 @@ hipError_t launch_stream(const QuantRows& p, hipStream_t stream)
         const uint32_t need   = (q.rows + kGroups - 1) / kGroups;
         const uint32_t blocks = std::max<uint32_t>(1, std::min<uint32_t>(need, (uint32_t)max_blocks));
         const uint32_t iters  = (q.rows + blocks * kGroups - 1) / (blocks * kGroups);
-        hipLaunchKernelGGL((sq_stream_kernel<CPL, WPR, THREADS, NT>), dim3(blocks), dim3(THREADS), lds,
+        hipLaunchKernelGGL((sq_stream_kernel<CPL, WPR, THREADS, NT, NTS>), dim3(blocks), dim3(THREADS), lds,
                            stream, q, iters);
         const hipError_t e = hipGetLastError();
         if(e != hipSuccess) return e;
@@ -447,8 +448,11 @@ hipError_t dispatch(const QuantRows& p, hipStream_t stream)
             if(n <= 4096 && p.rows < 1024) return launch_stream<4, 2, 256, 2>(p, stream);
             if(n <= 4096 && p.rows >= 4096 && p.rows < 32768)
                 return launch_stream<4, 2, 256, 4, true>(p, stream);
+            // (1024-4095 rows also store q non-temporally: 2048 x 4096 cold
+            // 7.4 -> 6.5 us; from 4096 rows it no longer pays, 8192 rows 17.6
+            // against 18.4 us)
             if(n <= 4096 && p.rows >= 32768) return launch_stream<4, 2, 512, 1, true>(p, stream);
-            if(n <= 4096) return launch_stream<8, 1, 256, 2, true>(p, stream);
+            if(n <= 4096) return launch_stream<8, 1, 256, 2, true, true>(p, stream);
             if(n <= 8192) return launch_stream<4, 4, 512, 2>(p, stream);
             // one row group of 16 waves per block (4 chunks per lane), x read
             // non-temporally: n = 14336 cold, 2048 / 8192 rows 19.4 -> 16.7 /
