@@ -454,9 +454,9 @@ hipError_t dispatch(const QuantRows& p, hipStream_t stream)
             if(n <= 4096 && p.rows >= 32768) return launch_stream<4, 2, 512, 1, true>(p, stream);
             if(n <= 4096) return launch_stream<8, 1, 256, 2, true, true>(p, stream);
             if(n <= 8192) return launch_stream<4, 4, 512, 2>(p, stream);
-            // one row group of 16 waves per block (4 chunks per lane), x read
-            // non-temporally: n = 14336 cold, 2048 / 8192 rows 19.4 -> 16.7 /
-            // 64.2 -> 58.0 us
+            // two row groups of 8 waves per 1024-thread block (4 chunks per
+            // lane), x read non-temporally: n = 14336 cold, 2048 / 8192 rows
+            // 19.4 -> 16.7 / 64.2 -> 58.0 us
             if(n <= 16384) return launch_stream<4, 8, 1024, 1, true>(p, stream);
             if(n <= 32768) return launch_stream<4, 16, 1024>(p, stream);
         }
