@@ -48,11 +48,15 @@ __device__ __forceinline__ bool find_slot(uint32_t count, uint32_t target, F til
             if(hit) {
                 const int l = __ffsll((unsigned long long)hit) - 1;
                 slot        = base + l;
-                first       = __shfl(incl - t, l, kWave);
+                // one lane's value read by every lane: uniform, and said so
+                // (a shuffle result is otherwise taken as divergent, and so is
+                // everything derived from it: the tile's loads would then run
+                // in readfirstlane loops)
+                first       = __builtin_amdgcn_readfirstlane(__shfl(incl - t, l, kWave));
                 found       = true;
             }
         }
-        carry = __shfl(incl, kWave - 1, kWave);
+        carry = __builtin_amdgcn_readfirstlane(__shfl(incl, kWave - 1, kWave));
     }
     total = carry;
     return found;
@@ -214,7 +218,11 @@ __device__ __forceinline__ void moe_tile(const MoeArgs& q, uint32_t lid, KArgs& 
     uint32_t first, total;
     find_slot(q.experts, lid, [&](uint32_t i) { return S::tiles(moe_rows_of(q, i), q.n); }, e,
               first, total);
-    row0  = (uint32_t)q.expert_start[e];
+    // wave-uniform values, said so: the operand buffer resources built from
+    // them must be scalar, or every load of the tile runs in a readfirstlane
+    // loop
+    e     = __builtin_amdgcn_readfirstlane(e);
+    row0  = __builtin_amdgcn_readfirstlane((uint32_t)q.expert_start[e]);
     p.a   = q.a + (size_t)row0 * q.lda;
     p.b   = q.w + (size_t)e * q.w_stride;
     p.c   = static_cast<int8_t*>(q.c) + (size_t)row0 * q.ldc * (OUT == W8A8_OUT_I32 ? 4 : 2);
