@@ -752,6 +752,17 @@ hipError_t launch_gemm_streamk(const GemmArgs& g, uint32_t blocks, void* ws, hip
     const ExplicitSk e      = explicit_streamk(g.m, g.n, g.k, blocks);
     const KArgs      p      = make_kargs(g);
     const int        vec_ok = out_vec_ok(g);
+    if(e.plan.blocks == e.plan.ntiles) {
+        // one whole tile per block, no pieces: the schedule is the tile
+        // kernel's one-block-per-tile grid (the same logical block -> tile
+        // order), which runs it without the counters' clear launch and with
+        // the epilogue's scales loaded under the last k-tile
+        switch(e.cfg) {
+        case TileCfg::kMain: return gemm::launch_cfg<GemmMain>(p, g.out_type, vec_ok, stream);
+        case TileCfg::kMidM: return gemm::launch_cfg<GemmMidM>(p, g.out_type, vec_ok, stream);
+        default: return gemm::launch_cfg<GemmSmall>(p, g.out_type, vec_ok, stream);
+        }
+    }
     switch(e.cfg) {
     case TileCfg::kMain:
         return gemm::launch_cfg_streamk<GemmMain>(p, g.out_type, vec_ok, 0, e.plan, ws, watch,

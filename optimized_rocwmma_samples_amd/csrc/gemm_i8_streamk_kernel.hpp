@@ -203,8 +203,11 @@ __global__ void __launch_bounds__(C::kThreads, 1)
                 mine += sk.cut(b) && sk.start(b) < (uint64_t)t * sk.nk;
             if(mine) atomicAdd(&bcast[1], mine);
             __syncthreads();
-            const uint32_t order  = bcast[0];
-            const uint32_t base   = bcast[1];
+            // wave-uniform (read from LDS, so taken as divergent unless said:
+            // the partial slot's buffer resource would then be rebuilt in a
+            // readfirstlane loop around every store and load)
+            const uint32_t order  = __builtin_amdgcn_readfirstlane(bcast[0]);
+            const uint32_t base   = __builtin_amdgcn_readfirstlane(bcast[1]);
             const uint32_t pieces = sk.pieces(t);
             if(order + 1 < pieces) {
                 store_partial_dev<C>(part + (size_t)(base + order) * Partial<C>::kInts, acc);
