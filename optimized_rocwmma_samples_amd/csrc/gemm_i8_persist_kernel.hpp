@@ -54,10 +54,14 @@ struct Persist {
 // pass; every lane issues exactly Persist<C>::kStores 16-byte stores.  The
 // host guarantees N % 8 == 0, ldc % 8 == 0 and a 16-byte aligned C, so an
 // 8-column chunk is either inside the matrix or entirely past it.
-// NT: non-temporal stores, for outputs larger than the MALL (they cannot
-// stay resident, and write-allocating them leaves the MALL full of dirty
-// lines that the next kernel pays to write back: the quantizer that follows
-// the 470 MB gate_up output of cfg3 runs 62 instead of 89 us).
+// NT: non-temporal stores, for outputs of at least a quarter of the MALL.
+// Larger than the MALL they cannot stay resident, and
+// write-allocating them leaves it full of dirty lines that the next kernel
+// pays to write back (the quantizer that follows the 470 MB gate_up output of
+// cfg3 runs 62 instead of 89 us).  From a quarter of it they still crowd out
+// the next kernels' operands: cfg3's qkv and o_proj outputs (100 / 67 MB)
+// stored this way take the step from 1.493 to 1.463-1.476 ms (same box,
+// alternating).
 template <class C, bool NT>
 __device__ __forceinline__ void epilogue_f16_persist(const KArgs& p, __amdgpu_buffer_rsrc_t rc,
                                                      uint32_t m0, uint32_t n0, int8_t* slice,
@@ -322,7 +326,7 @@ template <class C>
 hipError_t launch_cfg_persist(const KArgs& p, int vec_ok, uint32_t cus, hipStream_t stream)
 {
     raise_persist_lds_once<C>();
-    const int nt = (uint64_t)p.m * p.ldc * 2 > kMallBytes;
+    const int nt = (uint64_t)p.m * p.ldc * 2 >= kMallBytes / 4;
     hipLaunchKernelGGL((gemm_i8_persist_kernel<C>), dim3(cus), dim3(C::kThreads),
                        Persist<C>::kLdsBytes, stream, p, vec_ok, nt);
     return hipGetLastError();
