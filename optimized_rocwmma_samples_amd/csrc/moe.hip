@@ -530,7 +530,10 @@ struct SiluRequant {
 // segment per wave instruction), reduced through LDS, and the rows' experts.
 // Phase 2: each wave quantizes kRqRows / kSqWaves rows, kRqBatch 8-column
 // chunks per lane in flight (h and s2 loads issued before any store).
-constexpr int kRqRows  = 16;
+// 8 rows per block: cfg5's 8448 rows make 1056 blocks, 4.1 per CU; with 16
+// rows (528 blocks, 2.06 per CU) the CUs holding a third block finished alone
+// (cfg5 layer 1535-1547 -> 1526-1528 us, same box, alternating).
+constexpr int kRqRows  = 8;
 constexpr int kRqSlots = kSqThreads / kRqRows;
 constexpr int kRqBatch = 7;
 
