@@ -670,6 +670,76 @@ def bench_hipblaslt_yardstick(torch, projs, iters=10):
     return out
 
 
+def board_power(torch, dev, loads, secs=2.0, lead=1.0, every=0.02):
+    """Socket power and GFX clock read through amdsmi (read-only queries; no
+    setting is changed) every `every` s while each callable of `loads` runs
+    back to back for `lead` + `secs` s, sampled over the last `secs` (the
+    reported power follows a load change with a lag of about a second):
+    medians and 90th percentiles per load, with the board's power cap.  The GPU is matched to the amdsmi handle by PCI bus id.
+    Empty when amdsmi is not importable or reports no matching GPU."""
+    try:
+        import amdsmi
+    except ImportError:
+        return {"note": "amdsmi not importable"}
+    import statistics
+    import threading
+
+    try:
+        amdsmi.amdsmi_init()
+    except Exception as e:  # no driver interface visible: nothing to report
+        return {"note": f"amdsmi_init failed: {e}"[:200]}
+    try:
+        props = torch.cuda.get_device_properties(dev)
+        want = getattr(props, "pci_bus_id", None)
+        handle = None
+        for h in amdsmi.amdsmi_get_processor_handles():
+            bdf = amdsmi.amdsmi_get_gpu_device_bdf(h)  # dddd:bb:dd.f
+            if want is None or int(bdf.split(":")[1], 16) == want:
+                handle = h
+                break
+        if handle is None:
+            return {"note": "no amdsmi handle with this GPU's PCI bus id"}
+        cap = amdsmi.amdsmi_get_power_cap_info(handle).get("power_cap")
+        out = {"power_cap_W": cap / 1e6 if isinstance(cap, (int, float)) else None,
+               "note": f"amdsmi current_socket_power and GFX clock sampled every {every * 1e3:.0f} ms "
+                       f"over {secs:.1f} s, after each load had run {lead:.1f} s"}
+        for name, fn in loads.items():
+            watts, mhz, stop = [], [], [False]
+
+            def sample():
+                while not stop[0]:
+                    try:
+                        w = amdsmi.amdsmi_get_power_info(handle).get("current_socket_power")
+                        c = amdsmi.amdsmi_get_clock_info(handle, amdsmi.AmdSmiClkType.GFX).get("clk")
+                        if isinstance(w, (int, float)):
+                            watts.append(w)
+                        if isinstance(c, (int, float)):
+                            mhz.append(c)
+                    except Exception:  # a failed query drops one sample
+                        pass
+                    time.sleep(every)
+
+            t_lead = time.perf_counter() + lead
+            while time.perf_counter() < t_lead:
+                fn()
+            th = threading.Thread(target=sample, daemon=True)
+            th.start()
+            t_end = time.perf_counter() + secs
+            while time.perf_counter() < t_end:
+                fn()
+            torch.cuda.synchronize()
+            stop[0] = True
+            th.join()
+            q90 = lambda v: sorted(v)[int(0.9 * (len(v) - 1))] if v else None
+            out[name] = {"socket_W_median": statistics.median(watts) if watts else None,
+                         "socket_W_p90": q90(watts),
+                         "gfx_MHz_median": statistics.median(mhz) if mhz else None,
+                         "samples": len(watts)}
+        return out
+    finally:
+        amdsmi.amdsmi_shut_down()
+
+
 def measured_peaks(torch, dev, cus):
     """Ceilings measured on this GPU in this run (libw8a8_peaks.so, built from
     csrc/peaks.hip): the int8 MFMA-only loop (random and zero operands), a
@@ -951,6 +1021,29 @@ def main(argv=None) -> int:
 
     extras = {}
     if not args.no_extras:
+        # the step and the MFMA-only loop of the GEMM's instruction (random
+        # operands) against the board's power cap
+        import ctypes
+
+        plib = ctypes.CDLL(str(ROOT / "optimized_rocwmma_samples_amd" / "lib" / "libw8a8_peaks.so"))
+        plib.w8a8_peak_mfma.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int,
+                                        ctypes.c_void_p, ctypes.c_void_p]
+        psink = torch.empty(cus * 8, dtype=torch.int32, device=dev)
+
+        def mfma_loop():
+            st = torch.cuda.current_stream(dev).cuda_stream
+            for _ in range(8):
+                if plib.w8a8_peak_mfma(cus, 4096, 3, psink.data_ptr(), st) != 0:
+                    raise RuntimeError("w8a8_peak_mfma failed")
+            torch.cuda.synchronize()
+
+        def step_sync():
+            step()
+            torch.cuda.synchronize()
+
+        extras["board_power"] = board_power(torch, dev, {"cfg3_step": step_sync,
+                                                         "mfma16_random_loop": mfma_loop})
+        log(json.dumps(extras["board_power"]))
         cpu_x = not args.no_cpu_baseline
         extras["smoothquant_cfg1"] = bench_quantizer(torch, w8a8, dev, gen, cpu=cpu_x)
         q1 = extras["smoothquant_cfg1"]
