@@ -1,0 +1,104 @@
+"""The path as PyTorch operators: `torch.library` custom ops under the
+namespace `w8a8`, each calling the same C ABI (libw8a8.so, through this
+package's ctypes layer) on torch's current stream, with a fake kernel for
+shape and dtype inference, so torch.compile and torch.export trace through
+them without a graph break.
+
+    import optimized_rocwmma_samples_amd.torch_ops  # registers the ops
+    q, r = torch.ops.w8a8.smoothquant(x, s, 127.0)
+    c = torch.ops.w8a8.gemm(q, w, r, sb)
+    c, q, r = torch.ops.w8a8.fused_sq_gemm(x, s, w, sb)
+    x_out, q, r = torch.ops.w8a8.add_rmsnorm_smoothquant(x, residual, gamma, s, 1e-5, 127.0)
+
+The ops are functional (every output is a new tensor), as torch.library
+custom ops must be; the package functions keep the in-place and
+preallocated-output forms.  They run only on device tensors: a CPU tensor
+raises, as everywhere in the package (there is no CPU path).
+
+Reference kernels: smoothquant <- kernel_smoothquant
+(rocwmma_smoothquant.cpp:58-122); gemm <- gemm_quant_tensor_scale
+(rocwmma_gemm_quantized.cpp:127-195) with per-token x per-channel scales;
+add_rmsnorm_smoothquant <- kernel_add_rmsnorm2d_fwd
+(rocwmma_rmsnorm2d.cpp:127-186) feeding the quantizer.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import add_rmsnorm_smoothquant as _add_rmsnorm_smoothquant
+from . import fused_sq_gemm as _fused_sq_gemm
+from . import gemm as _gemm
+from . import smoothquant as _smoothquant
+
+Tensor = torch.Tensor
+
+
+@torch.library.custom_op("w8a8::smoothquant", mutates_args=())
+def smoothquant(x: Tensor, smooth_scale: Tensor, quant_max: float = 127.0) -> Tuple[Tensor, Tensor]:
+    """(q int8 [M, N], row_scale fp32 [M]) of fp16 x [M, N]."""
+    return _smoothquant(x, smooth_scale, quant_max)
+
+
+@smoothquant.register_fake
+def _(x, smooth_scale, quant_max=127.0):
+    m, n = x.shape
+    return x.new_empty((m, n), dtype=torch.int8), x.new_empty((m,), dtype=torch.float32)
+
+
+@torch.library.custom_op("w8a8::gemm", mutates_args=())
+def gemm(a: Tensor, b: Tensor, scale_a: Optional[Tensor] = None,
+         scale_b: Optional[Tensor] = None, tensor_scale_a: float = 1.0,
+         tensor_scale_b: float = 1.0) -> Tensor:
+    """fp16 C [M, N] = dequant(a [M, K] . b [N, K]^T): per-row / per-column
+    scales where given, else the tensor scales."""
+    return _gemm(a, b, scale_a, scale_b, tensor_scale_a, tensor_scale_b)
+
+
+@gemm.register_fake
+def _(a, b, scale_a=None, scale_b=None, tensor_scale_a=1.0, tensor_scale_b=1.0):
+    return a.new_empty((a.shape[0], b.shape[0]), dtype=torch.float16)
+
+
+@torch.library.custom_op("w8a8::gemm_i32", mutates_args=())
+def gemm_i32(a: Tensor, b: Tensor) -> Tensor:
+    """int32 accumulators a [M, K] . b [N, K]^T."""
+    return _gemm(a, b, out_dtype=torch.int32)
+
+
+@gemm_i32.register_fake
+def _(a, b):
+    return a.new_empty((a.shape[0], b.shape[0]), dtype=torch.int32)
+
+
+@torch.library.custom_op("w8a8::fused_sq_gemm", mutates_args=())
+def fused_sq_gemm(x: Tensor, smooth_scale: Tensor, w: Tensor,
+                  scale_w: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
+    """SmoothQuant of x [M, K] then C = dequant(q . w^T): (c fp16 [M, N], q, row_scale)."""
+    return _fused_sq_gemm(x, smooth_scale, w, scale_w)
+
+
+@fused_sq_gemm.register_fake
+def _(x, smooth_scale, w, scale_w):
+    m, k = x.shape
+    return (x.new_empty((m, w.shape[0]), dtype=torch.float16),
+            x.new_empty((m, k), dtype=torch.int8), x.new_empty((m,), dtype=torch.float32))
+
+
+@torch.library.custom_op("w8a8::add_rmsnorm_smoothquant", mutates_args=())
+def add_rmsnorm_smoothquant(x: Tensor, residual: Tensor, gamma: Tensor, smooth_scale: Tensor,
+                            eps: float = 1e-5,
+                            quant_max: float = 127.0) -> Tuple[Tensor, Tensor, Tensor]:
+    """(x_out = half(x + residual), q int8, row_scale) of RMSNorm(x_out) fed
+    to the quantizer; x and residual are left unchanged."""
+    x_out, _, q, r = _add_rmsnorm_smoothquant(x, gamma, smooth_scale, residual=residual, eps=eps,
+                                              quant_max=quant_max)
+    return x_out, q, r
+
+
+@add_rmsnorm_smoothquant.register_fake
+def _(x, residual, gamma, smooth_scale, eps=1e-5, quant_max=127.0):
+    m, n = x.shape
+    return (torch.empty_like(x), x.new_empty((m, n), dtype=torch.int8),
+            x.new_empty((m,), dtype=torch.float32))

@@ -1,0 +1,112 @@
+"""The torch.library custom ops (namespace w8a8) on the GPU: each op gives
+the bits the package function and the oracle give on the same inputs,
+passes torch.library.opcheck (schema, fake kernel, no input mutation or
+aliasing, dynamic-shape AOT dispatch), and a block compiled with
+torch.compile(fullgraph=True) returns what eager returns, bit for bit.
+
+Bars: int8 / int32 / row scales bit-exact; fp16 bit-exact against the
+oracle's dequant of the oracle's accumulators (the path's 1e-2 rel / 1e-3
+abs bar is implied); RMSNorm-fed q, r equal the package function's (the
+same kernel), x_out = half(x + residual) bit-exact against the oracle.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from checks import assert_f16_bitexact, assert_i32_equal, dev, host
+from optimized_rocwmma_samples_amd import datagen as G
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def ops(w8a8):
+    import optimized_rocwmma_samples_amd.torch_ops  # noqa: F401
+    return torch.ops.w8a8
+
+
+def gemm_inputs(m, n, k, seed):
+    x = G.activations(seed, m, k)
+    s = G.uniform(seed, G.TID_S, (k,), 0.5, 2.0)
+    w = G.int8(seed, G.TID_B, (n, k))
+    sb = G.uniform(seed, G.TID_SB, (n,), 1e-3, 2e-3)
+    return x, s, w, sb
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 256, 512), (5, 96, 64), (200, 320, 1024)])
+def test_ops_match_oracle(ops, gpu, m, n, k):
+    x, s, w, sb = gemm_inputs(m, n, k, 40 + m)
+    q_o, r_o = O.smoothquant(x, s)
+    acc_o = O.gemm_i32(q_o, w)
+    c_o = O.dequant_f16(acc_o, r_o, sb)
+    xd, sd, wd, sbd = dev(x, gpu), dev(s, gpu), dev(w, gpu), dev(sb, gpu)
+
+    q, r = ops.smoothquant(xd, sd, 127.0)
+    assert np.array_equal(host(q), q_o)
+    assert np.array_equal(host(r).view(np.uint32), r_o.view(np.uint32))
+    assert_f16_bitexact(host(ops.gemm(q, wd, r, sbd)), c_o)
+    assert_i32_equal(host(ops.gemm_i32(q, wd)), acc_o)
+    assert_f16_bitexact(host(ops.gemm(q, wd, None, None, 0.5, 0.25)),
+                        O.dequant_f16(acc_o, tsa=0.5, tsb=0.25))
+    c, q2, r2 = ops.fused_sq_gemm(xd, sd, wd, sbd)
+    assert np.array_equal(host(q2), q_o)
+    assert np.array_equal(host(r2).view(np.uint32), r_o.view(np.uint32))
+    assert_f16_bitexact(host(c), c_o)
+
+
+@pytest.mark.parametrize("m,n", [(64, 4096), (7, 1000)])
+def test_add_rmsnorm_op(ops, w8a8, gpu, m, n):
+    x, res, gamma = G.rmsnorm_inputs(300 + m, m, n)
+    s = G.uniform(300 + m, G.TID_S, (n,), 0.5, 2.0)
+    xd, rd, gd, sd = dev(x, gpu), dev(res, gpu), dev(gamma, gpu), dev(s, gpu)
+    xo, q, r = ops.add_rmsnorm_smoothquant(xd, rd, gd, sd, 1e-5, 127.0)
+    xo_p, _, q_p, r_p = w8a8.add_rmsnorm_smoothquant(xd, gd, sd, residual=rd)
+    xo_o = O.rmsnorm_smoothquant(x, gamma, s, res=res)[0]
+    assert np.array_equal(host(xo).view(np.uint16), xo_o.view(np.uint16))
+    assert np.array_equal(host(xo).view(np.uint16), host(xo_p).view(np.uint16))
+    assert np.array_equal(host(q), host(q_p))
+    assert np.array_equal(host(r).view(np.uint32), host(r_p).view(np.uint32))
+    # the op leaves its inputs as they were
+    assert np.array_equal(host(xd).view(np.uint16), x.view(np.uint16))
+    assert np.array_equal(host(rd).view(np.uint16), res.view(np.uint16))
+
+
+def test_opcheck(ops, gpu):
+    x, s, w, sb = gemm_inputs(48, 128, 256, 7)
+    xd, sd, wd, sbd = dev(x, gpu), dev(s, gpu), dev(w, gpu), dev(sb, gpu)
+    q, r = ops.smoothquant(xd, sd, 127.0)
+    xr, res, gamma = G.rmsnorm_inputs(8, 48, 256)
+    cases = [
+        (ops.smoothquant.default, (xd, sd, 127.0)),
+        (ops.gemm.default, (q, wd, r, sbd, 1.0, 1.0)),
+        (ops.gemm.default, (q, wd, None, None, 0.5, 0.25)),
+        (ops.gemm_i32.default, (q, wd)),
+        (ops.fused_sq_gemm.default, (xd, sd, wd, sbd)),
+        (ops.add_rmsnorm_smoothquant.default,
+         (dev(xr, gpu), dev(res, gpu), dev(gamma, gpu), sd, 1e-5, 127.0)),
+    ]
+    for op, args in cases:
+        torch.library.opcheck(op, args)
+
+
+def test_compiled_block_matches_eager(ops, gpu):
+    m, n, k = 32, 192, 512
+    xr, res, gamma = G.rmsnorm_inputs(11, m, k)
+    _, s, w, sb = gemm_inputs(m, n, k, 11)
+    args = [dev(a, gpu) for a in (xr, res, gamma, s, w, sb)]
+
+    def block(x, residual, g, s_, w_, sb_):
+        xo, q, r = ops.add_rmsnorm_smoothquant(x, residual, g, s_, 1e-5, 127.0)
+        return ops.gemm(q, w_, r, sb_), xo
+
+    torch._dynamo.reset()
+    compiled = torch.compile(block, backend="aot_eager", fullgraph=True)
+    c_e, xo_e = block(*args)
+    c_c, xo_c = compiled(*args)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(c_c).view(np.uint16), host(c_e).view(np.uint16))
+    assert np.array_equal(host(xo_c).view(np.uint16), host(xo_e).view(np.uint16))
