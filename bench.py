@@ -742,8 +742,8 @@ def board_power(torch, dev, loads, secs=2.0, lead=1.0, every=0.02):
 
 def measured_peaks(torch, dev, cus):
     """Ceilings measured on this GPU in this run (libw8a8_peaks.so, built from
-    csrc/peaks.hip): the int8 MFMA-only loop (random and zero operands), a
-    streaming copy over 2 x 1 GiB, and the launch floor of back-to-back
+    csrc/peaks.hip): the int8 MFMA-only loop (random and zero operands), the
+    LDS read rate per CU, a streaming copy over 2 x 1 GiB, and the launch floor of back-to-back
     launches replayed from a graph (48 per replay, as the cfg1 quantizer is
     timed)."""
     import ctypes
@@ -794,6 +794,28 @@ def measured_peaks(torch, dev, cus):
                         f"accumulators x {iters} rounds of v_mfma_i32_32x32x32_i8, or 8 waves "
                         f"(the GEMM's two per SIMD) x 16 accumulators x {iters // 2} rounds of "
                         "v_mfma_i32_16x16x64_i8; operands held in registers")
+    # LDS read ceiling: ds_read_b128 only, conflict-free, one block per CU;
+    # bytes per shader clock per CU from each CU's slowest wave (s_memtime)
+    lib.w8a8_peak_lds.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    lds_iters = 4096
+    cyc = torch.zeros(cus * 16, dtype=torch.int64, device=dev)
+    lsink = torch.empty(cus * 1024, dtype=torch.int32, device=dev)
+    lds = {}
+    for th in (256, 512, 1024):
+        waves = th // 64
+        sec = timed(lambda s, th=th: check(lib.w8a8_peak_lds(cus, th, lds_iters, cyc.data_ptr(),
+                                                             lsink.data_ptr(), s), "peak_lds"), 5)
+        slowest = cyc.view(cus, 16)[:, :waves].max(dim=1).values.double()
+        lds[f"{waves}_waves"] = {
+            "B_per_clk_per_CU": float((waves * lds_iters * 1024 / slowest).median()),
+            "chip_TBps": cus * waves * lds_iters * 1024 / sec / 1e12}
+    out["lds_read"] = lds
+    out["lds_read_note"] = ("ds_read_b128 loop (64 lanes on 64 consecutive 16-byte chunks, no "
+                            "bank conflicts), one block of 4/8/16 waves per CU, 4096 reads per "
+                            "lane; bytes per shader clock per CU from s_memtime over each CU's "
+                            "slowest wave (median over CUs), chip rate from events")
+    del cyc, lsink
     nbytes = 1 << 30
     src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(3)
     dst = torch.empty_like(src)

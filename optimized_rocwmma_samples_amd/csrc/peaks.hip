@@ -8,6 +8,8 @@
 //     accesses in flight per lane, grid-stride or contiguous per block, plain
 //     or non-temporal loads -- the HBM rate a plain stream reaches, as the
 //     best over those forms and the launch shapes the host sweeps;
+//   * an LDS read loop: ds_read_b128 only, conflict-free, per-wave shader
+//     cycles from s_memtime -- the bytes per clock one CU's LDS returns;
 //   * an empty kernel -- the launch floor of back-to-back launches (timed by
 //     the caller in a captured graph).
 #include <hip/hip_runtime.h>
@@ -176,6 +178,48 @@ hipError_t launch_stream(const v4i* s, void* d, size_t n16, uint32_t blocks, uin
     return hipGetLastError();
 }
 
+// LDS read loop.  Every lane of the block's waves reads 16 bytes per
+// access (ds_read_b128; the 64 lanes of a wave on 64 consecutive chunks, so
+// no bank conflicts) from a kLdsPeakBytes region `iters` times, the wave
+// instructions of a block walking the region in turn, kLdsPeakBatch reads in
+// flight per wave.  The empty asm after each batch keeps the compiler from
+// merging or hoisting reads of one address across batches; the sums go to
+// `sink`.  Shader-clock cycles of each wave's
+// loop (s_memtime) go to cyc[block * 16 + wave], so bytes per clock come
+// out whatever clock the chip holds.  The host launches one block per CU
+// (kLdsPeakLaunch bytes of dynamic LDS each).
+constexpr int kLdsPeakBytes  = 64 * 1024;
+constexpr int kLdsPeakLaunch = 96 * 1024;
+constexpr int kLdsPeakBatch  = 8;
+
+__global__ void __launch_bounds__(1024) peak_lds_kernel(int iters, unsigned long long* cyc,
+                                                        int* sink)
+{
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, waves = blockDim.x >> 6;
+    for(int i = tid; i < kLdsPeakBytes / 16; i += blockDim.x)
+        reinterpret_cast<v4i*>(lds)[i] = v4i{i, i ^ 1, i ^ 2, i ^ 3};
+    __syncthreads();
+    v4i                      acc{0, 0, 0, 0};
+    const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+    for(int i = 0; i < iters; i += kLdsPeakBatch) {
+        v4i v[kLdsPeakBatch];
+#pragma unroll
+        for(int u = 0; u < kLdsPeakBatch; ++u) {
+            const int off = ((((i + u) * waves + wave) * 64 + lane) * 16) & (kLdsPeakBytes - 1);
+            v[u]          = *reinterpret_cast<const v4i*>(lds + off);
+        }
+#pragma unroll
+        for(int u = 0; u < kLdsPeakBatch; ++u) acc += v[u];
+        asm volatile("" ::: "memory");
+    }
+    __builtin_amdgcn_s_waitcnt(0); // every read has returned
+    const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+    const int                s  = acc.x + acc.y + acc.z + acc.w;
+    if(lane == 0) cyc[blockIdx.x * 16 + wave] = t1 - t0;
+    sink[blockIdx.x * blockDim.x + tid] = s;
+}
+
 __global__ void peak_empty_kernel() {}
 
 } // namespace
@@ -224,6 +268,25 @@ int w8a8_peak_stream(const void* src, void* dst, size_t bytes, uint32_t blocks, 
     if(mode == 0) return (int)launch_stream<0>(s, dst, bytes / 16, blocks, threads, variant, sink, stream);
     if(mode == 1) return (int)launch_stream<1>(s, dst, bytes / 16, blocks, threads, variant, sink, stream);
     return (int)launch_stream<2>(s, dst, bytes / 16, blocks, threads, variant, sink, stream);
+}
+
+// One LDS read launch: `blocks` blocks (one per CU: use the CU count) of
+// `threads` threads (64-1024, a multiple of 64), `iters` reads of 16 bytes
+// per lane (a multiple of 8).  cyc: blocks * 16 entries (per-wave shader cycles), sink:
+// blocks * threads ints.  Bytes read per wave: iters * 1024.
+int w8a8_peak_lds(uint32_t blocks, uint32_t threads, uint32_t iters, unsigned long long* cyc,
+                  int* sink, hipStream_t stream)
+{
+    if(blocks == 0 || iters == 0 || iters % kLdsPeakBatch || iters > (1u << 30) || threads < 64
+       || threads > 1024 || threads % 64 || cyc == nullptr || sink == nullptr)
+        return (int)hipErrorInvalidValue;
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(peak_lds_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+        kLdsPeakLaunch);
+    if(attr != hipSuccess) return (int)attr;
+    hipLaunchKernelGGL(peak_lds_kernel, dim3(blocks), dim3(threads), kLdsPeakLaunch, stream,
+                       (int)iters, cyc, sink);
+    return (int)hipGetLastError();
 }
 
 int w8a8_peak_empty(hipStream_t stream)
