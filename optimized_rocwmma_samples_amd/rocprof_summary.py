@@ -3,6 +3,13 @@
     python -m optimized_rocwmma_samples_amd.rocprof_summary trace DIR        # kernel trace
     python -m optimized_rocwmma_samples_amd.rocprof_summary pmc DIR [DIR..]  # counters
     python -m optimized_rocwmma_samples_amd.rocprof_summary traffic FETCH_DIR WRITE_DIR [CYCLE [REGEX]]
+    python -m optimized_rocwmma_samples_amd.rocprof_summary step DIR LAUNCHES  # per launch of a step
+
+`step` takes the traced W8A8 dispatches in start order as whole steps of
+LAUNCHES launches each (the last whole steps of the run) and prints one line
+per launch position of the step: kernel, grid, median and minimum duration
+over the steps, then the sum of the medians.  A position whose dispatches are
+not all one kernel prints MIXED (the trace does not hold whole steps).
 
 `traffic` turns FETCH_SIZE and WRITE_SIZE (KiB per dispatch, one run each) into
 bytes per dispatch, scaled by what the same counters read for the calibration
@@ -73,6 +80,30 @@ def trace(directory: str, match: str = "w8a8|gemm|sq_|neg") -> str:
     for (name, grid), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
         out.append(f"{name[:88]:88s} {grid:>9s} {len(d):5d} {sum(d) / len(d) / 1e3:10.2f} "
                    f"{min(d) / 1e3:10.2f}")
+    return "\n".join(out)
+
+
+def step(directory: str, launches: int, match: str = "w8a8|gemm|sq_") -> str:
+    rows = [r for r in _rows(os.path.join(directory, "**", "*kernel_trace.csv"))
+            if re.search(match, r.get("Kernel_Name", "")) and "peak" not in r.get("Kernel_Name", "")]
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    whole = len(rows) // launches * launches
+    rows = rows[len(rows) - whole:]
+    out = [f"{'pos':>3s} {'kernel':82s} {'grid':>9s} {'steps':>5s} {'median_us':>10s} "
+           f"{'min_us':>8s}"]
+    total = 0.0
+    for i in range(launches):
+        at = rows[i::launches]
+        names = {compact_name(r["Kernel_Name"]) for r in at}
+        grids = {_grid(r) for r in at}
+        d = sorted(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in at)
+        med = d[len(d) // 2] / 1e3 if d else 0.0
+        total += med
+        name = names.pop() if len(names) == 1 else "MIXED"
+        grid = grids.pop() if len(grids) == 1 else "MIXED"
+        out.append(f"{i:3d} {name[:82]:82s} {grid:>9s} {len(d):5d} {med:10.2f} "
+                   f"{(d[0] / 1e3 if d else 0.0):8.2f}")
+    out.append(f"sum of medians: {total:.1f} us per step")
     return "\n".join(out)
 
 
@@ -199,11 +230,16 @@ def traffic(fetch_dir: str, write_dir: str, match: str = "w8a8|gemm|sq_", cycle:
 
 
 def main(argv: list[str]) -> int:
-    if len(argv) < 2 or argv[0] not in ("trace", "pmc", "traffic"):
+    if len(argv) < 2 or argv[0] not in ("trace", "pmc", "traffic", "step"):
         print(__doc__)
         return 2
     if argv[0] == "trace":
         print(trace(argv[1]))
+    elif argv[0] == "step":
+        if len(argv) != 3 or int(argv[2]) < 1:
+            print(__doc__)
+            return 2
+        print(step(argv[1], int(argv[2])))
     elif argv[0] == "pmc":
         print(pmc(argv[1:]))
     else:

@@ -118,3 +118,27 @@ def test_bench_reads_per_projection_traffic_from_the_profile():
     assert by_order and len(per) == 4
     assert per[2] > per[0] > per[1] > 0  # gate_up > qkv > o_proj
     assert avg == pytest.approx(sum(per) / 4)
+
+
+def test_step_positions_take_whole_steps_from_the_end(tmp_path):
+    # a partial step first (one quantizer), then three steps of 2 launches:
+    # the quantizer (10, 12, 14 us) and the GEMM (100, 90, 95 us)
+    sq = "void w8a8::(anonymous namespace)::sq_stream_kernel<4, 2, 256, false, false>(int)"
+    fields = ["Kernel_Name", "Grid_Size_X", "Grid_Size_Y", "Grid_Size_Z", "Start_Timestamp",
+              "End_Timestamp"]
+    rows, t = [], 0
+    seq = [(sq, 99_000)] + [x for a, b in ((10_000, 100_000), (12_000, 90_000), (14_000, 95_000))
+                             for x in ((sq, a), (GEMM, b))]
+    for name, d in seq:
+        rows.append({"Kernel_Name": name, "Grid_Size_X": 512, "Grid_Size_Y": 1,
+                     "Grid_Size_Z": 1, "Start_Timestamp": t, "End_Timestamp": t + d})
+        t += d + 1000
+    _write(tmp_path / "s" / "run_kernel_trace.csv", fields, rows)
+    lines = R.step(str(tmp_path / "s"), 2).splitlines()
+    assert lines[1].split()[1].startswith("sq_stream_kernel<4,2,256,false,false>")
+    assert lines[1].split()[-3:] == ["3", "12.00", "10.00"]
+    assert lines[2].split()[1] == "gemm_i8_persist_kernel<Cfg<256,256,128,2,2,4,4,16>"
+    assert lines[2].split()[-3:] == ["3", "95.00", "90.00"]
+    assert lines[3] == "sum of medians: 107.0 us per step"
+    # a cycle length that does not match the steps shows up as MIXED
+    assert "MIXED" in R.step(str(tmp_path / "s"), 3)
