@@ -9,6 +9,9 @@ them without a graph break.
     c = torch.ops.w8a8.gemm(q, w, r, sb)
     c, q, r = torch.ops.w8a8.fused_sq_gemm(x, s, w, sb)
     x_out, q, r = torch.ops.w8a8.add_rmsnorm_smoothquant(x, residual, gamma, s, 1e-5, 127.0)
+    pw = w8a8.pack_weights(w)                        # once; the op takes pw.data and pw.n
+    c, q, r = torch.ops.w8a8.fused_sq_gemm_packed(x, s, pw.data, pw.n, sb)
+    out = torch.ops.w8a8.moe_ffn(x, logits, s, w_gu, sb_gu, w_d, sb_d, 2)
 
 The ops are functional (every output is a new tensor), as torch.library
 custom ops must be; the package functions keep the in-place and
@@ -18,8 +21,12 @@ raises, as everywhere in the package (there is no CPU path).
 Reference kernels: smoothquant <- kernel_smoothquant
 (rocwmma_smoothquant.cpp:58-122); gemm <- gemm_quant_tensor_scale
 (rocwmma_gemm_quantized.cpp:127-195) with per-token x per-channel scales;
-add_rmsnorm_smoothquant <- kernel_add_rmsnorm2d_fwd
-(rocwmma_rmsnorm2d.cpp:127-186) feeding the quantizer.
+gemm_packed / fused_sq_gemm_packed <- the pre-shuffled weight format of
+rocwmma_flatmm.cpp:12-16 and the decode role of rocwmma_gemm_splitk.cpp:
+104-201; add_rmsnorm_smoothquant <- kernel_add_rmsnorm2d_fwd
+(rocwmma_rmsnorm2d.cpp:127-186) feeding the quantizer; moe_ffn <- the
+route / sort / quantize / expert GEMM / combine chain of
+rocwmma_fused_moe.cpp:96-211.
 """
 from __future__ import annotations
 
@@ -27,9 +34,13 @@ from typing import Optional, Tuple
 
 import torch
 
+from . import PackedWeights
 from . import add_rmsnorm_smoothquant as _add_rmsnorm_smoothquant
 from . import fused_sq_gemm as _fused_sq_gemm
+from . import fused_sq_gemm_packed as _fused_sq_gemm_packed
 from . import gemm as _gemm
+from . import gemm_packed as _gemm_packed
+from . import moe_ffn as _moe_ffn
 from . import smoothquant as _smoothquant
 
 Tensor = torch.Tensor
@@ -102,3 +113,55 @@ def _(x, residual, gamma, smooth_scale, eps=1e-5, quant_max=127.0):
     m, n = x.shape
     return (torch.empty_like(x), x.new_empty((m, n), dtype=torch.int8),
             x.new_empty((m,), dtype=torch.float32))
+
+
+@torch.library.custom_op("w8a8::gemm_packed", mutates_args=())
+def gemm_packed(a: Tensor, packed: Tensor, n: int, scale_a: Optional[Tensor] = None,
+                scale_b: Optional[Tensor] = None) -> Tensor:
+    """fp16 C [M, n] = dequant(a [M, K] . W^T) with W [n, K] given packed
+    (`pack_weights(w).data`); split-K workspace allocated as the shape needs."""
+    return _gemm_packed(a, PackedWeights(packed, n, a.shape[1]), scale_a, scale_b)
+
+
+@gemm_packed.register_fake
+def _(a, packed, n, scale_a=None, scale_b=None):
+    return a.new_empty((a.shape[0], n), dtype=torch.float16)
+
+
+@torch.library.custom_op("w8a8::fused_sq_gemm_packed", mutates_args=())
+def fused_sq_gemm_packed(x: Tensor, smooth_scale: Tensor, packed: Tensor, n: int,
+                         scale_w: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
+    """SmoothQuant of x [M, K] then C = dequant(q . W^T), W [n, K] packed:
+    (c fp16 [M, n], q, row_scale)."""
+    return _fused_sq_gemm_packed(x, smooth_scale, PackedWeights(packed, n, x.shape[1]), scale_w)
+
+
+@fused_sq_gemm_packed.register_fake
+def _(x, smooth_scale, packed, n, scale_w):
+    m, k = x.shape
+    return (x.new_empty((m, n), dtype=torch.float16), x.new_empty((m, k), dtype=torch.int8),
+            x.new_empty((m,), dtype=torch.float32))
+
+
+@torch.library.custom_op("w8a8::moe_ffn", mutates_args=())
+def moe_ffn(x: Tensor, logits: Tensor, smooth_scale: Tensor, w_gate_up: Tensor,
+            sb_gate_up: Tensor, w_down: Tensor, sb_down: Tensor, topk: int,
+            smooth_scale_down: Optional[Tensor] = None, unit_size: int = 32,
+            gate_up_interleaved: bool = False) -> Tensor:
+    """The expert FFN of x [T, H] (fp16 out [T, H]): routing, sort, quantize,
+    gate_up, SiLU(gate)*up requant, down, combine.  gate_up_interleaved: the
+    gate_up weights and scales come from moe_interleave_gate_up, and the
+    gate_up GEMM runs with the SiLU epilogue."""
+    if gate_up_interleaved:
+        out, _ = _moe_ffn(x, logits, smooth_scale, None, None, w_down, sb_down, topk,
+                          smooth_scale_down, unit_size, (w_gate_up, sb_gate_up))
+    else:
+        out, _ = _moe_ffn(x, logits, smooth_scale, w_gate_up, sb_gate_up, w_down, sb_down, topk,
+                          smooth_scale_down, unit_size)
+    return out
+
+
+@moe_ffn.register_fake
+def _(x, logits, smooth_scale, w_gate_up, sb_gate_up, w_down, sb_down, topk,
+      smooth_scale_down=None, unit_size=32, gate_up_interleaved=False):
+    return torch.empty_like(x, dtype=torch.float16)

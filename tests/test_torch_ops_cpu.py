@@ -10,7 +10,8 @@ torch = pytest.importorskip("torch")
 
 import optimized_rocwmma_samples_amd.torch_ops  # noqa: F401,E402  (registers the ops)
 
-OPS = ("smoothquant", "gemm", "gemm_i32", "fused_sq_gemm", "add_rmsnorm_smoothquant")
+OPS = ("smoothquant", "gemm", "gemm_i32", "fused_sq_gemm", "add_rmsnorm_smoothquant",
+       "gemm_packed", "fused_sq_gemm_packed", "moe_ffn")
 
 
 def meta(shape, dtype=torch.float32):
@@ -43,6 +44,19 @@ def test_fake_shapes(m, n, k):
                                                       1e-5, 127.0)
     assert (xo.shape, xo.dtype, q.shape, q.dtype, r.dtype) == ((m, k), torch.float16, (m, k),
                                                                torch.int8, torch.float32)
+    packed = meta((1024,), torch.int8)
+    c, q, r = torch.ops.w8a8.fused_sq_gemm_packed(x, s, packed, n, sb)
+    assert (c.shape, c.dtype, q.shape, r.shape) == ((m, n), torch.float16, (m, k), (m,))
+    c = torch.ops.w8a8.gemm_packed(q, packed, n, r, sb)
+    assert (c.shape, c.dtype) == ((m, n), torch.float16)
+
+
+def test_moe_ffn_fake_shape():
+    t, h, inter, e = 16, 64, 32, 4
+    out = torch.ops.w8a8.moe_ffn(meta((t, h), torch.float16), meta((t, e)), meta((e, h)),
+                                 meta((e, 2 * inter, h), torch.int8), meta((e, 2 * inter)),
+                                 meta((e, h, inter), torch.int8), meta((e, h)), 2)
+    assert (out.shape, out.dtype) == ((t, h), torch.float16)
 
 
 class _Block(torch.nn.Module):
