@@ -56,10 +56,15 @@ struct DecCfg {
 // per-element operations as the quantizer kernels (rocwmma_smoothquant.cpp:
 // 58-122): p = float(x) * s; r = max|p| / qmax; inv = r > 0 ? 1 / r : 0;
 // q = int8(clamp(rint(p * inv), -qmax, qmax)); the maximum does not depend
-// on the order of the reduction, so q and r are bit-identical.
-constexpr uint32_t kFuseRows = 4;
+// on the order of the reduction, so q and r are bit-identical.  One row: the
+// prologue grows with the rows every block quantizes, and from two rows on
+// the separate quantizer launch is as fast or faster (M = 4, N = 28672,
+// K = 8192: 55.0 fused against 41.9 us; with the kernel built for up to 4
+// rows, M = 1 ran 8.1 / 5.0 us at 4096^2 / 1024^2 against 7.2 / 4.1 us
+// built for one).
+constexpr uint32_t kFuseRows = 1;
 // LDS row pitch = ka + kFusePad: the fused rows' 16-byte fragment reads at one
-// k offset (up to 4 rows x 2 lane halves) then fall on distinct bank groups.
+// k offset (up to kFuseRows rows x 2 lane halves) then fall on distinct bank groups.
 constexpr uint32_t kFusePad = 32;
 struct FuseQ {
     const uint16_t* x;    // [m, ldx] fp16 activations (16-byte aligned rows)

@@ -91,7 +91,7 @@ hipError_t noalloc_scratch(void** ptr);
 constexpr uint32_t kDecodeMaxM = 64;
 bool       gemm_decode_ok(const GemmArgs& g);
 // The decode kernel with the activation quantization folded in (packed
-// weights, fp16 output, m <= 4 when decode_fuse_ok): x fp16 [m, ldx] (16-byte
+// weights, fp16 output, m = 1 when decode_fuse_ok): x fp16 [m, ldx] (16-byte
 // aligned rows), s [k] (16-byte aligned); q [m, k] and r [m] are written as
 // by the quantizer, and g.a = q, g.scale_a = r.
 struct FuseArgs {

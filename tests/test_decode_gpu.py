@@ -169,12 +169,13 @@ def config4_weights(gpu):
     return out
 
 
-# m <= 4 and k <= 8192: the quantization runs inside the decode kernel
-# (every block quantizes the rows into LDS; block (0, 0) writes q and the row
-# scales); k = 28672 keeps the separate quantizer.  q, r and c must equal the
-# quantizer + GEMM path bit for bit.
-FUSED_SMALL = [(1, 1000, 4112, 4112), (2, 777, 2048, 2056), (3, 4096, 28672, 28672),
-               (4, 64, 16, 24), (4, 28672, 8192, 8192)]
+# m = 1 and k <= 8192: the quantization runs inside the decode kernel
+# (every block quantizes the row into LDS; block (0, 0) writes q and the row
+# scale); more rows and k = 28672 take the separate quantizer.  q, r and c
+# must equal the quantizer + GEMM path bit for bit either way.
+FUSED_SMALL = [(1, 1000, 4112, 4112), (1, 777, 2048, 2056), (1, 64, 16, 24),
+               (1, 28672, 8192, 8192), (1, 4096, 28672, 28672), (2, 777, 2048, 2056),
+               (3, 4096, 28672, 28672), (4, 64, 16, 24), (4, 28672, 8192, 8192)]
 
 
 @pytest.mark.parametrize("m,n,k,ldx", FUSED_SMALL)
